@@ -1,0 +1,353 @@
+"""Benchmark of the VecAttention prefill hot path on one MI355X.
+
+A step is one VecAttention_prefill call (pooling + TilingSelect selection +
+vector-sparse attention) on the seeded synthetic input of the workload, with
+inputs resident in HBM.  Default workload: B (Qwen2.5-VL-shaped 32K causal
+prefill, GQA 28/4, bf16, keep ~10%).
+
+Prints ONE JSON line.  `value` is the end-to-end sparse-effective throughput
+F_attn / (t_select + t_attn) in TFLOP/s, where F_attn counts the attention
+FLOPs actually executed (4*D per query row per gathered key, local diagonal
+blocks counted whole).  Extra fields: per-stage latencies, selection GB/s,
+dense bf16 SDPA latency on the same GPU and the speedup over it, the roofline
+of the dominant kernel, and the CPU oracle timed on a bounded sample.
+"""
+import argparse
+import json
+import math
+import os
+import platform
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+import torch  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+METRIC = "prefill attn latency (ms) + effective TFLOPS at 32k/128k; speedup vs dense"
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", default="B", help="workload key A..E")
+    ap.add_argument("--no-dense", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--stage-reps", type=int, default=5)
+    ap.add_argument("--extra-json", default=None, help="append the result line to this file too")
+    return ap.parse_args()
+
+
+# ------------------------------------------------------------ workload math --
+
+def local_keys(J, qps, S, causal):
+    if not causal:
+        return 0
+    if J == 0:
+        return min(qps, S)
+    return qps + min(qps, S - J * qps)
+
+
+def attn_flops(counts_per_chunk, wl, S, Sk):
+    """Executed attention FLOPs: 4*D * sum rows(J) * (count + local keys)."""
+    qps, D = wl.q_pooling_size, wl.D
+    total = 0
+    for J0, cnt in counts_per_chunk:
+        nc = cnt.shape[-1]
+        J = torch.arange(J0, J0 + nc)
+        rows = torch.clamp(S - J * qps, max=qps).double()
+        loc = torch.tensor([local_keys(int(j), qps, Sk, wl.causal) for j in J], dtype=torch.float64)
+        total += float((rows * (cnt.double() + loc)).sum())
+    return 4.0 * D * total
+
+
+def dense_flops(wl, S, Sk):
+    if wl.causal:
+        return 4.0 * wl.D * wl.B * wl.Hq * S * (S + 1) / 2
+    return 4.0 * wl.D * wl.B * wl.Hq * S * Sk
+
+
+def selection_bytes(wl, S, Sk, sum_count, nqb):
+    e = 2 if wl.dtype != torch.float32 else 4
+    return (e * wl.B * wl.Hq * S * wl.D + e * wl.B * wl.Hk * Sk * wl.D + 4 * sum_count
+            + 4 * wl.B * wl.Hq * nqb)
+
+
+def selectable(wl, S):
+    """Keys the rule can select (gap -> infinity), summed over rows."""
+    qps = wl.q_pooling_size
+    nqb = math.ceil(S / qps)
+    if not wl.causal:
+        return wl.B * wl.Hq * nqb * S
+    bsq = 64
+    tot = 0
+    for i in range(0, S, wl.chunk_size):
+        J0 = i // qps
+        for jr in range(math.ceil(min(wl.chunk_size, S - i) / qps)):
+            J = J0 + jr
+            n = max(0, (J - 1) * qps)
+            if jr % bsq == 0 and J >= 2:
+                n -= qps - wl.k_local_size
+            tot += n
+    return wl.B * wl.Hq * tot
+
+
+# ------------------------------------------------------------------- stages --
+
+def run_stages(wl, q, k, v, gap, out, events=None):
+    """Pool + per-chunk select/attention through the stage API (same kernels
+    as VecAttention_prefill).  Returns per-chunk counts; records events."""
+    from vecattention_amd import stages
+    qps, S = wl.q_pooling_size, q.shape[2]
+    ev = events
+    if ev is not None:
+        ev["p0"].record()
+    qs, _ = stages.pool_scaled(q, qps)
+    if ev is not None:
+        ev["p1"].record()
+    res = []
+    nqb = qs.shape[2]
+    for ci, i in enumerate(range(0, S, wl.chunk_size)):
+        J0 = i // qps
+        nc = math.ceil(min(wl.chunk_size, S - i) / qps)
+        if ev is not None:
+            ev[f"s0_{ci}"].record()
+        cnt, idx = stages.select_rows(qs[:, :, J0:J0 + nc], k, J0, gap, None, wl.causal, qps,
+                                      wl.k_local_size, wl.group_k_block, wl.causal)
+        if ev is not None:
+            ev[f"s1_{ci}"].record()
+        stages.sparse_attention(q, k, v, out, J0, nc, cnt, idx, wl.causal, qps)
+        if ev is not None:
+            ev[f"a1_{ci}"].record()
+        res.append((J0, cnt))
+    return res
+
+
+def calibrate_threshold(wl, q, k, v, out):
+    """Bisection on the threshold for the workload's keep ratio (GPU selection)."""
+    target = wl.keep * selectable(wl, q.shape[2])
+    lo, hi = 1e-8, 1.0
+    for _ in range(16):
+        th = math.sqrt(lo * hi)
+        gap = -math.log(th + 1e-9)
+        counts = count_only(wl, q, k, gap)
+        if counts > target:
+            lo = th
+        else:
+            hi = th
+    return math.sqrt(lo * hi)
+
+
+def count_only(wl, q, k, gap):
+    from vecattention_amd import stages
+    qps, S = wl.q_pooling_size, q.shape[2]
+    qs, _ = stages.pool_scaled(q, qps)
+    tot = 0
+    for i in range(0, S, wl.chunk_size):
+        J0 = i // qps
+        nc = math.ceil(min(wl.chunk_size, S - i) / qps)
+        cnt, _ = stages.select_rows(qs[:, :, J0:J0 + nc], k, J0, gap, None, wl.causal, qps,
+                                    wl.k_local_size, wl.group_k_block, wl.causal)
+        tot += int(cnt.sum().item())
+    return tot
+
+
+def time_dense(wl, q, k, v, reps=10, warmup=3):
+    """PyTorch SDPA (flash backend only; never the bf16 math path) on the same GPU."""
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+    for backend in (SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION):
+        try:
+            with sdpa_kernel([backend]):
+                kk, vv = k, v
+                if wl.Hq != wl.Hk:
+                    kk = k.repeat_interleave(wl.Hq // wl.Hk, dim=1).contiguous()
+                    vv = v.repeat_interleave(wl.Hq // wl.Hk, dim=1).contiguous()
+                f = lambda: torch.nn.functional.scaled_dot_product_attention(  # noqa: E731
+                    q, kk, vv, is_causal=wl.causal)
+                for _ in range(warmup):
+                    f()
+                torch.cuda.synchronize()
+                ts = []
+                for _ in range(reps):
+                    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                    a.record()
+                    f()
+                    b.record()
+                    torch.cuda.synchronize()
+                    ts.append(a.elapsed_time(b))
+                del kk, vv
+                return statistics.median(ts), str(backend).split(".")[-1]
+        except RuntimeError as e:  # backend unavailable for this shape
+            last = str(e)
+            continue
+    return None, f"unavailable: {last[:80]}"
+
+
+# --------------------------------------------------------------- CPU oracle --
+
+def cpu_baseline(wl, q_cpu, k_cpu, v_cpu, threshold, seconds):
+    """The oracle (C selection + numpy attention, 1 thread) on sampled q-blocks
+    of head 0; TFLOP/s on the executed attention FLOPs of the sample."""
+    import numpy as np
+    from threadpoolctl import threadpool_limits
+
+    from oracle import oracle as orc
+    qps, S, D = wl.q_pooling_size, q_cpu.shape[2], wl.D
+    Sk = k_cpu.shape[2]
+    dt = {torch.bfloat16: "bfloat16", torch.float16: "float16", torch.float32: "float32"}[wl.dtype]
+    qh = q_cpu[:, :1].float().numpy()
+    kh = k_cpu[:, :1].float().numpy()
+    vh = v_cpu[:, :1].float().numpy()
+    nqb = math.ceil(S / qps)
+    gaps = orc.gap_from_threshold(threshold, 1, 1)
+    bc, bi = orc.local_blocks(1, 1, S, qps, wl.causal)
+    order = np.random.default_rng(0).permutation(nqb)
+    flops, done, t0 = 0.0, 0, time.perf_counter()
+    with threadpool_limits(1):
+        _, qs = orc.pool(qh, qps, dt)
+        for J in order:
+            J = int(J)
+            c0 = (J * qps) // wl.chunk_size * (wl.chunk_size // qps)
+            ncc = min(wl.chunk_size // qps, nqb - c0)
+            cnt, lists = orc.select(qs, kh, c0, ncc, gaps, qps, wl.k_local_size, wl.group_k_block,
+                                    wl.causal, wl.causal, 64, rows=(J - c0, J - c0 + 1))
+            orc.attention(qh, kh, vh, qps, wl.causal, bc, bi, [[lists[0][0][J - c0:J - c0 + 1]]],
+                          J0=J, nc=1, acc=np.float32)
+            rows = min(qps, S - J * qps)
+            flops += 4.0 * D * rows * (int(cnt[0, 0, J - c0]) + local_keys(J, qps, Sk, wl.causal))
+            done += 1
+            if time.perf_counter() - t0 > seconds and done >= 4:
+                break
+    el = time.perf_counter() - t0
+    return {"value": flops / el / 1e12, "unit": "TFLOP/s", "cores": 1, "kind": "port",
+            "sample": f"oracle (C selection, numpy fp32 attention) on {done} random q-blocks of "
+                      f"head 0 of workload {wl.name}, {el:.1f} s",
+            "host_cpu": platform.processor() or platform.machine(),
+            "host_threads_available": len(os.sched_getaffinity(0))}
+
+
+# --------------------------------------------------------------------- main --
+
+def main():
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for "
+              f"--gpus {args.gpus}); per-GPU sharding is by (batch, kv head) and needs no "
+              f"collective (see DESIGN.md).", file=sys.stderr)
+        sys.exit(2)
+    from vecattention_amd import VecAttention_prefill
+    from vecattention_amd.synth import WORKLOADS, workload_inputs
+
+    wl = WORKLOADS[args.config]
+    dev = torch.device("cuda:0")
+    t_gen = time.perf_counter()
+    q_cpu, k_cpu, v_cpu = workload_inputs(wl, seed=0)
+    q, k, v = q_cpu.to(dev), k_cpu.to(dev), v_cpu.to(dev)
+    print(f"[bench] {wl.name}: inputs ready in {time.perf_counter() - t_gen:.1f}s", file=sys.stderr,
+          flush=True)
+    S, Sk = q.shape[2], k.shape[2]
+    out = torch.empty_like(q)
+
+    th = calibrate_threshold(wl, q, k, v, out)
+    gap = -math.log(th + 1e-9)
+    print(f"[bench] threshold {th:.6g} (gap {gap:.6g})", file=sys.stderr, flush=True)
+
+    # ---- per-stage timing through the stage API ----
+    nch = math.ceil(S / wl.chunk_size)
+    names = ["p0", "p1"] + [f"{p}_{c}" for c in range(nch) for p in ("s0", "s1", "a1")]
+    t_pool, t_sel, t_attn = [], [], []
+    counts = None
+    for r in range(args.stage_reps + 1):
+        ev = {n: torch.cuda.Event(enable_timing=True) for n in names}
+        counts = run_stages(wl, q, k, v, gap, out, ev)
+        torch.cuda.synchronize()
+        if r == 0:
+            continue
+        t_pool.append(ev["p0"].elapsed_time(ev["p1"]))
+        t_sel.append(sum(ev[f"s0_{c}"].elapsed_time(ev[f"s1_{c}"]) for c in range(nch)))
+        t_attn.append(sum(ev[f"s1_{c}"].elapsed_time(ev[f"a1_{c}"]) for c in range(nch)))
+    t_pool, t_sel, t_attn = (statistics.median(x) for x in (t_pool, t_sel, t_attn))
+    F_attn = attn_flops(counts, wl, S, Sk)
+    F_dense = dense_flops(wl, S, Sk)
+    sum_count = sum(int(c.sum().item()) for _, c in counts)
+    nqb = math.ceil(S / wl.q_pooling_size)
+    sel_bytes = selection_bytes(wl, S, Sk, sum_count, nqb)
+    keep = sum_count / selectable(wl, S)
+    print(f"[bench] stages: pool {t_pool:.3f} ms, select {t_sel:.3f} ms, attn {t_attn:.3f} ms; "
+          f"keep {keep:.4f}", file=sys.stderr, flush=True)
+
+    # ---- the timed steps: whole VecAttention_prefill calls ----
+    def step():
+        return VecAttention_prefill(q, k, v, threshold=th, q_pooling_size=wl.q_pooling_size,
+                                    k_local_size=wl.k_local_size, group_k_block=wl.group_k_block,
+                                    causal=wl.causal, chunk_size=wl.chunk_size)
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    ms_per_step = (time.perf_counter() - t0) * 1e3 / max(args.steps, 1)
+    print(f"[bench] {args.steps} steps: {ms_per_step:.3f} ms/step", file=sys.stderr, flush=True)
+
+    dense_ms, dense_backend = (None, "skipped")
+    if not args.no_dense:
+        dense_ms, dense_backend = time_dense(wl, q, k, v)
+        print(f"[bench] dense SDPA ({dense_backend}): {dense_ms} ms", file=sys.stderr, flush=True)
+
+    t_sel_total = t_pool + t_sel
+    e2e_tflops = F_attn / ((t_sel_total + t_attn) * 1e-3) / 1e12
+    attn_tflops = F_attn / (t_attn * 1e-3) / 1e12
+    result = {
+        "metric": METRIC,
+        "value": round(e2e_tflops, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": {torch.bfloat16: "bf16", torch.float16: "fp16", torch.float32: "fp32"}[wl.dtype],
+        "data": "synthetic (seeded N(0,1) + vertical-column and frame structure; threshold "
+                "calibrated to the keep ratio)",
+        "config": {"workload": wl.name, "B": wl.B, "Hq": wl.Hq, "Hk": wl.Hk, "S": S, "D": wl.D,
+                   "causal": wl.causal, "q_pooling_size": wl.q_pooling_size,
+                   "k_local_size": wl.k_local_size, "group_k_block": wl.group_k_block,
+                   "chunk_size": wl.chunk_size, "threshold": th, "keep": round(keep, 5),
+                   "parallelism": "single GPU"},
+        "latency_ms": {"pool": round(t_pool, 4), "select": round(t_sel, 4),
+                       "attn": round(t_attn, 4), "total": round(t_sel_total + t_attn, 4)},
+        "sparse_attn_tflops": round(attn_tflops, 3),
+        "selection_gbs": round(sel_bytes / (t_sel_total * 1e-3) / 1e9, 1),
+        "selection_hbm_frac": round(sel_bytes / (t_sel_total * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "dense_ms": None if dense_ms is None else round(dense_ms, 4),
+        "dense_backend": dense_backend,
+        "speedup_vs_dense": None if dense_ms is None else round(dense_ms / (t_sel_total + t_attn), 3),
+        "dense_equiv_tflops": round(F_dense / ((t_sel_total + t_attn) * 1e-3) / 1e12, 3),
+        "roofline": {"bound": "mfma", "kernel": "attn_mfma_kernel",
+                     "achieved": round(attn_tflops, 3), "peak": BF16_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(attn_tflops / BF16_PEAK_TFLOPS, 4),
+                     "traffic": None},
+        "flops": {"attn_executed": F_attn, "dense": F_dense},
+    }
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline(wl, q_cpu, k_cpu, v_cpu, th, args.cpu_seconds)
+    line = json.dumps(result)
+    print(line, flush=True)
+    if args.extra_json:
+        with open(args.extra_json, "a") as f:
+            f.write(line + "\n")
+
+
+if __name__ == "__main__":
+    main()

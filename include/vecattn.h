@@ -1,0 +1,144 @@
+/*
+ * C ABI of the MI355X-native VecAttention prefill hot path (libvecattn.so).
+ *
+ * Plain pointers and sizes only.  All device pointers are HIP device memory on
+ * the current device; `stream` is a hipStream_t (NULL = default stream).
+ * Every entry point is stream-ordered, allocates nothing, and returns VA_OK or
+ * a negative error code; va_last_error() returns the message of the last
+ * failure on the calling thread.  Strides are in elements; the feature
+ * dimension D must be contiguous (stride 1).
+ *
+ * Element types: VA_F32 (float), VA_BF16 (bfloat16), VA_F16 (IEEE half).
+ * Tensor shapes use the reference's BHSD convention:
+ *   q (B, Hq, Sq, D), k and v (B, Hk, Sk, D), out (B, Hq, Sq, D).
+ *
+ * Selected key lists ("index layout"): row J of a chunk [J0, J0+nc) of q-block
+ * rows owns capacity(J) int32 slots, written in ascending key order from its
+ * row offset; counts[(b*Hq + h)*nc + (J - J0)] holds the number written.
+ *   dense_stride > 0 : every row has `dense_stride` slots (the reference's
+ *                      dense (B, H, nqb, padded_k) column_index layout);
+ *   dense_stride == 0: packed capacities; a causal row holds max(0, J*qps - smin)
+ *                      slots (keys [smin, J*qps), smin = wo_init ? qps : 0), a
+ *                      non-causal row Sk - smin slots (smin = wo_init ?
+ *                      min(qps, Sk) : 0).  va_select_index_capacity() gives
+ *                      the total, va_select_row_offset() the offset of a row.
+ */
+#ifndef VECATTN_H_
+#define VECATTN_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { VA_F32 = 0, VA_BF16 = 1, VA_F16 = 2 };
+
+enum {
+  VA_OK = 0,
+  VA_ERR_ARG = -1,          /* invalid argument (mirrors the reference's asserts) */
+  VA_ERR_UNSUPPORTED = -2,  /* valid for the reference, not handled by this build */
+  VA_ERR_HIP = -3,          /* a HIP runtime call failed (no device, launch error) */
+  VA_ERR_WORKSPACE = -4     /* workspace smaller than va_prefill_workspace_size() */
+};
+
+enum { VA_ATTN_AUTO = 0, VA_ATTN_MFMA = 1, VA_ATTN_SIMPLE = 2 };
+
+/* Library version (major*10000 + minor*100 + patch). */
+int va_version(void);
+
+/* Message of the last failing call on this thread ("" if none). */
+const char* va_last_error(void);
+
+/* Number of HIP devices visible, or a negative code (no GPU is an error). */
+int va_device_count(void);
+
+/*
+ * Query pooling: block means over q_pooling_size rows, fused with the
+ * selection's query scaling.
+ * Replaces spattn/src/utils.py:340-360 (average_vector -> triton_bnhd_pool
+ * :86-137 -> bnhd_pool_kernel :8-83) and the pooled-query scaling of
+ * spattn/src/kernels/vecattention_kernels.py:94,244-245.
+ *   pooled[b,h,J,:] = T(fp32 mean of rows J*qps .. min(S,(J+1)*qps)-1)
+ *   scaled[b,h,J,:] = T(fp32(pooled * fp32(1/sqrt(D))))
+ * pooled / scaled: contiguous (B, H, ceil(S/qps), D); either may be NULL.
+ */
+int va_pool(int dtype, const void* q, int64_t B, int64_t H, int64_t S, int64_t D,
+            int64_t sqb, int64_t sqh, int64_t sqs, int64_t q_pooling_size,
+            void* pooled, void* scaled, void* stream);
+
+/*
+ * TilingSelect: important-vertical-vector selection for q-block rows
+ * [J0, J0+nc) of every (b, h).
+ * Replaces spattn/src/kernels/vecattention_kernels.py:59-181
+ * (fuse_qk_softmax_minp_wo_causal) and its kernels :206-272 / :275-345.
+ *   qs     : scaled pooled queries of the chunk: row jr of (b, h) at
+ *            qs + b*sqb + h*sqh + jr*sqn (element strides, features contiguous)
+ *   k      : keys (B, Hk, Sk, D) with strides; q head h reads kv head h/(Hq/Hk)
+ *   gap    : fp32 gap (= -ln(threshold + 1e-9)) used when gaps == NULL
+ *   gaps   : device fp32 array of B*Hq gaps (per-head thresholds), or NULL
+ *   bsq    : BLOCK_SIZE_Q of the reference launch (64 for the shipped VLM
+ *            configs); it places the reference's causal first-row tile quirk
+ * Output: see "index layout" above.  Scores use canonical arithmetic (a
+ * sequential fp64 dot product rounded once to fp32), so the selected sets
+ * match the CPU restatement of the rule bit for bit.
+ */
+int va_select(int dtype, const void* qs, int64_t sqb, int64_t sqh, int64_t sqn,
+              const void* k, int64_t skb, int64_t skh, int64_t sks, int64_t B, int64_t Hq, int64_t Hk, int64_t Sk,
+              int64_t D, int64_t q_pooling_size, int64_t k_local_size,
+              int64_t group_k_block, int causal, int wo_init, int64_t J0, int64_t nc,
+              int64_t bsq, float gap, const float* gaps, int64_t dense_stride,
+              int32_t* counts, int32_t* indices, void* stream);
+
+/* Total int32 slots of the index layout for B*Hq rows sets [J0, J0+nc). */
+int64_t va_select_index_capacity(int64_t B, int64_t Hq, int64_t Sk, int64_t q_pooling_size,
+                                 int causal, int wo_init, int64_t J0, int64_t nc,
+                                 int64_t dense_stride);
+
+/* Offset of row (bh = b*Hq + h, jr = J - J0) in the index layout. */
+int64_t va_select_row_offset(int64_t Sk, int64_t q_pooling_size, int causal, int wo_init,
+                             int64_t J0, int64_t nc, int64_t dense_stride, int64_t bh,
+                             int64_t jr);
+
+/*
+ * Vector-sparse attention for q-block rows [J0, J0+nc): query row i of block J
+ * attends to the local blocks of J (causal: [0,qps) and the diagonal block) and
+ * the selected columns of J, with softmax scale `softmax_scale`.
+ * Replaces vllm_flash_attn.sparse_attn_func as called at
+ * spattn/src/VecAttention.py:104-121 (vertical + local-block semantics of
+ * spattn/threshold/model_tuner.py:193-216).  Rows with no key are 0.
+ * `kernel`: VA_ATTN_AUTO (MFMA for bf16/fp16, D in {64,128}, qps in {64,128};
+ * otherwise the per-row kernel), VA_ATTN_MFMA or VA_ATTN_SIMPLE.
+ */
+int va_sparse_attn(int dtype, const void* q, int64_t sqb, int64_t sqh, int64_t sqs,
+                   const void* k, int64_t skb, int64_t skh, int64_t sks, const void* v,
+                   int64_t svb, int64_t svh, int64_t svs, void* out, int64_t sob,
+                   int64_t soh, int64_t sos, int64_t B, int64_t Hq, int64_t Hk, int64_t Sq,
+                   int64_t Sk, int64_t D, int64_t q_pooling_size, int causal, int wo_init,
+                   int64_t J0, int64_t nc, int64_t dense_stride, const int32_t* counts,
+                   const int32_t* indices, float softmax_scale, int kernel, void* stream);
+
+/* Bytes of device workspace va_prefill needs (256-byte aligned segments). */
+int64_t va_prefill_workspace_size(int dtype, int64_t B, int64_t Hq, int64_t Sq, int64_t Sk,
+                                  int64_t D, int64_t q_pooling_size, int causal,
+                                  int64_t chunk_size);
+
+/*
+ * The whole VecAttention prefill: pooling, then per query chunk selection and
+ * vector-sparse attention, all on `stream` with no host synchronisation.
+ * Replaces spattn/src/VecAttention.py:10-123 (VecAttention_prefill).
+ * `gap`/`gaps` as in va_select.  out: (B, Hq, Sq, D) with strides.
+ */
+int va_prefill(int dtype, const void* q, int64_t sqb, int64_t sqh, int64_t sqs,
+               const void* k, int64_t skb, int64_t skh, int64_t sks, const void* v,
+               int64_t svb, int64_t svh, int64_t svs, void* out, int64_t sob, int64_t soh,
+               int64_t sos, int64_t B, int64_t Hq, int64_t Hk, int64_t Sq, int64_t Sk,
+               int64_t D, float gap, const float* gaps, int64_t q_pooling_size,
+               int64_t k_local_size, int64_t group_k_block, int causal, int64_t chunk_size,
+               int64_t bsq, void* workspace, int64_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* VECATTN_H_ */

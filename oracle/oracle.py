@@ -1,0 +1,236 @@
+"""CPU oracle of the VecAttention prefill path — TEST INFRASTRUCTURE ONLY.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import
+this module, and only as the checker (or, for the baseline, the thing timed on
+the host).  The product path (vecattention_amd/) never imports it.
+
+Pieces and the reference lines they restate:
+  pool / select       oracle/vecattn_oracle.c (pooling: spattn/src/utils.py:
+                      8-83,340-360; selection: spattn/src/kernels/
+                      vecattention_kernels.py:59-181,206-345)
+  local_blocks        spattn/src/VecAttention.py:63-92 (also
+                      spattn/threshold/model_tuner.py:144-176)
+  attention           spattn/threshold/model_tuner.py:193-216 (the dense-mask
+                      statement of sparse_attn_func: local blocks of 64 keys
+                      clipped to S_k, union selected columns, causal mask,
+                      softmax scale 1/sqrt(D)); an empty key set gives 0
+  prefill             spattn/src/VecAttention.py:43-123 (gap, chunk loop)
+
+Pinning (tests/test_oracle.py): closed forms for pooling and gap; hand-derived
+known answers for the selection rule (prefix maximum updated before the
+compare, group restarts, causal first-row tile rule, key tail); an
+independent brute force on exactly representable inputs; invariants (large
+gap selects every selectable key; larger gap selects a superset; chunk-size
+invariance; single-group equivalence); attention against torch's dense SDPA
+in float64 where the sparse set is all keys.
+"""
+import ctypes
+import math
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+SPATTN_BLOCK_SIZE_K = 64  # spattn/src/VecAttention.py:45-46
+
+ORC_F32, ORC_BF16, ORC_F16 = 0, 1, 2
+_lib = None
+
+
+def build():
+    """Compile the C restatement (oracle/Makefile)."""
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+    return LIB_PATH
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        h = ctypes.CDLL(LIB_PATH)
+        P = ctypes.c_void_p
+        I = ctypes.c_int64
+        h.orc_pool.restype = ctypes.c_int
+        h.orc_pool.argtypes = [P, I, I, I, I, I, ctypes.c_int, P, P]
+        h.orc_select.restype = ctypes.c_int
+        h.orc_select.argtypes = [P, I, P, I, I, I, I, I, I, I, I, ctypes.c_int, ctypes.c_int, I, I,
+                                 I, I, I, P, P, P, P, P]
+        h.orc_dot.restype = ctypes.c_float
+        h.orc_dot.argtypes = [P, P, I]
+        h.orc_round.restype = ctypes.c_float
+        h.orc_round.argtypes = [ctypes.c_float, ctypes.c_int]
+        _lib = h
+    return _lib
+
+
+def _p(a):
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+def dtype_code(name):
+    return {"float32": ORC_F32, "bfloat16": ORC_BF16, "float16": ORC_F16}[name]
+
+
+def as_f32(x):
+    """torch tensor or array -> contiguous float32 numpy array (exact for bf16/fp16)."""
+    try:
+        import torch
+        if isinstance(x, torch.Tensor):
+            return np.ascontiguousarray(x.detach().float().cpu().numpy())
+    except ImportError:
+        pass
+    return np.ascontiguousarray(np.asarray(x, dtype=np.float32))
+
+
+def pool(q, qps, dtype):
+    """(pooled, scaled) for q (B,H,S,D) float32 values of element type `dtype`."""
+    q = as_f32(q)
+    B, H, S, D = q.shape
+    nqb = math.ceil(S / qps)
+    pooled = np.empty((B, H, nqb, D), np.float32)
+    scaled = np.empty((B, H, nqb, D), np.float32)
+    rc = lib().orc_pool(_p(q), B, H, S, D, qps, dtype_code(dtype), _p(pooled), _p(scaled))
+    assert rc == 0, rc
+    return pooled, scaled
+
+
+def gap_from_threshold(threshold, B, H):
+    """fp32 gap per (b, h) as spattn/src/VecAttention.py:48-52 (float branch:
+    -ln(th + 1e-9) in double, then fp32)."""
+    if np.ndim(threshold) == 0:
+        return np.full(B * H, np.float32(-math.log(float(threshold) + 1e-9)), np.float32)
+    t = np.asarray(threshold, np.float32)
+    g = (-np.log(t + np.float32(1e-9))).astype(np.float32)
+    return np.ascontiguousarray(np.broadcast_to(g, (B, H)).reshape(-1))
+
+
+def row_capacity(J, qps, Sk, causal, wo_init):
+    smin = (qps if causal else min(qps, Sk)) if wo_init else 0
+    if causal:
+        return max(0, min(Sk, J * qps) - smin)
+    return Sk - smin
+
+
+def select(qs, k, J0, nc, gaps, qps, bk, group, causal, wo_init, bsq, rows=None):
+    """Selected key lists for rows [J0, J0+nc) of every (b, h).
+
+    qs: scaled pooled queries (B,Hq,nqb_total,D); k: (B,Hk,Sk,D); gaps: fp32 B*Hq.
+    rows: optional (jr_begin, jr_end) subset of the chunk [J0, J0+nc) to compute
+    (the chunk start still fixes the causal program tiling); others count 0.
+    Returns (counts (B,Hq,nc) int32, lists: nested list [b][h][jr] of int32 arrays).
+    """
+    qs = as_f32(qs)
+    k = as_f32(k)
+    B, Hq, nqb_total, D = qs.shape
+    Hk, Sk = k.shape[1], k.shape[2]
+    caps = np.array([[row_capacity(J0 + jr, qps, Sk, causal, wo_init) for jr in range(nc)]] * (B * Hq),
+                    np.int64).reshape(-1)
+    base = np.zeros_like(caps)
+    base[1:] = np.cumsum(caps)[:-1]
+    idx = np.zeros(max(int(caps.sum()), 1), np.int32)
+    counts = np.zeros(B * Hq * nc, np.int32)
+    gaps = np.ascontiguousarray(gaps, np.float32)
+    jb, je = rows if rows is not None else (0, nc)
+    rc = lib().orc_select(_p(qs), nqb_total, _p(k), B, Hq, Hk, Sk, D, qps, bk, group, int(causal),
+                          int(wo_init), J0, nc, jb, je, bsq, _p(gaps), _p(counts), _p(idx), _p(base),
+                          _p(caps))
+    assert rc == 0, rc
+    lists = [[[idx[base[(b * Hq + h) * nc + jr]: base[(b * Hq + h) * nc + jr] + counts[(b * Hq + h) * nc + jr]].copy()
+               for jr in range(nc)] for h in range(Hq)] for b in range(B)]
+    return counts.reshape(B, Hq, nc), lists
+
+
+def local_blocks(B, H, S, qps, causal):
+    """(blk_count (B,H,nqb) int32, blk_idx (B,H,nqb,2n|1) int32), as
+    spattn/src/VecAttention.py:63-92."""
+    nqb = math.ceil(S / qps)
+    if causal:
+        n = qps // SPATTN_BLOCK_SIZE_K
+        cnt = np.full((B, H, nqb), 2 * n, np.int32)
+        cnt[..., 0] = math.ceil(min(S, qps) / SPATTN_BLOCK_SIZE_K)
+        if S > qps and S % qps != 0:
+            cnt[..., -1] = n + math.ceil((S - (S // qps) * qps) / SPATTN_BLOCK_SIZE_K)
+        idx = np.zeros((B, H, nqb, 2 * n), np.int32)
+        offs = np.arange(n, dtype=np.int32) * SPATTN_BLOCK_SIZE_K
+        idx[..., :n] = offs
+        idx[..., n:] = (np.arange(nqb, dtype=np.int32) * qps)[:, None] + offs
+    else:
+        cnt = np.zeros((B, H, nqb), np.int32)
+        idx = np.zeros((B, H, nqb, 1), np.int32)
+    return cnt, idx
+
+
+def key_set(J, blk_count, blk_idx, cols, Sk):
+    """Sorted key positions of q-block J: blocks of 64 clipped to [0, Sk) ∪ columns."""
+    parts = [np.arange(int(o), min(int(o) + SPATTN_BLOCK_SIZE_K, Sk)) for o in blk_idx[:blk_count]]
+    parts.append(np.asarray(cols, np.int64))
+    return np.unique(np.concatenate(parts).astype(np.int64)) if parts else np.zeros(0, np.int64)
+
+
+def attention(q, k, v, qps, causal, blk_count, blk_idx, lists, J0=0, nc=None, acc=np.float64):
+    """Masked softmax attention for q-blocks [J0, J0+nc): out rows (B,Hq,rows,D) in `acc`.
+
+    q (B,Hq,Sq,D), k/v (B,Hk,Sk,D) as float arrays; lists[b][h][jr] selected columns.
+    Causal alignment is bottom-right (row i of the query sequence sees keys
+    <= i + Sk - Sq), as for each chunk of the reference.
+    """
+    q = as_f32(q).astype(acc)
+    k = as_f32(k).astype(acc)
+    v = as_f32(v).astype(acc)
+    B, Hq, Sq, D = q.shape
+    Hk, Sk = k.shape[1], k.shape[2]
+    rep = Hq // Hk
+    nqb = math.ceil(Sq / qps)
+    nc = nqb - J0 if nc is None else nc
+    r0, r1 = J0 * qps, min(Sq, (J0 + nc) * qps)
+    out = np.zeros((B, Hq, r1 - r0, D), acc)
+    scale = 1.0 / math.sqrt(D)
+    for b in range(B):
+        for h in range(Hq):
+            kh, vh = k[b, h // rep], v[b, h // rep]
+            for jr in range(nc):
+                J = J0 + jr
+                keys = key_set(J, blk_count[b, h, J], blk_idx[b, h, J], lists[b][h][jr], Sk)
+                a, e = J * qps, min(Sq, (J + 1) * qps)
+                if keys.size == 0:
+                    continue
+                s = (q[b, h, a:e] @ kh[keys].T) * scale
+                if causal:
+                    pos = np.arange(a, e)[:, None] + (Sk - Sq)
+                    s = np.where(keys[None, :] <= pos, s, -np.inf)
+                m = s.max(axis=1, keepdims=True)
+                m = np.where(np.isfinite(m), m, 0.0)
+                p = np.exp(s - m)
+                l = p.sum(axis=1, keepdims=True)
+                o = (p @ vh[keys]) / np.where(l > 0, l, 1.0)
+                out[b, h, a - r0:e - r0] = np.where(l > 0, o, 0.0)
+    return out
+
+
+def prefill(q, k, v, threshold, q_pooling_size=128, k_local_size=128, group_k_block=1,
+            causal=True, chunk_size=16 * 1024, bsq=64, dtype="bfloat16", acc=np.float64):
+    """Whole-path oracle: returns (out (B,Hq,S,D) in `acc`, per-chunk (counts, lists))."""
+    q, k, v = as_f32(q), as_f32(k), as_f32(v)
+    B, Hq, S, D = q.shape
+    Sk = k.shape[2]
+    gaps = gap_from_threshold(threshold, B, Hq)
+    _, qs = pool(q, q_pooling_size, dtype)
+    blk_count, blk_idx = local_blocks(B, Hq, S, q_pooling_size, causal)
+    out = np.zeros((B, Hq, S, D), acc)
+    chunks = []
+    for i in range(0, S, chunk_size):
+        J0 = i // q_pooling_size
+        nc = math.ceil(min(chunk_size, S - i) / q_pooling_size)
+        counts, lists = select(qs, k, J0, nc, gaps, q_pooling_size, k_local_size, group_k_block,
+                               causal, causal, bsq)
+        chunks.append((counts, lists))
+        kc = k[:, :, :i + chunk_size] if causal else k
+        vc = v[:, :, :i + chunk_size] if causal else v
+        qc = q[:, :, :min(S, i + chunk_size)]
+        o = attention(qc, kc, vc, q_pooling_size, causal, blk_count, blk_idx, lists, J0=J0, nc=nc,
+                      acc=acc)
+        out[:, :, i:i + o.shape[2]] = o
+    return out, chunks

@@ -1,0 +1,352 @@
+"""GPU parity of the HIP path against the CPU oracle (run on an MI355X).
+
+Bar: pooling and selected index sets bit-exact; attention outputs within
+max-abs 2e-2 and mean-abs 2e-3 of the oracle's float64 result (bf16/fp16
+inputs), 1e-4 / 1e-5 for fp32 inputs.  Every call goes through the C ABI of
+libvecattn.so.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as orc
+from vecattention_amd import VecAttention_prefill
+from vecattention_amd import _native as nat
+from vecattention_amd import stages
+from vecattention_amd.synth import make_inputs
+
+pytestmark = pytest.mark.gpu
+
+ATOL_MAX, ATOL_MEAN = 2e-2, 2e-3          # north-star tolerance, bf16/fp16
+ATOL_MAX_F32, ATOL_MEAN_F32 = 1e-4, 1e-5
+DTN = {torch.bfloat16: "bfloat16", torch.float16: "float16", torch.float32: "float32"}
+
+
+def note(*a):
+    print("[case]", *a, flush=True)
+
+
+def gpu_lists(counts, indices, B, Hq, J0, nc, qps, Sk, causal, wo_init, dense_stride=0):
+    """Per-row index lists from the GPU output, cut with the oracle's own
+    capacity arithmetic (independent of the library's layout code)."""
+    counts = counts.cpu().numpy().reshape(B, Hq, nc)
+    idx = indices.cpu().numpy().reshape(-1)
+    if dense_stride:
+        caps = [dense_stride] * nc
+    else:
+        caps = [orc.row_capacity(J0 + jr, qps, Sk, causal, wo_init) for jr in range(nc)]
+    out, base = [], 0
+    for b in range(B):
+        out.append([])
+        for h in range(Hq):
+            rows = []
+            for jr in range(nc):
+                c = int(counts[b, h, jr])
+                assert 0 <= c <= caps[jr]
+                rows.append(idx[base:base + c].copy())
+                base += caps[jr]
+            out[-1].append(rows)
+    return counts, out
+
+
+def assert_lists_equal(got, want, ctx=""):
+    for b in range(len(want)):
+        for h in range(len(want[b])):
+            for jr in range(len(want[b][h])):
+                g, w = got[b][h][jr], want[b][h][jr]
+                if not np.array_equal(g, w):
+                    extra = sorted(set(g.tolist()) ^ set(w.tolist()))[:10]
+                    raise AssertionError(f"{ctx} b={b} h={h} jr={jr}: {len(g)} vs {len(w)} keys, "
+                                         f"differ at {extra}")
+
+
+def calibrated_threshold(keep, q, k, qps, bk, G, causal):
+    """A threshold giving roughly `keep` of the selectable keys on these inputs (oracle)."""
+    _, qs = orc.pool(q, qps, DTN[q.dtype])
+    B, Hq = q.shape[:2]
+    nqb = qs.shape[2]
+    all_cnt, _ = orc.select(qs, k, 0, nqb, np.full(B * Hq, 1e6, np.float32), qps, bk, G, causal,
+                            causal, 64)
+    lo, hi = 1e-6, 1.0
+    for _ in range(18):
+        th = math.sqrt(lo * hi)
+        c, _ = orc.select(qs, k, 0, nqb, orc.gap_from_threshold(th, B, Hq), qps, bk, G, causal,
+                          causal, 64)
+        if c.sum() > keep * all_cnt.sum():
+            lo = th
+        else:
+            hi = th
+    return math.sqrt(lo * hi)
+
+
+# ------------------------------------------------------------------ pooling --
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("S,qps", [(1000, 64), (4096, 128), (77, 64)])
+def test_pool_bit_exact(device, dtype, S, qps):
+    note("pool", dtype, S, qps)
+    q, _, _ = make_inputs(2, 3, 3, S, 128 if dtype != torch.float32 else 64, dtype, seed=S)
+    scaled, pooled = stages.pool_scaled(q.to(device), qps, want_pooled=True)
+    want_p, want_s = orc.pool(q, qps, DTN[dtype])
+    assert np.array_equal(pooled.float().cpu().numpy(), want_p)
+    assert np.array_equal(scaled.float().cpu().numpy(), want_s)
+
+
+def test_pool_strided_bshd_view(device):
+    note("pool strided")
+    q, _, _ = make_inputs(1, 4, 4, 640, 128, torch.bfloat16, seed=11)
+    bshd = q.transpose(1, 2).contiguous().to(device)        # memory (B, S, H, D)
+    view = bshd.transpose(1, 2)                              # shape (B, H, S, D)
+    scaled, pooled = stages.pool_scaled(view, 64, want_pooled=True)
+    want_p, want_s = orc.pool(q, 64, "bfloat16")
+    assert np.array_equal(pooled.float().cpu().numpy(), want_p)
+    assert np.array_equal(scaled.float().cpu().numpy(), want_s)
+    avg = stages.average_vector(view, 64)
+    assert np.array_equal(avg.float().cpu().numpy(), want_p)
+
+
+# ---------------------------------------------------------------- selection --
+
+SELECT_CASES = [
+    # name, B, Hq, Hk, S, D, dtype, causal, qps, bk, G, keep, chunk_rows
+    ("A-fp32-noncausal", 1, 4, 4, 4096, 64, torch.float32, False, 64, 16, 16, 0.10, None),
+    ("bf16-gqa-causal-G16", 1, 8, 2, 2048, 128, torch.bfloat16, True, 64, 16, 16, 0.10, None),
+    ("bf16-gqa-causal-chunked", 1, 4, 1, 2048, 128, torch.bfloat16, True, 64, 16, 16, 0.10, 8),
+    ("bf16-noncausal-G8192-tail", 1, 4, 4, 3000, 128, torch.bfloat16, False, 64, 16, 8192, 0.15, None),
+    ("fp16-causal-qps128-bk32", 2, 4, 2, 1536, 64, torch.float16, True, 128, 32, 4, 0.10, None),
+    ("bf16-noncausal-G1-bk64", 1, 2, 1, 1100, 128, torch.bfloat16, False, 64, 64, 1, 0.2, None),
+]
+
+
+@pytest.mark.parametrize("case", SELECT_CASES, ids=[c[0] for c in SELECT_CASES])
+def test_select_bit_exact(device, case):
+    name, B, Hq, Hk, S, D, dtype, causal, qps, bk, G, keep, chunk_rows = case
+    note("select", name)
+    q, k, _ = make_inputs(B, Hq, Hk, S, D, dtype, seed=len(name))
+    th = calibrated_threshold(keep, q, k, qps, bk, G, causal)
+    gaps = orc.gap_from_threshold(th, B, Hq)
+    _, qs_cpu = orc.pool(q, qps, DTN[dtype])
+    nqb = qs_cpu.shape[2]
+    qs, _ = stages.pool_scaled(q.to(device), qps)
+    kd = k.to(device)
+    step = chunk_rows or nqb
+    total_sel = 0
+    for J0 in range(0, nqb, step):
+        nc = min(step, nqb - J0)
+        want_c, want = orc.select(qs_cpu, k, J0, nc, gaps, qps, bk, G, causal, causal, 64)
+        cnt, idx = stages.select_rows(qs[:, :, J0:J0 + nc], kd, J0, float(gaps[0]), None, causal,
+                                      qps, bk, G, causal)
+        got_c, got = gpu_lists(cnt, idx, B, Hq, J0, nc, qps, S, causal, causal)
+        assert np.array_equal(got_c, want_c)
+        assert_lists_equal(got, want, name)
+        total_sel += int(want_c.sum())
+    assert total_sel > 0
+
+
+def test_select_per_head_gaps_and_dense_layout(device):
+    note("select per-head dense")
+    B, Hq, Hk, S, D = 2, 4, 2, 1024, 128
+    q, k, _ = make_inputs(B, Hq, Hk, S, D, torch.bfloat16, seed=21)
+    th = torch.tensor([0.9, 0.5, 0.2, 0.05], dtype=torch.float32)
+    gaps = (-torch.log(th + 1e-9)).float()
+    gaps_bh = gaps.expand(B, Hq).contiguous()
+    _, qs_cpu = orc.pool(q, 64, "bfloat16")
+    nqb = qs_cpu.shape[2]
+    want_c, want = orc.select(qs_cpu, k, 0, nqb, gaps_bh.numpy().reshape(-1), 64, 16, 16, True,
+                              True, 64)
+    pooled = stages.average_vector(q.to(device), 64)
+    cnt, index = stages.fuse_qk_softmax_minp_wo_causal(pooled, k.to(device), 0, gaps.to(device),
+                                                       True, 64, 16, True, 16)
+    assert np.array_equal(cnt.cpu().numpy(), want_c)
+    assert index.shape[-1] == max(min(S, int(want_c.max())), 1)
+    idx = index.cpu().numpy()
+    for b in range(B):
+        for h in range(Hq):
+            for J in range(nqb):
+                c = want_c[b, h, J]
+                assert np.array_equal(idx[b, h, J, :c], want[b][h][J])
+                assert np.all(idx[b, h, J, c:] == 0)
+
+
+def test_select_ties_from_duplicate_keys(device):
+    # Repeated key rows give exactly equal scores: selection at equality.
+    note("select ties")
+    q, k, _ = make_inputs(1, 2, 1, 1024, 64, torch.bfloat16, seed=5)
+    k[:, :, 512:] = k[:, :, :512]
+    _, qs_cpu = orc.pool(q, 64, "bfloat16")
+    qs, _ = stages.pool_scaled(q.to(device), 64)
+    for gap in (0.0, 0.05, 0.3):
+        gaps = np.full(2, gap, np.float32)
+        want_c, want = orc.select(qs_cpu, k, 0, 16, gaps, 64, 16, 2, False, False, 64)
+        cnt, idx = stages.select_rows(qs, k.to(device), 0, gap, None, False, 64, 16, 2, False)
+        got_c, got = gpu_lists(cnt, idx, 1, 2, 0, 16, 64, 1024, False, False)
+        assert np.array_equal(got_c, want_c)
+        assert_lists_equal(got, want, f"ties gap={gap}")
+
+
+# ---------------------------------------------------------------- attention --
+
+ATTN_CASES = [
+    # name, B, Hq, Hk, Sq, Sk, D, dtype, causal, qps, keep
+    ("bf16-causal-gqa-d128", 1, 8, 2, 1536, 1536, 128, torch.bfloat16, True, 64, 0.1),
+    ("bf16-causal-tail-d64-qps128", 1, 4, 4, 1000, 1000, 64, torch.bfloat16, True, 128, 0.1),
+    ("fp16-noncausal-d128", 2, 4, 2, 1100, 1100, 128, torch.float16, False, 64, 0.15),
+    ("bf16-noncausal-sq-ne-sk", 1, 4, 4, 700, 1300, 128, torch.bfloat16, False, 64, 0.2),
+    ("fp32-noncausal-d64", 1, 4, 4, 1024, 1024, 64, torch.float32, False, 64, 0.1),
+]
+
+
+@pytest.mark.parametrize("kernel", [nat.VA_ATTN_AUTO, nat.VA_ATTN_SIMPLE], ids=["auto", "simple"])
+@pytest.mark.parametrize("case", ATTN_CASES, ids=[c[0] for c in ATTN_CASES])
+def test_sparse_attention_matches_oracle(device, case, kernel):
+    name, B, Hq, Hk, Sq, Sk, D, dtype, causal, qps, keep = case
+    note("attn", name, kernel)
+    g = torch.Generator().manual_seed(len(name))
+    q, k, v = make_inputs(B, Hq, Hk, max(Sq, Sk), D, dtype, seed=len(name) + 1)
+    q = q[:, :, :Sq].contiguous()
+    k, v = k[:, :, :Sk].contiguous(), v[:, :, :Sk].contiguous()
+    th = calibrated_threshold(keep, q, k, qps, 16, 16, causal) if Sq == Sk else 0.3
+    _, qs_cpu = orc.pool(q, qps, DTN[dtype])
+    nqb = qs_cpu.shape[2]
+    gaps = orc.gap_from_threshold(th, B, Hq)
+    _, lists = orc.select(qs_cpu, k, 0, nqb, gaps, qps, 16, 16, causal, causal, 64)
+    # Feed the oracle's lists to the GPU kernel through the index layout.
+    caps = [orc.row_capacity(J, qps, Sk, causal, causal) for J in range(nqb)]
+    idx = np.zeros(max(sum(caps) * B * Hq, 1), np.int32)
+    cnt = np.zeros((B, Hq, nqb), np.int32)
+    base = 0
+    for b in range(B):
+        for h in range(Hq):
+            for J in range(nqb):
+                l = lists[b][h][J]
+                idx[base:base + len(l)] = l
+                cnt[b, h, J] = len(l)
+                base += caps[J]
+    out = torch.zeros(B, Hq, Sq, D, dtype=dtype, device=device)
+    stages.sparse_attention(q.to(device), k.to(device), v.to(device), out, 0, nqb,
+                            torch.from_numpy(cnt).to(device), torch.from_numpy(idx).to(device),
+                            causal, qps, kernel=kernel)
+    bc, bi = orc.local_blocks(B, Hq, Sq, qps, causal)
+    want = orc.attention(q, k, v, qps, causal, bc, bi, lists)
+    err = np.abs(out.float().cpu().numpy() - want)
+    tol = (ATOL_MAX_F32, ATOL_MEAN_F32) if dtype == torch.float32 else (ATOL_MAX, ATOL_MEAN)
+    assert err.max() <= tol[0] and err.mean() <= tol[1], (err.max(), err.mean())
+
+
+def test_mfma_all_keys_equals_dense_sdpa(device):
+    # Non-causal, every key selected: the sparse kernel is dense attention.
+    note("attn dense equivalence")
+    B, Hq, Hk, S, D = 1, 4, 2, 2048, 128
+    q, k, v = make_inputs(B, Hq, Hk, S, D, torch.bfloat16, seed=9)
+    qd, kd, vd = q.to(device), k.to(device), v.to(device)
+    nqb = S // 64
+    cnt = torch.full((B, Hq, nqb), S, dtype=torch.int32, device=device)
+    idx = torch.arange(S, dtype=torch.int32, device=device).repeat(B * Hq * nqb)
+    out = torch.empty_like(qd)
+    stages.sparse_attention(qd, kd, vd, out, 0, nqb, cnt, idx, False, 64, kernel=nat.VA_ATTN_MFMA)
+    ref = torch.nn.functional.scaled_dot_product_attention(
+        qd.float(), kd.float().repeat_interleave(2, 1).contiguous(),
+        vd.float().repeat_interleave(2, 1).contiguous())
+    err = (out.float() - ref).abs()
+    assert err.max().item() <= ATOL_MAX and err.mean().item() <= ATOL_MEAN
+
+
+# -------------------------------------------------------------- end to end --
+
+E2E_CASES = [
+    # name, B, Hq, Hk, S, D, dtype, causal, qps, bk, G, chunk, threshold
+    ("vlm-like-causal", 1, 8, 2, 2048, 128, torch.bfloat16, True, 64, 16, 16, 1024, 0.5),
+    ("dit-like-noncausal", 1, 4, 4, 2000, 128, torch.bfloat16, False, 64, 16, 8192, 1024, 0.3),
+    ("causal-qps128-bk16", 1, 4, 4, 1300, 64, torch.bfloat16, True, 128, 16, 4, 512, 0.6),
+    ("A-fp32-noncausal", 1, 4, 4, 4096, 64, torch.float32, False, 64, 16, 16, 4096, 0.35),
+]
+
+
+@pytest.mark.parametrize("case", E2E_CASES, ids=[c[0] for c in E2E_CASES])
+def test_vecattention_prefill_matches_oracle(device, case):
+    name, B, Hq, Hk, S, D, dtype, causal, qps, bk, G, chunk, th = case
+    note("e2e", name)
+    q, k, v = make_inputs(B, Hq, Hk, S, D, dtype, seed=3)
+    # Queries arrive as a (B, H, S, D) view of (B, S, H, D) memory, as in the VLM caller.
+    qv = q.transpose(1, 2).contiguous().to(device).transpose(1, 2)
+    out = VecAttention_prefill(qv, k.to(device), v.to(device), threshold=th, q_pooling_size=qps,
+                               k_local_size=bk, group_k_block=G, causal=causal, chunk_size=chunk)
+    torch.cuda.synchronize()
+    assert out.shape == (B, Hq, S, D) and out.dtype == dtype and out.is_contiguous()
+    want, _ = orc.prefill(q, k, v, th, qps, bk, G, causal, chunk, 64, DTN[dtype])
+    err = np.abs(out.float().cpu().numpy() - want)
+    tol = (ATOL_MAX_F32, ATOL_MEAN_F32) if dtype == torch.float32 else (ATOL_MAX, ATOL_MEAN)
+    assert err.max() <= tol[0] and err.mean() <= tol[1], (err.max(), err.mean())
+
+
+def test_prefill_per_head_threshold_tensor(device):
+    note("e2e per-head")
+    B, Hq, S, D = 1, 4, 1024, 128
+    q, k, v = make_inputs(B, Hq, Hq, S, D, torch.bfloat16, seed=4)
+    th = torch.tensor([0.9, 0.5, 0.1, 0.01])
+    out = VecAttention_prefill(q.to(device), k.to(device), v.to(device), th.to(device), 64, 16, 16,
+                               False, 512)
+    want, _ = orc.prefill(q, k, v, th.numpy(), 64, 16, 16, False, 512, 64, "bfloat16")
+    err = np.abs(out.float().cpu().numpy() - want)
+    assert err.max() <= ATOL_MAX and err.mean() <= ATOL_MEAN
+
+
+# --------------------------------------------- full-size properties (config B) --
+
+@pytest.fixture(scope="module")
+def config_b(device):
+    q, k, v = make_inputs(1, 28, 4, 32768, 128, torch.bfloat16, seed=0)
+    return q, k, v, q.to(device), k.to(device), v.to(device)
+
+
+def test_full_size_large_gap_selects_every_selectable_key(config_b):
+    note("full-size all selectable")
+    q, k, v, qd, kd, vd = config_b
+    qps, nqb = 64, 512
+    qs, _ = stages.pool_scaled(qd, qps)
+    cnt, _ = stages.select_rows(qs, kd, 0, 1e6, None, True, qps, 16, 16, True)
+    J = torch.arange(nqb)
+    want = torch.clamp((J - 1) * qps, min=0) - torch.where((J % 64 == 0) & (J >= 2), 48, 0)
+    assert torch.equal(cnt.cpu(), want.to(torch.int32).expand(1, 28, nqb))
+
+
+def test_full_size_rows_match_oracle(config_b):
+    # Bit-exact selection and attention on sampled rows of the full 32K config.
+    note("full-size sampled rows")
+    q, k, v, qd, kd, vd = config_b
+    qps = 64
+    out = VecAttention_prefill(qd, kd, vd, 0.35, qps, 16, 16, True, 32768)
+    qs_gpu, _ = stages.pool_scaled(qd, qps)
+    cnt, idx = stages.select_rows(qs_gpu, kd, 0, -math.log(0.35 + 1e-9), None, True, qps, 16, 16,
+                                  True)
+    torch.cuda.synchronize()
+    out_cpu = out.float().cpu().numpy()
+    cnt_cpu, idx_cpu = cnt.cpu().numpy(), idx.cpu().numpy()
+    gaps = orc.gap_from_threshold(0.35, 1, 28)
+    rng = np.random.default_rng(0)
+    for h in (0, 13, 27):
+        qh, kh, vh = q[:, h:h + 1], k[:, h // 7:h // 7 + 1], v[:, h // 7:h // 7 + 1]
+        _, qs = orc.pool(qh, qps, "bfloat16")
+        for J in sorted(rng.choice(np.arange(1, 512), 4, replace=False).tolist()) + [511]:
+            _, lists = orc.select(qs, kh, 0, 512, gaps[:1], qps, 16, 16, True, True, 64,
+                                  rows=(J, J + 1))
+            off = stages.row_offset(32768, qps, True, True, 0, 512, h, J)
+            c = cnt_cpu[0, h, J]
+            assert np.array_equal(idx_cpu[off:off + c], lists[0][0][J]), (h, J)
+            bc, bi = orc.local_blocks(1, 1, 32768, qps, True)
+            want = orc.attention(qh, kh, vh, qps, True, bc, bi, [[lists[0][0][J:J + 1]]], J0=J,
+                                 nc=1)
+            err = np.abs(out_cpu[0, h, J * qps:(J + 1) * qps] - want[0, 0])
+            assert err.max() <= ATOL_MAX and err.mean() <= ATOL_MEAN, (h, J, err.max())
+
+
+def test_full_size_chunking_invariant(config_b):
+    # Chunks of 16K and 32K start q-block programs at multiples of 64 rows
+    # either way, so the selection and therefore the output are identical.
+    note("full-size chunk invariance")
+    _, _, _, qd, kd, vd = config_b
+    a = VecAttention_prefill(qd, kd, vd, 0.35, 64, 16, 16, True, 32768)
+    b = VecAttention_prefill(qd, kd, vd, 0.35, 64, 16, 16, True, 16384)
+    assert torch.equal(a, b)

@@ -1,0 +1,108 @@
+"""libvecattn.so on a machine without a GPU: it loads, exports every symbol
+include/vecattn.h declares, answers its pure-host queries, and turns invalid
+arguments into error codes before any device work."""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as orc
+from vecattention_amd import _native as nat
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+@pytest.fixture(scope="module")
+def L():
+    if not os.path.exists(nat.LIB_PATH):
+        from vecattention_amd import build
+        build.build()
+    return nat.lib()
+
+
+def header_functions():
+    text = open(os.path.join(ROOT, "include", "vecattn.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(va_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_every_declared_symbol_is_exported(L):
+    names = header_functions()
+    assert len(names) >= 9
+    for name in names:
+        assert hasattr(L, name), name
+        assert name in nat.SIGNATURES, name
+    assert sorted(nat.SIGNATURES) == names
+
+
+def test_version_and_error_string(L):
+    assert L.va_version() == 100
+    assert isinstance(L.va_last_error(), bytes)
+
+
+@pytest.mark.skipif(torch.cuda.is_available(), reason="checks the no-device path")
+def test_no_device_is_an_error(L):
+    rc = L.va_device_count()
+    assert rc == nat.VA_ERR_HIP
+    assert L.va_last_error()
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("wo_init", [False, True])
+def test_index_layout_matches_capacities(L, causal, wo_init):
+    B, Hq, Sk, qps = 2, 3, 1000, 64
+    for J0, nc in [(0, 16), (5, 7), (3, 1)]:
+        caps = [orc.row_capacity(J0 + jr, qps, Sk, causal, wo_init) for jr in range(nc)]
+        total = L.va_select_index_capacity(B, Hq, Sk, qps, int(causal), int(wo_init), J0, nc, 0)
+        assert total == B * Hq * sum(caps)
+        off = [L.va_select_row_offset(Sk, qps, int(causal), int(wo_init), J0, nc, 0, bh, jr)
+               for bh in range(B * Hq) for jr in range(nc)]
+        want = np.concatenate([[0], np.cumsum(caps * (B * Hq))[:-1]])
+        assert off == want.tolist()
+    # dense rows
+    assert L.va_select_row_offset(Sk, qps, 1, 1, 0, 4, 1008, 2, 3) == (2 * 4 + 3) * 1008
+
+
+def _null_select(L, **over):
+    args = dict(dtype=nat.VA_BF16, qs=1, sqb=0, sqh=0, sqn=0, k=1, skb=0, skh=0, sks=128, B=1, Hq=4,
+                Hk=2, Sk=1024, D=128, qps=64, bk=16, G=16, causal=1, wo_init=1, J0=0, nc=16, bsq=64,
+                gap=0.2, gaps=None, dense=0, counts=1, indices=1, stream=None)
+    args.update(over)
+    return L.va_select(*args.values())
+
+
+def test_select_argument_errors_before_launch(L):
+    assert _null_select(L, bk=48) == nat.VA_ERR_UNSUPPORTED
+    assert b"k_local_size" in L.va_last_error()
+    assert _null_select(L, Hk=3) == nat.VA_ERR_ARG
+    assert _null_select(L, qps=64, bk=128) == nat.VA_ERR_ARG   # the reference's causal assert
+    assert _null_select(L, qps=64, bk=128, causal=0) == nat.VA_ERR_UNSUPPORTED  # wo_init tiling
+    assert _null_select(L, dtype=7) == nat.VA_ERR_ARG
+    assert _null_select(L, counts=None) == nat.VA_ERR_ARG
+    assert _null_select(L, D=512) == nat.VA_ERR_UNSUPPORTED
+
+
+def test_prefill_argument_errors_before_launch(L):
+    f = L.va_prefill
+    base = [nat.VA_BF16, 1, 0, 0, 128, 1, 0, 0, 128, 1, 0, 0, 128, 1, 0, 0, 128,
+            1, 4, 2, 1024, 1024, 128, 0.2, None, 64, 16, 16, 1, 1000, 64, 1, 1 << 30, None]
+    a = list(base)
+    assert f(*a) == nat.VA_ERR_ARG            # chunk 1000 not a multiple of 64
+    a = list(base); a[29] = 1024; a[25] = 96
+    assert f(*a) == nat.VA_ERR_ARG            # q_pooling_size not 64/128
+    a = list(base); a[29] = 1024; a[32] = 16
+    assert f(*a) == nat.VA_ERR_WORKSPACE      # workspace too small
+    a = list(base); a[29] = 1024; a[21] = 512
+    assert f(*a) == nat.VA_ERR_UNSUPPORTED    # causal with Sq != Sk
+
+
+def test_workspace_size_covers_largest_chunk(L):
+    # causal: the last chunk has the largest index capacity.
+    B, Hq, S, D, qps, chunk = 1, 28, 131072, 128, 64, 32768
+    ws = L.va_prefill_workspace_size(nat.VA_BF16, B, Hq, S, S, D, qps, 1, chunk)
+    last = L.va_select_index_capacity(B, Hq, S, qps, 1, 1, (S - chunk) // qps, chunk // qps, 0)
+    assert ws >= last * 4 + B * Hq * (S // qps) * D * 2
+    assert ws < last * 4 + B * Hq * (S // qps) * D * 2 + 1 << 20

@@ -1,0 +1,14 @@
+"""MI355X-native VecAttention prefill (selection + vector-sparse attention).
+
+Drop-in for ``spattn.src.VecAttention.VecAttention_prefill`` and the
+selection-stage helpers its threshold tuner calls.
+"""
+from .vecattention import VecAttention_prefill, threshold_to_gap
+from .stages import average_vector, fuse_qk_softmax_minp_wo_causal
+
+__all__ = [
+    "VecAttention_prefill",
+    "average_vector",
+    "fuse_qk_softmax_minp_wo_causal",
+    "threshold_to_gap",
+]

@@ -1,0 +1,100 @@
+"""ctypes binding of libvecattn.so (the C ABI declared in include/vecattn.h).
+
+The library is built in-tree by ``python -m vecattention_amd.build`` (or
+``__graft_entry__.build()``).  There is no fallback: if the library is missing
+or fails to load, every entry point raises.
+"""
+import ctypes
+import os
+import threading
+
+import torch
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libvecattn.so")
+
+VA_F32, VA_BF16, VA_F16 = 0, 1, 2
+VA_OK, VA_ERR_ARG, VA_ERR_UNSUPPORTED, VA_ERR_HIP, VA_ERR_WORKSPACE = 0, -1, -2, -3, -4
+VA_ATTN_AUTO, VA_ATTN_MFMA, VA_ATTN_SIMPLE = 0, 1, 2
+
+_DTYPES = {torch.float32: VA_F32, torch.bfloat16: VA_BF16, torch.float16: VA_F16}
+
+_lock = threading.Lock()
+_lib = None
+
+_i64 = ctypes.c_int64
+_int = ctypes.c_int
+_vp = ctypes.c_void_p
+_f32 = ctypes.c_float
+
+# name -> (restype, argtypes); the exported surface of include/vecattn.h.
+SIGNATURES = {
+    "va_version": (_int, []),
+    "va_last_error": (ctypes.c_char_p, []),
+    "va_device_count": (_int, []),
+    "va_pool": (_int, [_int, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp]),
+    "va_select": (_int, [_int, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+                         _i64, _i64, _i64, _int, _int, _i64, _i64, _i64, _f32, _vp, _i64, _vp,
+                         _vp, _vp]),
+    "va_select_index_capacity": (_i64, [_i64, _i64, _i64, _i64, _int, _int, _i64, _i64, _i64]),
+    "va_select_row_offset": (_i64, [_i64, _i64, _int, _int, _i64, _i64, _i64, _i64, _i64]),
+    "va_sparse_attn": (_int, [_int, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _vp, _i64, _i64,
+                              _i64, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+                              _i64, _int, _int, _i64, _i64, _i64, _vp, _vp, _f32, _int, _vp]),
+    "va_prefill_workspace_size": (_i64, [_int, _i64, _i64, _i64, _i64, _i64, _i64, _int, _i64]),
+    "va_prefill": (_int, [_int, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _vp, _i64, _i64,
+                          _i64, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _f32,
+                          _vp, _i64, _i64, _i64, _int, _i64, _i64, _vp, _i64, _vp]),
+}
+
+
+class NativeError(RuntimeError):
+    """A libvecattn call returned an error code."""
+
+    def __init__(self, fn, code, msg):
+        super().__init__(f"{fn} failed ({code}): {msg}")
+        self.code = code
+
+
+def lib():
+    """Load (once) and return the ctypes handle; raises if the library is absent."""
+    global _lib
+    with _lock:
+        if _lib is None:
+            if not os.path.exists(LIB_PATH):
+                raise RuntimeError(
+                    f"{LIB_PATH} is missing: build it with `python -m vecattention_amd.build` "
+                    "(the HIP path has no CPU fallback)")
+            handle = ctypes.CDLL(LIB_PATH)
+            for name, (res, args) in SIGNATURES.items():
+                fn = getattr(handle, name)
+                fn.restype = res
+                fn.argtypes = args
+            _lib = handle
+        return _lib
+
+
+def check(fn, code):
+    if code != VA_OK:
+        msg = lib().va_last_error().decode(errors="replace")
+        if code == VA_ERR_ARG:
+            raise AssertionError(f"{fn}: {msg}")
+        if code == VA_ERR_UNSUPPORTED:
+            raise NotImplementedError(f"{fn}: {msg}")
+        raise NativeError(fn, code, msg)
+    return code
+
+
+def dtype_code(t):
+    try:
+        return _DTYPES[t.dtype]
+    except KeyError:
+        raise TypeError(f"unsupported dtype {t.dtype}; expected float32, bfloat16 or float16")
+
+
+def ptr(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else None
+
+
+def stream_ptr(device):
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)

@@ -1,0 +1,312 @@
+// C ABI of libvecattn.so: argument validation, dispatch and the fused prefill.
+// Declarations and their reference counterparts: include/vecattn.h.
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+#include "../../include/vecattn.h"
+#include "common.h"
+
+namespace va {
+hipError_t launch_pool(int dtype, const void* q, int64_t B, int64_t H, int64_t S, int64_t D,
+                       int64_t sqb, int64_t sqh, int64_t sqs, int64_t qps, void* pooled,
+                       void* scaled, hipStream_t stream);
+hipError_t launch_select_exact(int dtype, const void* qs, int64_t sqb, int64_t sqh,
+                               int64_t sqn, const void* k,
+                               int64_t skb, int64_t skh, int64_t sks, int64_t B, int64_t Hq,
+                               int64_t Hk, int64_t Sk, int64_t D, int64_t qps, int64_t bk,
+                               int64_t group, int causal, int64_t bsq, float gap_scalar,
+                               const float* gaps, const RowLayout& lay, int32_t* counts,
+                               int32_t* indices, hipStream_t stream);
+hipError_t launch_attn_simple(int dtype, const void* q, const int64_t* sq, const void* k,
+                              const int64_t* sk, const void* v, const int64_t* sv, void* out,
+                              const int64_t* so, int64_t B, int64_t Hq, int64_t Hk, int64_t Sq,
+                              int64_t Sk, int64_t D, int64_t qps, int causal, float scale_log2,
+                              const int32_t* counts, const int32_t* indices,
+                              const RowLayout& lay, hipStream_t stream);
+bool attn_mfma_supported(int dtype, int64_t D, int64_t qps);
+hipError_t launch_attn_mfma(int dtype, int64_t D, int64_t qps, const void* q, const int64_t* sq,
+                            const void* k, const int64_t* sk, const void* v, const int64_t* sv,
+                            void* out, const int64_t* so, int64_t B, int64_t Hq, int64_t Hk,
+                            int64_t Sq, int64_t Sk, int causal, float scale_log2,
+                            const int32_t* counts, const int32_t* indices, const RowLayout& lay,
+                            hipStream_t stream);
+}  // namespace va
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+int ok() {
+  g_err.clear();
+  return VA_OK;
+}
+
+int hip_check(hipError_t e, const char* what) {
+  if (e != hipSuccess) return fail(VA_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+  return VA_OK;
+}
+
+int64_t esize(int dtype) { return dtype == VA_F32 ? 4 : 2; }
+bool dtype_ok(int dtype) { return dtype == VA_F32 || dtype == VA_BF16 || dtype == VA_F16; }
+bool pow2(int64_t x) { return x > 0 && (x & (x - 1)) == 0; }
+int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
+
+va::RowLayout make_layout(int64_t J0, int64_t nc, int64_t qps, int64_t Sk, int causal,
+                          int wo_init, int64_t dense_stride) {
+  va::RowLayout lay;
+  lay.J0 = J0;
+  lay.nc = nc;
+  lay.qps = qps;
+  lay.Sk = Sk;
+  lay.dense_stride = dense_stride;
+  lay.causal = causal ? 1 : 0;
+  lay.wo_init = wo_init ? 1 : 0;
+  return lay;
+}
+
+constexpr int64_t kMaxGrid = (int64_t(1) << 31) - 1;
+
+int check_select_args(int dtype, const void* qs, const void* k, int64_t B, int64_t Hq,
+                      int64_t Hk, int64_t Sk, int64_t D, int64_t qps, int64_t bk,
+                      int64_t group, int causal, int wo_init, int64_t J0, int64_t nc,
+                      int64_t bsq) {
+  if (!dtype_ok(dtype)) return fail(VA_ERR_ARG, "unknown dtype %d", dtype);
+  if (!qs || !k) return fail(VA_ERR_ARG, "null tensor pointer");
+  if (B <= 0 || Hq <= 0 || Hk <= 0 || Sk <= 0 || D <= 0 || nc <= 0 || J0 < 0)
+    return fail(VA_ERR_ARG, "non-positive size");
+  if (Hq % Hk) return fail(VA_ERR_ARG, "num q heads %lld not a multiple of kv heads %lld",
+                           (long long)Hq, (long long)Hk);
+  if (D > 256) return fail(VA_ERR_UNSUPPORTED, "head_dim %lld > 256", (long long)D);
+  if (qps <= 0) return fail(VA_ERR_ARG, "q_pooling_size must be positive");
+  if (!pow2(bk) || bk < 16 || bk > 256)
+    return fail(VA_ERR_UNSUPPORTED, "k_local_size %lld must be a power of two in [16, 256]",
+                (long long)bk);
+  if (group <= 0) return fail(VA_ERR_ARG, "group_k_block must be positive");
+  if (bsq <= 0) return fail(VA_ERR_ARG, "bsq must be positive");
+  if (causal && qps % bk) return fail(VA_ERR_ARG, "causal requires q_pooling_size %% k_local_size == 0");
+  if (wo_init && qps % bk)
+    return fail(VA_ERR_UNSUPPORTED, "wo_initial requires q_pooling_size %% k_local_size == 0");
+  if (Sk >= (int64_t(1) << 31)) return fail(VA_ERR_UNSUPPORTED, "Sk does not fit int32 indices");
+  if (cdiv(nc, 16) * B * Hq > kMaxGrid) return fail(VA_ERR_UNSUPPORTED, "grid too large");
+  return VA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int va_version(void) { return 100; }
+
+const char* va_last_error(void) { return g_err.c_str(); }
+
+int va_device_count(void) {
+  int n = 0;
+  hipError_t e = hipGetDeviceCount(&n);
+  if (e != hipSuccess) return fail(VA_ERR_HIP, "hipGetDeviceCount: %s", hipGetErrorString(e));
+  if (n <= 0) return fail(VA_ERR_HIP, "no HIP device");
+  ok();
+  return n;
+}
+
+int va_pool(int dtype, const void* q, int64_t B, int64_t H, int64_t S, int64_t D, int64_t sqb,
+            int64_t sqh, int64_t sqs, int64_t qps, void* pooled, void* scaled, void* stream) {
+  if (!dtype_ok(dtype)) return fail(VA_ERR_ARG, "unknown dtype %d", dtype);
+  if (!q) return fail(VA_ERR_ARG, "null q");
+  if (B <= 0 || H <= 0 || S <= 0 || D <= 0 || qps <= 0) return fail(VA_ERR_ARG, "non-positive size");
+  if (D > 256) return fail(VA_ERR_UNSUPPORTED, "head_dim %lld > 256", (long long)D);
+  if (B * H > 65535) return fail(VA_ERR_UNSUPPORTED, "B*H > 65535");
+  if (!pooled && !scaled) return ok();
+  int rc = hip_check(va::launch_pool(dtype, q, B, H, S, D, sqb, sqh, sqs, qps, pooled, scaled,
+                                     static_cast<hipStream_t>(stream)),
+                     "pool launch");
+  return rc ? rc : ok();
+}
+
+int64_t va_select_index_capacity(int64_t B, int64_t Hq, int64_t Sk, int64_t qps, int causal,
+                                 int wo_init, int64_t J0, int64_t nc, int64_t dense_stride) {
+  if (B <= 0 || Hq <= 0 || Sk <= 0 || qps <= 0 || nc <= 0 || J0 < 0) return -1;
+  return B * Hq * make_layout(J0, nc, qps, Sk, causal, wo_init, dense_stride).block_size();
+}
+
+int64_t va_select_row_offset(int64_t Sk, int64_t qps, int causal, int wo_init, int64_t J0,
+                             int64_t nc, int64_t dense_stride, int64_t bh, int64_t jr) {
+  if (Sk <= 0 || qps <= 0 || nc <= 0 || J0 < 0 || jr < 0 || jr > nc || bh < 0) return -1;
+  return make_layout(J0, nc, qps, Sk, causal, wo_init, dense_stride).row_offset(bh, jr);
+}
+
+int va_select(int dtype, const void* qs, int64_t sqb, int64_t sqh, int64_t sqn,
+              const void* k, int64_t skb,
+              int64_t skh, int64_t sks, int64_t B, int64_t Hq, int64_t Hk, int64_t Sk, int64_t D,
+              int64_t qps, int64_t bk, int64_t group, int causal, int wo_init, int64_t J0,
+              int64_t nc, int64_t bsq, float gap, const float* gaps, int64_t dense_stride,
+              int32_t* counts, int32_t* indices, void* stream) {
+  int rc = check_select_args(dtype, qs, k, B, Hq, Hk, Sk, D, qps, bk, group, causal, wo_init, J0,
+                             nc, bsq);
+  if (rc) return rc;
+  if (!counts || !indices) return fail(VA_ERR_ARG, "null output pointer");
+  if (dense_stride < 0) return fail(VA_ERR_ARG, "negative dense_stride");
+  if (dense_stride > 0 && dense_stride < Sk)
+    return fail(VA_ERR_ARG, "dense_stride %lld < Sk %lld", (long long)dense_stride, (long long)Sk);
+  const va::RowLayout lay = make_layout(J0, nc, qps, Sk, causal, wo_init, dense_stride);
+  rc = hip_check(va::launch_select_exact(dtype, qs, sqb, sqh, sqn, k, skb, skh, sks, B, Hq, Hk, Sk, D,
+                                         qps, bk, group, causal, bsq, gap, gaps, lay, counts,
+                                         indices, static_cast<hipStream_t>(stream)),
+                 "select launch");
+  return rc ? rc : ok();
+}
+
+static int attn_dispatch(int dtype, const void* q, const int64_t* sq, const void* k,
+                         const int64_t* sk, const void* v, const int64_t* sv, void* out,
+                         const int64_t* so, int64_t B, int64_t Hq, int64_t Hk, int64_t Sq,
+                         int64_t Sk, int64_t D, int64_t qps, int causal,
+                         const va::RowLayout& lay, const int32_t* counts,
+                         const int32_t* indices, float softmax_scale, int kernel,
+                         hipStream_t stream) {
+  const float scale_log2 = softmax_scale * 1.4426950408889634f;
+  const int64_t es = esize(dtype);
+  auto aligned = [&](const void* p, const int64_t* s, int64_t a) {
+    return reinterpret_cast<uintptr_t>(p) % 16 == 0 && s[0] % a == 0 && s[1] % a == 0 &&
+           s[2] % a == 0;
+  };
+  const bool mfma_shape = va::attn_mfma_supported(dtype, D, qps);
+  const bool mfma_align = aligned(q, sq, 16 / es) && aligned(k, sk, 16 / es) &&
+                          aligned(v, sv, 16 / es) && aligned(out, so, 8 / es);
+  bool use_mfma = false;
+  if (kernel == VA_ATTN_MFMA) {
+    if (!mfma_shape)
+      return fail(VA_ERR_UNSUPPORTED, "MFMA attention needs bf16/fp16, D in {64,128}, qps in {64,128}");
+    if (!mfma_align) return fail(VA_ERR_UNSUPPORTED, "MFMA attention needs 16-byte aligned rows");
+    use_mfma = true;
+  } else if (kernel == VA_ATTN_AUTO) {
+    use_mfma = mfma_shape && mfma_align;
+  } else if (kernel != VA_ATTN_SIMPLE) {
+    return fail(VA_ERR_ARG, "unknown kernel selector %d", kernel);
+  }
+  if (!use_mfma && qps > 1024) return fail(VA_ERR_UNSUPPORTED, "q_pooling_size > 1024");
+  hipError_t e = use_mfma
+                     ? va::launch_attn_mfma(dtype, D, qps, q, sq, k, sk, v, sv, out, so, B, Hq,
+                                            Hk, Sq, Sk, causal, scale_log2, counts, indices, lay,
+                                            stream)
+                     : va::launch_attn_simple(dtype, q, sq, k, sk, v, sv, out, so, B, Hq, Hk, Sq,
+                                              Sk, D, qps, causal, scale_log2, counts, indices,
+                                              lay, stream);
+  return hip_check(e, "attention launch");
+}
+
+int va_sparse_attn(int dtype, const void* q, int64_t sqb, int64_t sqh, int64_t sqs,
+                   const void* k, int64_t skb, int64_t skh, int64_t sks, const void* v,
+                   int64_t svb, int64_t svh, int64_t svs, void* out, int64_t sob, int64_t soh,
+                   int64_t sos, int64_t B, int64_t Hq, int64_t Hk, int64_t Sq, int64_t Sk,
+                   int64_t D, int64_t qps, int causal, int wo_init, int64_t J0, int64_t nc,
+                   int64_t dense_stride, const int32_t* counts, const int32_t* indices,
+                   float softmax_scale, int kernel, void* stream) {
+  if (!dtype_ok(dtype)) return fail(VA_ERR_ARG, "unknown dtype %d", dtype);
+  if (!q || !k || !v || !out) return fail(VA_ERR_ARG, "null tensor pointer");
+  if ((counts == nullptr) != (indices == nullptr))
+    return fail(VA_ERR_ARG, "counts and indices must both be given or both be NULL");
+  if (B <= 0 || Hq <= 0 || Hk <= 0 || Sq <= 0 || Sk <= 0 || D <= 0 || qps <= 0 || nc <= 0 || J0 < 0)
+    return fail(VA_ERR_ARG, "non-positive size");
+  if (Hq % Hk) return fail(VA_ERR_ARG, "num q heads not a multiple of kv heads");
+  if (D > 256) return fail(VA_ERR_UNSUPPORTED, "head_dim %lld > 256", (long long)D);
+  if (causal && Sq != Sk) return fail(VA_ERR_UNSUPPORTED, "causal attention needs Sq == Sk");
+  if (J0 + nc > cdiv(Sq, qps)) return fail(VA_ERR_ARG, "rows [J0, J0+nc) exceed q blocks");
+  if (nc * B * Hq > kMaxGrid) return fail(VA_ERR_UNSUPPORTED, "grid too large");
+  const int64_t sq[3] = {sqb, sqh, sqs}, sk[3] = {skb, skh, sks}, sv[3] = {svb, svh, svs},
+                so[3] = {sob, soh, sos};
+  const va::RowLayout lay = make_layout(J0, nc, qps, Sk, causal, wo_init, dense_stride);
+  int rc = attn_dispatch(dtype, q, sq, k, sk, v, sv, out, so, B, Hq, Hk, Sq, Sk, D, qps, causal,
+                         lay, counts, indices, softmax_scale, kernel,
+                         static_cast<hipStream_t>(stream));
+  return rc ? rc : ok();
+}
+
+// Workspace of va_prefill: [scaled pooled q][counts][indices], 256-byte aligned.
+static void prefill_segments(int dtype, int64_t B, int64_t Hq, int64_t Sq, int64_t Sk, int64_t D,
+                             int64_t qps, int causal, int64_t chunk, int64_t* qs_bytes,
+                             int64_t* cnt_bytes, int64_t* idx_bytes) {
+  const int64_t nqb = cdiv(Sq, qps);
+  *qs_bytes = align256(B * Hq * nqb * D * esize(dtype));
+  const int64_t nc_max = cdiv(chunk < Sq ? chunk : Sq, qps);
+  *cnt_bytes = align256(B * Hq * nc_max * 4);
+  int64_t idx_max = 0;
+  for (int64_t i = 0; i < Sq; i += chunk) {
+    const int64_t rows = (Sq - i < chunk) ? (Sq - i) : chunk;
+    const int64_t nc = cdiv(rows, qps);
+    const int64_t cap =
+        B * Hq * make_layout(i / qps, nc, qps, Sk, causal, causal, 0).block_size();
+    if (cap > idx_max) idx_max = cap;
+  }
+  *idx_bytes = align256((idx_max > 0 ? idx_max : 1) * 4);
+}
+
+int64_t va_prefill_workspace_size(int dtype, int64_t B, int64_t Hq, int64_t Sq, int64_t Sk,
+                                  int64_t D, int64_t qps, int causal, int64_t chunk_size) {
+  if (!dtype_ok(dtype) || B <= 0 || Hq <= 0 || Sq <= 0 || Sk <= 0 || D <= 0 || qps <= 0 ||
+      chunk_size <= 0 || chunk_size % qps)
+    return -1;
+  int64_t a, b, c;
+  prefill_segments(dtype, B, Hq, Sq, Sk, D, qps, causal, chunk_size, &a, &b, &c);
+  return a + b + c;
+}
+
+int va_prefill(int dtype, const void* q, int64_t sqb, int64_t sqh, int64_t sqs, const void* k,
+               int64_t skb, int64_t skh, int64_t sks, const void* v, int64_t svb, int64_t svh,
+               int64_t svs, void* out, int64_t sob, int64_t soh, int64_t sos, int64_t B,
+               int64_t Hq, int64_t Hk, int64_t Sq, int64_t Sk, int64_t D, float gap,
+               const float* gaps, int64_t qps, int64_t bk, int64_t group, int causal,
+               int64_t chunk_size, int64_t bsq, void* workspace, int64_t workspace_bytes,
+               void* stream) {
+  if (chunk_size <= 0 || chunk_size % qps)
+    return fail(VA_ERR_ARG, "chunk_size must be a multiple of q_pooling_size");
+  if (qps != 64 && qps != 128) return fail(VA_ERR_ARG, "q_pooling_size must be 64 or 128");
+  if (!q || !k || !v || !out) return fail(VA_ERR_ARG, "null tensor pointer");
+  if (causal && Sq != Sk) return fail(VA_ERR_UNSUPPORTED, "causal prefill needs Sq == Sk");
+  const int64_t need = va_prefill_workspace_size(dtype, B, Hq, Sq, Sk, D, qps, causal, chunk_size);
+  if (need < 0) return fail(VA_ERR_ARG, "invalid prefill sizes");
+  if (!workspace || workspace_bytes < need)
+    return fail(VA_ERR_WORKSPACE, "workspace %lld bytes < required %lld",
+                (long long)workspace_bytes, (long long)need);
+  const int64_t nqb = cdiv(Sq, qps);
+  int64_t qs_bytes, cnt_bytes, idx_bytes;
+  prefill_segments(dtype, B, Hq, Sq, Sk, D, qps, causal, chunk_size, &qs_bytes, &cnt_bytes,
+                   &idx_bytes);
+  char* ws = static_cast<char*>(workspace);
+  void* qs = ws;
+  int32_t* counts = reinterpret_cast<int32_t*>(ws + qs_bytes);
+  int32_t* indices = reinterpret_cast<int32_t*>(ws + qs_bytes + cnt_bytes);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+
+  int rc = va_pool(dtype, q, B, Hq, Sq, D, sqb, sqh, sqs, qps, nullptr, qs, stream);
+  if (rc) return rc;
+  const float scale = float(1.0 / std::sqrt(double(D)));
+  for (int64_t i = 0; i < Sq; i += chunk_size) {
+    const int64_t rows = (Sq - i < chunk_size) ? (Sq - i) : chunk_size;
+    const int64_t J0 = i / qps, nc = cdiv(rows, qps);
+    const int64_t es = esize(dtype);
+    const void* qs_chunk = static_cast<const char*>(qs) + J0 * D * es;
+    rc = va_select(dtype, qs_chunk, Hq * nqb * D, nqb * D, D, k, skb, skh, sks, B, Hq, Hk, Sk, D,
+                   qps, bk, group, causal,
+                   causal, J0, nc, bsq, gap, gaps, 0, counts, indices, stream);
+    if (rc) return rc;
+    rc = va_sparse_attn(dtype, q, sqb, sqh, sqs, k, skb, skh, sks, v, svb, svh, svs, out, sob,
+                        soh, sos, B, Hq, Hk, Sq, Sk, D, qps, causal, causal, J0, nc, 0, counts,
+                        indices, scale, VA_ATTN_AUTO, st);
+    if (rc) return rc;
+  }
+  return ok();
+}
+
+}  // extern "C"

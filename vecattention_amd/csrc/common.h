@@ -1,0 +1,107 @@
+// Shared device/host helpers for the VecAttention prefill kernels (gfx950).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace va {
+
+enum DType : int { kF32 = 0, kBF16 = 1, kF16 = 2 };
+
+// Raw 16-bit storage types; arithmetic goes through explicit conversions so
+// that every rounding step is visible.
+struct bf16_t { uint16_t bits; };
+struct f16_t { uint16_t bits; };
+
+__host__ __device__ inline float bits_to_float(uint32_t u) {
+  return __builtin_bit_cast(float, u);
+}
+__host__ __device__ inline uint32_t float_to_bits(float f) {
+  return __builtin_bit_cast(uint32_t, f);
+}
+
+// bf16 -> fp32 is exact (bf16 is the upper half of an fp32 pattern).
+__device__ inline float to_f32(bf16_t x) { return bits_to_float(uint32_t(x.bits) << 16); }
+__device__ inline float to_f32(f16_t x) { return float(__builtin_bit_cast(_Float16, x.bits)); }
+__device__ inline float to_f32(float x) { return x; }
+
+// Round-to-nearest-even fp32 -> bf16, NaN kept quiet.
+__device__ inline uint16_t rne_bf16_bits(float f) {
+  uint32_t u = float_to_bits(f);
+  if ((u & 0x7f800000u) == 0x7f800000u) {
+    if (u & 0x007fffffu) u |= 0x00400000u;
+    return uint16_t(u >> 16);
+  }
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return uint16_t(u >> 16);
+}
+
+// fp32 -> fp16 with the hardware conversion (round-to-nearest-even mode).
+__device__ inline uint16_t rne_f16_bits(float f) {
+  return __builtin_bit_cast(uint16_t, _Float16(f));
+}
+
+template <typename T> struct Round;
+template <> struct Round<float> {
+  __device__ static float rt(float x) { return x; }
+  __device__ static float store(float x) { return x; }
+};
+template <> struct Round<bf16_t> {
+  __device__ static float rt(float x) { return bits_to_float(uint32_t(rne_bf16_bits(x)) << 16); }
+  __device__ static bf16_t store(float x) { return bf16_t{rne_bf16_bits(x)}; }
+};
+template <> struct Round<f16_t> {
+  __device__ static float rt(float x) { return float(__builtin_bit_cast(_Float16, rne_f16_bits(x))); }
+  __device__ static f16_t store(float x) { return f16_t{rne_f16_bits(x)}; }
+};
+
+// ---------------------------------------------------------------------------
+// Per-row index lists of the selection ("capacity layout").
+//
+// Row J of a chunk [J0, J0+nc) owns `row_capacity(J)` int32 slots: the number
+// of keys the selection rule can ever pick for it.  The rows of one (b, h) are
+// packed back to back, and the (b, h) blocks follow each other, so the offset
+// of every row is a closed form and selection needs no host round trip to size
+// its output.  A non-zero `dense_stride` instead gives every row that stride
+// (the reference's dense (B, H, nqb, padded_k) layout).
+//   causal:     keys [smin, J*qps) with smin = wo_init ? qps : 0
+//   non-causal: keys [smin, Sk)    with smin = wo_init ? min(qps, Sk) : 0
+// ---------------------------------------------------------------------------
+struct RowLayout {
+  int64_t J0, nc, qps, Sk;
+  int64_t dense_stride;  // > 0: dense rows
+  int causal, wo_init;
+
+  __host__ __device__ int64_t smin() const {
+    if (!wo_init) return 0;
+    if (causal) return qps;
+    return qps < Sk ? qps : Sk;
+  }
+  // T(n) = n(n-1)/2 for n >= 1, else 0.
+  __host__ __device__ static int64_t tri(int64_t n) { return n >= 1 ? n * (n - 1) / 2 : 0; }
+  // Sum over j in [0, J) of max(0, j - a).
+  __host__ __device__ int64_t prefix_causal(int64_t J) const {
+    const int64_t a = smin() / qps;  // 0 or 1
+    return tri(J - a);
+  }
+  __host__ __device__ int64_t capacity(int64_t J) const {
+    if (dense_stride > 0) return dense_stride;
+    if (causal) {
+      int64_t c = J * qps - smin();
+      return c > 0 ? c : 0;
+    }
+    return Sk - smin();
+  }
+  // Offset of chunk row jr (J = J0 + jr) inside one (b, h) block.
+  __host__ __device__ int64_t row_in_block(int64_t jr) const {
+    if (dense_stride > 0) return jr * dense_stride;
+    if (causal) return qps * (prefix_causal(J0 + jr) - prefix_causal(J0));
+    return jr * (Sk - smin());
+  }
+  __host__ __device__ int64_t block_size() const { return row_in_block(nc); }
+  __host__ __device__ int64_t row_offset(int64_t bh, int64_t jr) const {
+    return bh * block_size() + row_in_block(jr);
+  }
+};
+
+}  // namespace va

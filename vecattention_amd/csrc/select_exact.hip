@@ -1,0 +1,225 @@
+// TilingSelect — important-vertical-vector selection, exact-arithmetic kernel.
+//
+// Restates the program body of spattn/src/kernels/vecattention_kernels.py:206-272
+// (and the per-head-gap twin :275-345) for one work-group per (b, q head,
+// set of R pooled rows):
+//   * keys are visited in tiles of `bk` in ascending order; a group of `group`
+//     tiles restarts the running maximum (:227,231-233,252);
+//   * with wo_init the first qps keys are skipped (:231);
+//   * the running maximum takes the whole tile's maximum BEFORE the compare
+//     (:257), and key c is selected iff fp32(s_c + gap) >= m (:258);
+//   * the causal tile mask is  r > trunc((k_off - off0) / qps)  with Triton's
+//     truncating signed division (:238,259-260), which rejects the tiles in
+//     (off0 - qps, off0) for the first row of every BLOCK_SIZE_Q program;
+//   * keys past the end are never selected and never move the maximum (the
+//     reference pads them with NaN, :117-127, and tl.max ignores NaN).
+// Output rows are written in ascending key order (the reference appends tile
+// runs in atomic order; the set is the same).
+//
+// Scores are canonical: a sequential fp64 sum over d of exact products
+// (bf16*bf16, fp16*fp16 and fp32*fp32 products are exact in fp64), rounded
+// once to fp32.  This makes every decision bit-identical to the CPU oracle.
+// The kernel is fp64-FMA bound (R*D FMAs per key per work-group).
+#include "common.h"
+
+namespace va {
+
+constexpr int kSelRows = 16;     // pooled rows per work-group
+constexpr int kSelChunk = 256;   // keys per inner chunk (== blockDim.x)
+constexpr int kSelMaxD = 256;
+
+template <typename T>
+__global__ __launch_bounds__(256) void select_exact_kernel(
+    const T* __restrict__ qs, int64_t sqb, int64_t sqh, int64_t sqn, const T* __restrict__ k,
+    int64_t skb, int64_t skh, int64_t sks, int64_t B, int64_t Hq, int64_t Hk,
+    int64_t Sk, int64_t D, int64_t qps, int64_t bk, int64_t group, int causal,
+    int64_t bsq, float gap_scalar, const float* __restrict__ gaps, RowLayout lay,
+    int32_t* __restrict__ counts, int32_t* __restrict__ indices, int64_t nrowsets) {
+  __shared__ double qd[kSelMaxD * kSelRows];          // [d][row]
+  __shared__ float sc[kSelRows * kSelChunk];          // [row][key]
+  __shared__ float mt[kSelRows * (kSelChunk / 16)];   // [row][tile] running max
+  __shared__ float m_run[kSelRows];
+  __shared__ int32_t cnt[kSelRows];
+
+  const int tid = threadIdx.x;
+  const int64_t BH = B * Hq;
+  const int64_t rs = nrowsets - 1 - int64_t(blockIdx.x) / BH;  // heavy rows first
+  const int64_t bh = int64_t(blockIdx.x) % BH;
+  const int64_t b = bh / Hq, h = bh % Hq;
+  const int64_t hk = h / (Hq / Hk);
+  const int64_t jr0 = rs * kSelRows;
+  const int64_t nc = lay.nc, J0 = lay.J0;
+  const int64_t rows_here = (nc - jr0 < kSelRows) ? (nc - jr0) : kSelRows;
+  const float gap = gaps ? gaps[bh] : gap_scalar;
+  const int64_t smin = lay.smin();
+  const int64_t gspan = bk * group;
+  const int ntile = int(kSelChunk / bk);
+
+  // Key range of this work-group: [kstart, kend).
+  const int64_t kstart = smin;
+  int64_t kend = Sk;
+  if (causal) {
+    const int64_t lim = (J0 + jr0 + rows_here - 1) * qps;  // keys < J*qps only
+    if (lim < kend) kend = lim;
+  }
+
+  // Stage the R pooled rows in fp64, transposed for broadcast reads.
+  for (int64_t e = tid; e < int64_t(kSelRows) * D; e += blockDim.x) {
+    const int64_t i = e / D, d = e % D;
+    double v = 0.0;
+    if (i < rows_here) v = double(to_f32(qs[b * sqb + h * sqh + (jr0 + i) * sqn + d]));
+    qd[d * kSelRows + i] = v;
+  }
+  if (tid < kSelRows) {
+    m_run[tid] = -__builtin_inff();
+    cnt[tid] = 0;
+  }
+  __syncthreads();
+
+  const T* kh = k + b * skb + hk * skh;
+  constexpr int VEC = int(16 / sizeof(T));
+  const bool vec_ok = (D % VEC == 0) && (reinterpret_cast<uintptr_t>(kh) % 16 == 0) &&
+                      (sks % VEC == 0);
+
+  for (int64_t kbase = kstart; kbase < kend; kbase += kSelChunk) {
+    // ---- Phase A: canonical scores for R rows x 256 keys -----------------
+    {
+      const int64_t key = kbase + tid;
+      double acc[kSelRows];
+#pragma unroll
+      for (int i = 0; i < kSelRows; ++i) acc[i] = 0.0;
+      if (key < kend) {
+        const T* kr = kh + key * sks;
+        if (vec_ok) {
+          for (int64_t d0 = 0; d0 < D; d0 += VEC) {
+            T v[VEC];
+            *reinterpret_cast<uint4*>(v) = *reinterpret_cast<const uint4*>(kr + d0);
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) {
+              const double kd = double(to_f32(v[e]));
+              const double* qrow = &qd[(d0 + e) * kSelRows];
+#pragma unroll
+              for (int i = 0; i < kSelRows; ++i) acc[i] = __builtin_fma(qrow[i], kd, acc[i]);
+            }
+          }
+        } else {
+          for (int64_t d = 0; d < D; ++d) {
+            const double kd = double(to_f32(kr[d]));
+            const double* qrow = &qd[d * kSelRows];
+#pragma unroll
+            for (int i = 0; i < kSelRows; ++i) acc[i] = __builtin_fma(qrow[i], kd, acc[i]);
+          }
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < kSelRows; ++i) sc[i * kSelChunk + tid] = float(acc[i]);
+    }
+    __syncthreads();
+
+    // ---- Phase B1: tile maxima over the valid keys of each tile ------------
+    if (tid < kSelRows * ntile) {
+      const int i = tid / ntile, tl = tid % ntile;
+      const int64_t koff = kbase + int64_t(tl) * bk;
+      float tmax = -__builtin_inff();
+      for (int64_t c = 0; c < bk; ++c) {
+        if (koff + c < kend) tmax = __builtin_fmaxf(tmax, sc[i * kSelChunk + tl * bk + c]);
+      }
+      mt[i * (kSelChunk / 16) + tl] = tmax;
+    }
+    __syncthreads();
+
+    // ---- Phase B2: running maximum, restarted at every group start ---------
+    if (tid < kSelRows) {
+      float m = m_run[tid];
+      for (int tl = 0; tl < ntile; ++tl) {
+        const int64_t koff = kbase + int64_t(tl) * bk;
+        if (koff >= kend) break;
+        if (koff % gspan == 0) m = -__builtin_inff();
+        m = __builtin_fmaxf(m, mt[tid * (kSelChunk / 16) + tl]);
+        mt[tid * (kSelChunk / 16) + tl] = m;
+      }
+      m_run[tid] = m;
+    }
+    __syncthreads();
+
+    // ---- Phase B3: decisions and ordered compaction, one wave per row ------
+    {
+      const int wave = tid / 64, lane = tid % 64;
+      for (int i = wave; i < rows_here; i += int(blockDim.x / 64)) {
+        const int64_t jr = jr0 + i;
+        const int64_t J = J0 + jr;
+        const int64_t qtile = jr / bsq;
+        const int64_t r = jr - qtile * bsq;
+        const int64_t off0 = (J0 + qtile * bsq) * qps;
+        const int64_t row_off = lay.row_offset(bh, jr);
+        const int64_t cap = lay.capacity(J);
+        int32_t c = cnt[i];
+        for (int step = 0; step < kSelChunk / 64; ++step) {
+          const int kk = step * 64 + lane;
+          const int64_t key = kbase + kk;
+          const int tl = int(kk / bk);
+          const int64_t koff = kbase + int64_t(tl) * bk;
+          bool sel = key < kend;
+          if (sel && causal) sel = r > (koff - off0) / qps;  // C++ '/' truncates
+          if (sel) sel = (sc[i * kSelChunk + kk] + gap) >= mt[i * (kSelChunk / 16) + tl];
+          const uint64_t ballot = __ballot(sel);
+          const uint32_t below = __builtin_amdgcn_mbcnt_hi(
+              uint32_t(ballot >> 32), __builtin_amdgcn_mbcnt_lo(uint32_t(ballot), 0u));
+          const int64_t pos = int64_t(c) + below;
+          if (sel && pos < cap) indices[row_off + pos] = int32_t(key);
+          c += __builtin_popcountll(ballot);
+        }
+        if (lane == 0) cnt[i] = c;
+      }
+    }
+    __syncthreads();
+  }
+
+  if (tid < rows_here) {
+    const int64_t cap = lay.capacity(J0 + jr0 + tid);
+    const int32_t c = cnt[tid];
+    counts[bh * nc + jr0 + tid] = (c < cap) ? c : int32_t(cap);
+  }
+}
+
+template <typename T>
+static hipError_t launch_select_exact_t(
+    const void* qs, int64_t sqb, int64_t sqh, int64_t sqn, const void* k, int64_t skb, int64_t skh,
+    int64_t sks, int64_t B, int64_t Hq, int64_t Hk, int64_t Sk, int64_t D,
+    int64_t qps, int64_t bk, int64_t group, int causal, int64_t bsq,
+    float gap_scalar, const float* gaps, const RowLayout& lay, int32_t* counts,
+    int32_t* indices, hipStream_t stream) {
+  const int64_t nrowsets = (lay.nc + kSelRows - 1) / kSelRows;
+  const int64_t nblocks = nrowsets * B * Hq;
+  hipLaunchKernelGGL((select_exact_kernel<T>), dim3(unsigned(nblocks)), dim3(kSelChunk), 0,
+                     stream, static_cast<const T*>(qs), sqb, sqh, sqn, static_cast<const T*>(k),
+                     skb, skh, sks, B, Hq, Hk, Sk, D, qps, bk, group, causal, bsq,
+                     gap_scalar, gaps, lay, counts, indices, nrowsets);
+  return hipGetLastError();
+}
+
+hipError_t launch_select_exact(int dtype, const void* qs, int64_t sqb, int64_t sqh,
+                               int64_t sqn, const void* k, int64_t skb, int64_t skh, int64_t sks,
+                               int64_t B, int64_t Hq, int64_t Hk, int64_t Sk, int64_t D,
+                               int64_t qps, int64_t bk, int64_t group, int causal,
+                               int64_t bsq, float gap_scalar, const float* gaps,
+                               const RowLayout& lay, int32_t* counts, int32_t* indices,
+                               hipStream_t stream) {
+  switch (dtype) {
+    case kF32:
+      return launch_select_exact_t<float>(qs, sqb, sqh, sqn, k, skb, skh, sks, B, Hq, Hk, Sk, D, qps, bk,
+                                          group, causal, bsq, gap_scalar, gaps, lay, counts,
+                                          indices, stream);
+    case kBF16:
+      return launch_select_exact_t<bf16_t>(qs, sqb, sqh, sqn, k, skb, skh, sks, B, Hq, Hk, Sk, D, qps,
+                                           bk, group, causal, bsq, gap_scalar, gaps, lay, counts,
+                                           indices, stream);
+    case kF16:
+      return launch_select_exact_t<f16_t>(qs, sqb, sqh, sqn, k, skb, skh, sks, B, Hq, Hk, Sk, D, qps, bk,
+                                          group, causal, bsq, gap_scalar, gaps, lay, counts,
+                                          indices, stream);
+  }
+  return hipErrorInvalidValue;
+}
+
+}  // namespace va
