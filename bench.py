@@ -64,7 +64,7 @@ def attn_flops(counts_per_chunk, wl, S, Sk):
         J = torch.arange(J0, J0 + nc)
         rows = torch.clamp(S - J * qps, max=qps).double()
         loc = torch.tensor([local_keys(int(j), qps, Sk, wl.causal) for j in J], dtype=torch.float64)
-        total += float((rows * (cnt.double() + loc)).sum())
+        total += float((rows * (cnt.detach().cpu().double() + loc)).sum())
     return 4.0 * D * total
 
 
