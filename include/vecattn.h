@@ -43,6 +43,7 @@ enum {
 };
 
 enum { VA_ATTN_AUTO = 0, VA_ATTN_MFMA = 1, VA_ATTN_SIMPLE = 2 };
+enum { VA_SEL_AUTO = 0, VA_SEL_EXACT = 1, VA_SEL_MFMA = 2 };
 
 /* Library version (major*10000 + minor*100 + patch). */
 int va_version(void);
@@ -79,16 +80,27 @@ int va_pool(int dtype, const void* q, int64_t B, int64_t H, int64_t S, int64_t D
  *   gaps   : device fp32 array of B*Hq gaps (per-head thresholds), or NULL
  *   bsq    : BLOCK_SIZE_Q of the reference launch (64 for the shipped VLM
  *            configs); it places the reference's causal first-row tile quirk
- * Output: see "index layout" above.  Scores use canonical arithmetic (a
- * sequential fp64 dot product rounded once to fp32), so the selected sets
- * match the CPU restatement of the rule bit for bit.
+ * Output: see "index layout" above.  Decisions follow canonical arithmetic
+ * (a sequential fp64 dot product rounded once to fp32), so the selected sets
+ * match the CPU restatement of the rule bit for bit, whichever kernel runs:
+ *   VA_SEL_EXACT : fp64 scores for every pair (any dtype, any k_local_size);
+ *   VA_SEL_MFMA  : bf16/fp16 MFMA scores with a certified error band and exact
+ *                  fp64 recomputation inside the band (D in {64,128},
+ *                  k_local_size in {16,32,64}); needs `scratch`;
+ *   VA_SEL_AUTO  : MFMA when supported and scratch is given, else exact.
+ * scratch: device fp32 buffer of va_select_scratch_floats(B, Hk) floats (key
+ * norms), or NULL.
  */
 int va_select(int dtype, const void* qs, int64_t sqb, int64_t sqh, int64_t sqn,
-              const void* k, int64_t skb, int64_t skh, int64_t sks, int64_t B, int64_t Hq, int64_t Hk, int64_t Sk,
-              int64_t D, int64_t q_pooling_size, int64_t k_local_size,
+              const void* k, int64_t skb, int64_t skh, int64_t sks, int64_t B, int64_t Hq,
+              int64_t Hk, int64_t Sk, int64_t D, int64_t q_pooling_size, int64_t k_local_size,
               int64_t group_k_block, int causal, int wo_init, int64_t J0, int64_t nc,
               int64_t bsq, float gap, const float* gaps, int64_t dense_stride,
-              int32_t* counts, int32_t* indices, void* stream);
+              int32_t* counts, int32_t* indices, int kernel, float* scratch,
+              int64_t scratch_floats, void* stream);
+
+/* fp32 scratch floats va_select's MFMA kernel needs (B*Hk key-norm slots). */
+int64_t va_select_scratch_floats(int64_t B, int64_t Hk);
 
 /* Total int32 slots of the index layout for B*Hq rows sets [J0, J0+nc). */
 int64_t va_select_index_capacity(int64_t B, int64_t Hq, int64_t Sk, int64_t q_pooling_size,

@@ -120,10 +120,14 @@ SELECT_CASES = [
 ]
 
 
+SEL_KERNELS = [nat.VA_SEL_EXACT, nat.VA_SEL_AUTO]
+
+
+@pytest.mark.parametrize("kernel", SEL_KERNELS, ids=["exact", "auto"])
 @pytest.mark.parametrize("case", SELECT_CASES, ids=[c[0] for c in SELECT_CASES])
-def test_select_bit_exact(device, case):
+def test_select_bit_exact(device, case, kernel):
     name, B, Hq, Hk, S, D, dtype, causal, qps, bk, G, keep, chunk_rows = case
-    note("select", name)
+    note("select", name, kernel)
     q, k, _ = make_inputs(B, Hq, Hk, S, D, dtype, seed=len(name))
     th = calibrated_threshold(keep, q, k, qps, bk, G, causal)
     gaps = orc.gap_from_threshold(th, B, Hq)
@@ -137,7 +141,7 @@ def test_select_bit_exact(device, case):
         nc = min(step, nqb - J0)
         want_c, want = orc.select(qs_cpu, k, J0, nc, gaps, qps, bk, G, causal, causal, 64)
         cnt, idx = stages.select_rows(qs[:, :, J0:J0 + nc], kd, J0, float(gaps[0]), None, causal,
-                                      qps, bk, G, causal)
+                                      qps, bk, G, causal, kernel=kernel)
         got_c, got = gpu_lists(cnt, idx, B, Hq, J0, nc, qps, S, causal, causal)
         assert np.array_equal(got_c, want_c)
         assert_lists_equal(got, want, name)
@@ -170,7 +174,37 @@ def test_select_per_head_gaps_and_dense_layout(device):
                 assert np.all(idx[b, h, J, c:] == 0)
 
 
-def test_select_ties_from_duplicate_keys(device):
+MFMA_STRESS = [
+    # name, Hq, Hk, S, D, causal, bk, G, gap   (gap 0: every running maximum is in the band)
+    ("causal-G16-gap0", 4, 1, 2048, 128, True, 16, 16, 0.0),
+    ("noncausal-G8192-gap0", 2, 2, 3000, 128, False, 16, 8192, 0.0),
+    ("noncausal-G8192-bk32", 2, 1, 2500, 128, False, 32, 8192, 0.12),
+    ("noncausal-G3-bk64-gap0", 2, 2, 1500, 64, False, 64, 3, 0.0),
+    ("causal-G5-bk16", 2, 2, 2048, 64, True, 16, 5, 0.05),
+]
+
+
+@pytest.mark.parametrize("case", MFMA_STRESS, ids=[c[0] for c in MFMA_STRESS])
+def test_select_mfma_exact_fallback(device, case):
+    # Exact ties at gap 0 and groups straddling chunks drive the certified
+    # kernel through its exact paths (ambiguous pairs, carried maxima).
+    name, Hq, Hk, S, D, causal, bk, G, gap = case
+    note("select mfma stress", name)
+    q, k, _ = make_inputs(1, Hq, Hk, S, D, torch.bfloat16, seed=S + bk)
+    _, qs_cpu = orc.pool(q, 64, "bfloat16")
+    nqb = qs_cpu.shape[2]
+    gaps = np.full(Hq, gap, np.float32)
+    want_c, want = orc.select(qs_cpu, k, 0, nqb, gaps, 64, bk, G, causal, causal, 64)
+    qs, _ = stages.pool_scaled(q.to(device), 64)
+    cnt, idx = stages.select_rows(qs, k.to(device), 0, gap, None, causal, 64, bk, G, causal,
+                                  kernel=nat.VA_SEL_MFMA)
+    got_c, got = gpu_lists(cnt, idx, 1, Hq, 0, nqb, 64, S, causal, causal)
+    assert np.array_equal(got_c, want_c)
+    assert_lists_equal(got, want, name)
+
+
+@pytest.mark.parametrize("kernel", SEL_KERNELS, ids=["exact", "auto"])
+def test_select_ties_from_duplicate_keys(device, kernel):
     # Repeated key rows give exactly equal scores: selection at equality.
     note("select ties")
     q, k, _ = make_inputs(1, 2, 1, 1024, 64, torch.bfloat16, seed=5)
@@ -180,7 +214,8 @@ def test_select_ties_from_duplicate_keys(device):
     for gap in (0.0, 0.05, 0.3):
         gaps = np.full(2, gap, np.float32)
         want_c, want = orc.select(qs_cpu, k, 0, 16, gaps, 64, 16, 2, False, False, 64)
-        cnt, idx = stages.select_rows(qs, k.to(device), 0, gap, None, False, 64, 16, 2, False)
+        cnt, idx = stages.select_rows(qs, k.to(device), 0, gap, None, False, 64, 16, 2, False,
+                                      kernel=kernel)
         got_c, got = gpu_lists(cnt, idx, 1, 2, 0, 16, 64, 1024, False, False)
         assert np.array_equal(got_c, want_c)
         assert_lists_equal(got, want, f"ties gap={gap}")
@@ -350,3 +385,25 @@ def test_full_size_chunking_invariant(config_b):
     a = VecAttention_prefill(qd, kd, vd, 0.35, 64, 16, 16, True, 32768)
     b = VecAttention_prefill(qd, kd, vd, 0.35, 64, 16, 16, True, 16384)
     assert torch.equal(a, b)
+
+
+def test_full_size_mfma_selection_equals_exact_kernel(config_b):
+    # Every row of the 32K config: the certified MFMA kernel and the fp64 kernel
+    # (two independent implementations of the canonical rule) agree bit for bit.
+    note("full-size mfma == exact")
+    _, _, _, qd, kd, vd = config_b
+    qs, _ = stages.pool_scaled(qd, 64)
+    gap = -math.log(0.75 + 1e-9)
+    c1, i1 = stages.select_rows(qs, kd, 0, gap, None, True, 64, 16, 16, True,
+                                kernel=nat.VA_SEL_EXACT)
+    c2, i2 = stages.select_rows(qs, kd, 0, gap, None, True, 64, 16, 16, True,
+                                kernel=nat.VA_SEL_MFMA)
+    assert torch.equal(c1, c2)
+    # compare only the written slots of every row
+    lay_c = c1.cpu().numpy().reshape(-1)
+    a, b = i1.cpu().numpy(), i2.cpu().numpy()
+    for bh in range(28):
+        for J in range(512):
+            o = stages.row_offset(32768, 64, True, True, 0, 512, bh, J)
+            n = lay_c[bh * 512 + J]
+            assert np.array_equal(a[o:o + n], b[o:o + n]), (bh, J)

@@ -67,9 +67,10 @@ def test_index_layout_matches_capacities(L, causal, wo_init):
 
 
 def _null_select(L, **over):
-    args = dict(dtype=nat.VA_BF16, qs=1, sqb=0, sqh=0, sqn=0, k=1, skb=0, skh=0, sks=128, B=1, Hq=4,
+    args = dict(dtype=nat.VA_BF16, qs=256, sqb=0, sqh=0, sqn=0, k=256, skb=0, skh=0, sks=128, B=1, Hq=4,
                 Hk=2, Sk=1024, D=128, qps=64, bk=16, G=16, causal=1, wo_init=1, J0=0, nc=16, bsq=64,
-                gap=0.2, gaps=None, dense=0, counts=1, indices=1, stream=None)
+                gap=0.2, gaps=None, dense=0, counts=1, indices=1, kernel=0, scratch=None,
+                scratch_floats=0, stream=None)
     args.update(over)
     return L.va_select(*args.values())
 
@@ -83,6 +84,9 @@ def test_select_argument_errors_before_launch(L):
     assert _null_select(L, dtype=7) == nat.VA_ERR_ARG
     assert _null_select(L, counts=None) == nat.VA_ERR_ARG
     assert _null_select(L, D=512) == nat.VA_ERR_UNSUPPORTED
+    assert _null_select(L, kernel=nat.VA_SEL_MFMA) == nat.VA_ERR_ARG            # no scratch
+    assert _null_select(L, kernel=nat.VA_SEL_MFMA, dtype=nat.VA_F32) == nat.VA_ERR_UNSUPPORTED
+    assert _null_select(L, kernel=9) == nat.VA_ERR_ARG
 
 
 def test_prefill_argument_errors_before_launch(L):

@@ -16,6 +16,7 @@ LIB_PATH = os.path.join(_HERE, "libvecattn.so")
 VA_F32, VA_BF16, VA_F16 = 0, 1, 2
 VA_OK, VA_ERR_ARG, VA_ERR_UNSUPPORTED, VA_ERR_HIP, VA_ERR_WORKSPACE = 0, -1, -2, -3, -4
 VA_ATTN_AUTO, VA_ATTN_MFMA, VA_ATTN_SIMPLE = 0, 1, 2
+VA_SEL_AUTO, VA_SEL_EXACT, VA_SEL_MFMA = 0, 1, 2
 
 _DTYPES = {torch.float32: VA_F32, torch.bfloat16: VA_BF16, torch.float16: VA_F16}
 
@@ -33,9 +34,10 @@ SIGNATURES = {
     "va_last_error": (ctypes.c_char_p, []),
     "va_device_count": (_int, []),
     "va_pool": (_int, [_int, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp]),
-    "va_select": (_int, [_int, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
-                         _i64, _i64, _i64, _int, _int, _i64, _i64, _i64, _f32, _vp, _i64, _vp,
-                         _vp, _vp]),
+    "va_select": (_int, [_int, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _i64, _i64, _i64,
+                         _i64, _i64, _i64, _i64, _i64, _int, _int, _i64, _i64, _i64, _f32, _vp,
+                         _i64, _vp, _vp, _int, _vp, _i64, _vp]),
+    "va_select_scratch_floats": (_i64, [_i64, _i64]),
     "va_select_index_capacity": (_i64, [_i64, _i64, _i64, _i64, _int, _int, _i64, _i64, _i64]),
     "va_select_row_offset": (_i64, [_i64, _i64, _int, _int, _i64, _i64, _i64, _i64, _i64]),
     "va_sparse_attn": (_int, [_int, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _vp, _i64, _i64,

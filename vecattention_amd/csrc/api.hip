@@ -26,6 +26,17 @@ hipError_t launch_attn_simple(int dtype, const void* q, const int64_t* sq, const
                               const int32_t* counts, const int32_t* indices,
                               const RowLayout& lay, hipStream_t stream);
 bool attn_mfma_supported(int dtype, int64_t D, int64_t qps);
+bool select_mfma_supported(int dtype, int64_t D, int64_t bk);
+hipError_t launch_select_mfma(int dtype, const void* qs, int64_t sqb, int64_t sqh, int64_t sqn,
+                              const void* k, int64_t skb, int64_t skh, int64_t sks, int64_t B,
+                              int64_t Hq, int64_t Hk, int64_t Sk, int64_t D, int64_t qps,
+                              int64_t bk, int64_t group, int causal, int64_t bsq, float gap,
+                              const float* gaps, const float* kmax, const RowLayout& lay,
+                              int32_t* counts, int32_t* indices, hipStream_t stream);
+int64_t key_norm_scratch_floats(int64_t B, int64_t Hk);
+hipError_t launch_key_norm(int dtype, const void* k, int64_t skb, int64_t skh, int64_t sks,
+                           int64_t B, int64_t Hk, int64_t Sk, int64_t D, float* scratch,
+                           hipStream_t stream);
 hipError_t launch_attn_mfma(int dtype, int64_t D, int64_t qps, const void* q, const int64_t* sq,
                             const void* k, const int64_t* sk, const void* v, const int64_t* sv,
                             void* out, const int64_t* so, int64_t B, int64_t Hq, int64_t Hk,
@@ -147,12 +158,45 @@ int64_t va_select_row_offset(int64_t Sk, int64_t qps, int causal, int wo_init, i
   return make_layout(J0, nc, qps, Sk, causal, wo_init, dense_stride).row_offset(bh, jr);
 }
 
+int64_t va_select_scratch_floats(int64_t B, int64_t Hk) {
+  if (B <= 0 || Hk <= 0) return -1;
+  return va::key_norm_scratch_floats(B, Hk);
+}
+
+// Selection with the key norms (MFMA path) already in scratch[0 .. B*Hk).
+static int select_impl(int dtype, const void* qs, int64_t sqb, int64_t sqh, int64_t sqn,
+                       const void* k, int64_t skb, int64_t skh, int64_t sks, int64_t B,
+                       int64_t Hq, int64_t Hk, int64_t Sk, int64_t D, int64_t qps, int64_t bk,
+                       int64_t group, int causal, int wo_init, int64_t J0, int64_t nc,
+                       int64_t bsq, float gap, const float* gaps, int64_t dense_stride,
+                       int32_t* counts, int32_t* indices, bool use_mfma, const float* kmax,
+                       hipStream_t stream) {
+  const va::RowLayout lay = make_layout(J0, nc, qps, Sk, causal, wo_init, dense_stride);
+  hipError_t e =
+      use_mfma ? va::launch_select_mfma(dtype, qs, sqb, sqh, sqn, k, skb, skh, sks, B, Hq, Hk, Sk,
+                                        D, qps, bk, group, causal, bsq, gap, gaps, kmax, lay,
+                                        counts, indices, stream)
+               : va::launch_select_exact(dtype, qs, sqb, sqh, sqn, k, skb, skh, sks, B, Hq, Hk,
+                                         Sk, D, qps, bk, group, causal, bsq, gap, gaps, lay,
+                                         counts, indices, stream);
+  return hip_check(e, "select launch");
+}
+
+static bool select_mfma_ok(int dtype, const void* qs, int64_t sqb, int64_t sqh, int64_t sqn,
+                           const void* k, int64_t skb, int64_t skh, int64_t sks, int64_t D,
+                           int64_t bk) {
+  const int64_t a = 16 / esize(dtype);
+  return va::select_mfma_supported(dtype, D, bk) && reinterpret_cast<uintptr_t>(qs) % 16 == 0 &&
+         reinterpret_cast<uintptr_t>(k) % 16 == 0 && sqb % a == 0 && sqh % a == 0 &&
+         sqn % a == 0 && skb % a == 0 && skh % a == 0 && sks % a == 0;
+}
+
 int va_select(int dtype, const void* qs, int64_t sqb, int64_t sqh, int64_t sqn,
-              const void* k, int64_t skb,
-              int64_t skh, int64_t sks, int64_t B, int64_t Hq, int64_t Hk, int64_t Sk, int64_t D,
-              int64_t qps, int64_t bk, int64_t group, int causal, int wo_init, int64_t J0,
-              int64_t nc, int64_t bsq, float gap, const float* gaps, int64_t dense_stride,
-              int32_t* counts, int32_t* indices, void* stream) {
+              const void* k, int64_t skb, int64_t skh, int64_t sks, int64_t B, int64_t Hq,
+              int64_t Hk, int64_t Sk, int64_t D, int64_t qps, int64_t bk, int64_t group,
+              int causal, int wo_init, int64_t J0, int64_t nc, int64_t bsq, float gap,
+              const float* gaps, int64_t dense_stride, int32_t* counts, int32_t* indices,
+              int kernel, float* scratch, int64_t scratch_floats, void* stream) {
   int rc = check_select_args(dtype, qs, k, B, Hq, Hk, Sk, D, qps, bk, group, causal, wo_init, J0,
                              nc, bsq);
   if (rc) return rc;
@@ -160,11 +204,33 @@ int va_select(int dtype, const void* qs, int64_t sqb, int64_t sqh, int64_t sqn,
   if (dense_stride < 0) return fail(VA_ERR_ARG, "negative dense_stride");
   if (dense_stride > 0 && dense_stride < Sk)
     return fail(VA_ERR_ARG, "dense_stride %lld < Sk %lld", (long long)dense_stride, (long long)Sk);
-  const va::RowLayout lay = make_layout(J0, nc, qps, Sk, causal, wo_init, dense_stride);
-  rc = hip_check(va::launch_select_exact(dtype, qs, sqb, sqh, sqn, k, skb, skh, sks, B, Hq, Hk, Sk, D,
-                                         qps, bk, group, causal, bsq, gap, gaps, lay, counts,
-                                         indices, static_cast<hipStream_t>(stream)),
-                 "select launch");
+  const bool have_scratch = scratch != nullptr &&
+                            scratch_floats >= va::key_norm_scratch_floats(B, Hk);
+  const bool mfma_ok = select_mfma_ok(dtype, qs, sqb, sqh, sqn, k, skb, skh, sks, D, bk);
+  bool use_mfma;
+  if (kernel == VA_SEL_EXACT) {
+    use_mfma = false;
+  } else if (kernel == VA_SEL_MFMA) {
+    if (!mfma_ok)
+      return fail(VA_ERR_UNSUPPORTED,
+                  "MFMA selection needs bf16/fp16, D in {64,128}, k_local_size in {16,32,64} "
+                  "and 16-byte aligned rows");
+    if (!have_scratch) return fail(VA_ERR_ARG, "MFMA selection needs scratch");
+    use_mfma = true;
+  } else if (kernel == VA_SEL_AUTO) {
+    use_mfma = mfma_ok && have_scratch;
+  } else {
+    return fail(VA_ERR_ARG, "unknown selection kernel %d", kernel);
+  }
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (use_mfma) {
+    rc = hip_check(va::launch_key_norm(dtype, k, skb, skh, sks, B, Hk, Sk, D, scratch, st),
+                   "key norm launch");
+    if (rc) return rc;
+  }
+  rc = select_impl(dtype, qs, sqb, sqh, sqn, k, skb, skh, sks, B, Hq, Hk, Sk, D, qps, bk, group,
+                   causal, wo_init, J0, nc, bsq, gap, gaps, dense_stride, counts, indices, use_mfma,
+                   scratch, st);
   return rc ? rc : ok();
 }
 
@@ -236,7 +302,8 @@ int va_sparse_attn(int dtype, const void* q, int64_t sqb, int64_t sqh, int64_t s
 // Workspace of va_prefill: [scaled pooled q][counts][indices], 256-byte aligned.
 static void prefill_segments(int dtype, int64_t B, int64_t Hq, int64_t Sq, int64_t Sk, int64_t D,
                              int64_t qps, int causal, int64_t chunk, int64_t* qs_bytes,
-                             int64_t* cnt_bytes, int64_t* idx_bytes) {
+                             int64_t* cnt_bytes, int64_t* idx_bytes, int64_t* kn_bytes) {
+  *kn_bytes = align256(va::key_norm_scratch_floats(B, Hq) * 4);  // Hk <= Hq
   const int64_t nqb = cdiv(Sq, qps);
   *qs_bytes = align256(B * Hq * nqb * D * esize(dtype));
   const int64_t nc_max = cdiv(chunk < Sq ? chunk : Sq, qps);
@@ -257,9 +324,9 @@ int64_t va_prefill_workspace_size(int dtype, int64_t B, int64_t Hq, int64_t Sq, 
   if (!dtype_ok(dtype) || B <= 0 || Hq <= 0 || Sq <= 0 || Sk <= 0 || D <= 0 || qps <= 0 ||
       chunk_size <= 0 || chunk_size % qps)
     return -1;
-  int64_t a, b, c;
-  prefill_segments(dtype, B, Hq, Sq, Sk, D, qps, causal, chunk_size, &a, &b, &c);
-  return a + b + c;
+  int64_t a, b, c, d;
+  prefill_segments(dtype, B, Hq, Sq, Sk, D, qps, causal, chunk_size, &a, &b, &c, &d);
+  return a + b + c + d;
 }
 
 int va_prefill(int dtype, const void* q, int64_t sqb, int64_t sqh, int64_t sqs, const void* k,
@@ -280,26 +347,36 @@ int va_prefill(int dtype, const void* q, int64_t sqb, int64_t sqh, int64_t sqs, 
     return fail(VA_ERR_WORKSPACE, "workspace %lld bytes < required %lld",
                 (long long)workspace_bytes, (long long)need);
   const int64_t nqb = cdiv(Sq, qps);
-  int64_t qs_bytes, cnt_bytes, idx_bytes;
+  int64_t qs_bytes, cnt_bytes, idx_bytes, kn_bytes;
   prefill_segments(dtype, B, Hq, Sq, Sk, D, qps, causal, chunk_size, &qs_bytes, &cnt_bytes,
-                   &idx_bytes);
+                   &idx_bytes, &kn_bytes);
   char* ws = static_cast<char*>(workspace);
   void* qs = ws;
   int32_t* counts = reinterpret_cast<int32_t*>(ws + qs_bytes);
   int32_t* indices = reinterpret_cast<int32_t*>(ws + qs_bytes + cnt_bytes);
+  float* knorm = reinterpret_cast<float*>(ws + qs_bytes + cnt_bytes + idx_bytes);
   hipStream_t st = static_cast<hipStream_t>(stream);
 
   int rc = va_pool(dtype, q, B, Hq, Sq, D, sqb, sqh, sqs, qps, nullptr, qs, stream);
   if (rc) return rc;
+  rc = check_select_args(dtype, qs, k, B, Hq, Hk, Sk, D, qps, bk, group, causal, causal, 0,
+                         cdiv(Sq, qps), bsq);
+  if (rc) return rc;
+  const bool use_mfma = select_mfma_ok(dtype, qs, Hq * nqb * D, nqb * D, D, k, skb, skh, sks, D, bk);
+  if (use_mfma) {
+    rc = hip_check(va::launch_key_norm(dtype, k, skb, skh, sks, B, Hk, Sk, D, knorm, st),
+                   "key norm launch");
+    if (rc) return rc;
+  }
   const float scale = float(1.0 / std::sqrt(double(D)));
   for (int64_t i = 0; i < Sq; i += chunk_size) {
     const int64_t rows = (Sq - i < chunk_size) ? (Sq - i) : chunk_size;
     const int64_t J0 = i / qps, nc = cdiv(rows, qps);
     const int64_t es = esize(dtype);
     const void* qs_chunk = static_cast<const char*>(qs) + J0 * D * es;
-    rc = va_select(dtype, qs_chunk, Hq * nqb * D, nqb * D, D, k, skb, skh, sks, B, Hq, Hk, Sk, D,
-                   qps, bk, group, causal,
-                   causal, J0, nc, bsq, gap, gaps, 0, counts, indices, stream);
+    rc = select_impl(dtype, qs_chunk, Hq * nqb * D, nqb * D, D, k, skb, skh, sks, B, Hq, Hk, Sk,
+                     D, qps, bk, group, causal, causal, J0, nc, bsq, gap, gaps, 0, counts, indices,
+                     use_mfma, knorm, st);
     if (rc) return rc;
     rc = va_sparse_attn(dtype, q, sqb, sqh, sqs, k, skb, skh, sks, v, svb, svh, svs, out, sob,
                         soh, sos, B, Hq, Hk, Sq, Sk, D, qps, causal, causal, J0, nc, 0, counts,

@@ -67,11 +67,13 @@ def row_offset(Sk, qps, causal, wo_init, J0, nc, bh, jr, dense_stride=0):
 
 
 def select_rows(qs_chunk, k, J0, gap, gaps, causal, q_pooling_size, k_local_size, group_k_block,
-                wo_init, bsq=None, dense_stride=0, indices=None, counts=None):
+                wo_init, bsq=None, dense_stride=0, indices=None, counts=None,
+                kernel=nat.VA_SEL_AUTO):
     """TilingSelect for the pooled rows of one chunk.
 
     qs_chunk: (B, Hq, nc, D) scaled pooled rows J0 .. J0+nc-1 (any strides,
-    features contiguous); k: (B, Hk, Sk, D).
+    features contiguous); k: (B, Hk, Sk, D).  `kernel`: VA_SEL_AUTO (MFMA when
+    supported), VA_SEL_EXACT or VA_SEL_MFMA.
     Returns (counts (B, Hq, nc) int32, indices int32 in the index layout).
     """
     if qs_chunk.stride(-1) != 1:
@@ -87,12 +89,15 @@ def select_rows(qs_chunk, k, J0, gap, gaps, causal, q_pooling_size, k_local_size
         counts = torch.empty(B, Hq, nc, dtype=torch.int32, device=k.device)
     if indices is None:
         indices = torch.empty(max(cap, 1), dtype=torch.int32, device=k.device)
+    nscr = int(nat.lib().va_select_scratch_floats(B, Hk))
+    scratch = torch.empty(max(nscr, 1), dtype=torch.float32, device=k.device)
     with torch.cuda.device(k.device):
         rc = nat.lib().va_select(
             nat.dtype_code(k), nat.ptr(qs_chunk), qs_chunk.stride(0), qs_chunk.stride(1),
             qs_chunk.stride(2), nat.ptr(k), k.stride(0), k.stride(1), k.stride(2), B, Hq, Hk, Sk, D,
             q_pooling_size, k_local_size, group_k_block, int(causal), int(wo_init), J0, nc, bsq,
-            float(gap), nat.ptr(gaps), dense_stride, nat.ptr(counts), nat.ptr(indices), _stream(k))
+            float(gap), nat.ptr(gaps), dense_stride, nat.ptr(counts), nat.ptr(indices), int(kernel),
+            nat.ptr(scratch), nscr, _stream(k))
     nat.check("va_select", rc)
     return counts, indices
 
