@@ -172,6 +172,8 @@ static int select_impl(int dtype, const void* qs, int64_t sqb, int64_t sqh, int6
                        int32_t* counts, int32_t* indices, bool use_mfma, const float* kmax,
                        hipStream_t stream) {
   const va::RowLayout lay = make_layout(J0, nc, qps, Sk, causal, wo_init, dense_stride);
+  // A group longer than the key range is one group; cap it so bk * group fits.
+  if (group > cdiv(Sk, bk) + 1) group = cdiv(Sk, bk) + 1;
   hipError_t e =
       use_mfma ? va::launch_select_mfma(dtype, qs, sqb, sqh, sqn, k, skb, skh, sks, B, Hq, Hk, Sk,
                                         D, qps, bk, group, causal, bsq, gap, gaps, kmax, lay,

@@ -31,7 +31,7 @@ __device__ inline int perm_key(int kk) {
 }
 
 template <typename T, int D, int QPS>
-__global__ __launch_bounds__(QPS * 2) void attn_mfma_kernel(
+__global__ __launch_bounds__(QPS * 2, 2) void attn_mfma_kernel(
     const T* __restrict__ q, int64_t sqb, int64_t sqh, int64_t sqs,
     const T* __restrict__ k, int64_t skb, int64_t skh, int64_t sks,
     const T* __restrict__ v, int64_t svb, int64_t svh, int64_t svs,
@@ -52,7 +52,7 @@ __global__ __launch_bounds__(QPS * 2) void attn_mfma_kernel(
 
   __shared__ __attribute__((aligned(16))) uint16_t Ks[kTileKeys * KS];
   __shared__ __attribute__((aligned(16))) uint16_t Vt[D * VS];
-  __shared__ int32_t kid[kTileKeys];
+  __shared__ int32_t kid[2][kTileKeys];  // key ids of tiles t (slot t & 1)
 
   const int tid = threadIdx.x;
   const int wave = tid / 64, lane = tid % 64;
@@ -110,13 +110,13 @@ __global__ __launch_bounds__(QPS * 2) void attn_mfma_kernel(
   uint4 kbuf[KLOADS];
   uint4 vbuf[VUNITS][4];
 
-  auto load_tile = [&]() {
+  auto load_tile = [&](const int32_t* ids) {
 #pragma unroll
     for (int x = 0; x < KLOADS; ++x) {
       const int c = tid + NT * x;
       if (KTOTAL % NT != 0 && c >= KTOTAL) break;
       const int kk = c / DCH, dc = c % DCH;
-      const int64_t key = kid[kk];
+      const int64_t key = ids[kk];
       kbuf[x] = key >= 0 ? *reinterpret_cast<const uint4*>(kh + key * sks + dc * 8)
                          : make_uint4(0, 0, 0, 0);
     }
@@ -127,7 +127,7 @@ __global__ __launch_bounds__(QPS * 2) void attn_mfma_kernel(
       const int kq = u % (kTileKeys / 4), dc = u / (kTileKeys / 4);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int64_t key = kid[4 * kq + i];
+        const int64_t key = ids[4 * kq + i];
         vbuf[x][i] = key >= 0 ? *reinterpret_cast<const uint4*>(vh + key * svs + dc * 8)
                               : make_uint4(0, 0, 0, 0);
       }
@@ -160,9 +160,6 @@ __global__ __launch_bounds__(QPS * 2) void attn_mfma_kernel(
       }
     }
   };
-  auto stage_ids = [&](int64_t t) {
-    if (tid < kTileKeys) kid[tid] = int32_t(tile_key(t, tid));
-  };
 
   f32x16_t o[D / 32];
 #pragma unroll
@@ -171,21 +168,24 @@ __global__ __launch_bounds__(QPS * 2) void attn_mfma_kernel(
     for (int e = 0; e < 16; ++e) o[i][e] = 0.f;
   float m_run = -__builtin_inff(), l_run = 0.f;
 
+  // Key ids run two tiles ahead of the K/V gathers: the id of tile t+2 is
+  // read from the index list one iteration before it is needed.
+  int32_t nid = -1;
   if (ntiles > 0) {
-    stage_ids(0);
-    __syncthreads();
-    load_tile();
+    if (tid < kTileKeys) {
+      kid[0][tid] = int32_t(tile_key(0, tid));
+      kid[1][tid] = ntiles > 1 ? int32_t(tile_key(1, tid)) : -1;
+      nid = ntiles > 2 ? int32_t(tile_key(2, tid)) : -1;
+    }
+    lds_barrier();
+    load_tile(kid[0]);
     store_tile();
-    __syncthreads();
+    lds_barrier();
   }
 
   for (int64_t t = 0; t < ntiles; ++t) {
     const bool more = (t + 1) < ntiles;
-    if (more) {
-      stage_ids(t + 1);
-      __syncthreads();
-      load_tile();  // in flight while this tile computes
-    }
+    if (more) load_tile(kid[(t + 1) & 1]);  // in flight while this tile computes
 
     // ---- S^T = K Q^T for the two 32-key halves -----------------------------
     f32x16_t s[2];
@@ -202,31 +202,45 @@ __global__ __launch_bounds__(QPS * 2) void attn_mfma_kernel(
     }
 
     // ---- masking: empty slots, causal diagonal ------------------------------
-    int64_t lim;      // valid slots in this tile
-    int64_t dshift;   // for diagonal tiles: key - diag0 = dshift + slot
+    int lim;      // valid slots in this tile
+    int dshift;   // for diagonal tiles: key - diag0 = dshift + slot
     bool diag = false;
     if (t < t_init) {
-      lim = kl.n_init - t * kTileKeys;
+      const int64_t l = kl.n_init - t * kTileKeys;
+      lim = l > kTileKeys ? kTileKeys : int(l);
       dshift = 0;
     } else if (t < t_init + t_diag) {
-      dshift = (t - t_init) * kTileKeys;
-      lim = kl.n_diag - dshift;
+      dshift = int(t - t_init) * kTileKeys;
+      const int64_t l = kl.n_diag - dshift;
+      lim = l > kTileKeys ? kTileKeys : int(l);
       diag = causal != 0;
     } else {
-      lim = kl.n_col - (t - t_init - t_diag) * kTileKeys;
+      const int64_t l = kl.n_col - (t - t_init - t_diag) * kTileKeys;
+      lim = l > kTileKeys ? kTileKeys : int(l);
       dshift = 0;
     }
     float tmax = -__builtin_inff();
+    if (!diag && lim == kTileKeys) {  // full tile, nothing masked
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
+      for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int slot = kb * 32 + 8 * (e / 4) + 4 * hh + (e % 4);
-        bool ok = slot < lim;
-        if (diag) ok = ok && (dshift + slot <= qrow_local);
-        const float x = ok ? s[kb][e] * scale_log2 : -__builtin_inff();
-        s[kb][e] = x;
-        tmax = __builtin_fmaxf(tmax, x);
+        for (int e = 0; e < 16; ++e) {
+          const float x = s[kb][e] * scale_log2;
+          s[kb][e] = x;
+          tmax = __builtin_fmaxf(tmax, x);
+        }
+    } else {
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int slot = kb * 32 + 8 * (e / 4) + 4 * hh + (e % 4);
+          bool ok = slot < lim;
+          if (diag) ok = ok && (dshift + slot <= qrow_local);
+          const float x = ok ? s[kb][e] * scale_log2 : -__builtin_inff();
+          s[kb][e] = x;
+          tmax = __builtin_fmaxf(tmax, x);
+        }
       }
     }
     tmax = __builtin_fmaxf(tmax, __shfl_xor(tmax, 32));
@@ -246,10 +260,12 @@ __global__ __launch_bounds__(QPS * 2) void attn_mfma_kernel(
     lsum += __shfl_xor(lsum, 32);
     l_run = l_run * alpha + lsum;
     m_run = m_new;
+    if (__ballot(alpha != 1.f)) {  // some row's maximum moved
 #pragma unroll
-    for (int i = 0; i < D / 32; ++i)
+      for (int i = 0; i < D / 32; ++i)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) o[i][e] *= alpha;
+        for (int e = 0; e < 16; ++e) o[i][e] *= alpha;
+    }
 
     // ---- O^T += V^T P^T ------------------------------------------------------
 #pragma unroll
@@ -270,9 +286,13 @@ __global__ __launch_bounds__(QPS * 2) void attn_mfma_kernel(
       }
     }
 
-    __syncthreads();
+    __syncthreads();  // K/V of tile t+1 have arrived; Ks/Vt of tile t are free
+    if (tid < kTileKeys) {
+      kid[t & 1][tid] = nid;  // ids of tile t+2 (slot t & 1 was consumed by load_tile(t))
+      nid = (t + 3 < ntiles) ? int32_t(tile_key(t + 3, tid)) : -1;
+    }
     if (more) store_tile();
-    __syncthreads();
+    lds_barrier();
   }
 
   // ---- epilogue: O / l, four consecutive features per store ----------------

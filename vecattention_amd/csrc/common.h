@@ -55,6 +55,14 @@ template <> struct Round<f16_t> {
   __device__ static f16_t store(float x) { return f16_t{rne_f16_bits(x)}; }
 };
 
+// Work-group barrier for LDS traffic only.  __syncthreads() also orders global
+// memory, which makes every wave wait for all of its outstanding global loads
+// and stores (prefetches included); this barrier waits for LDS operations only,
+// so prefetched global loads stay in flight across it.
+__device__ inline void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 // ---------------------------------------------------------------------------
 // Per-row index lists of the selection ("capacity layout").
 //

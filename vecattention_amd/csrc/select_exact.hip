@@ -40,6 +40,7 @@ __global__ __launch_bounds__(256) void select_exact_kernel(
   __shared__ float mt[kSelRows * (kSelChunk / 16)];   // [row][tile] running max
   __shared__ float m_run[kSelRows];
   __shared__ int32_t cnt[kSelRows];
+  __shared__ int64_t klim[kSelRows];  // causal: keys < klim are allowed
 
   const int tid = threadIdx.x;
   const int64_t BH = B * Hq;
@@ -54,6 +55,7 @@ __global__ __launch_bounds__(256) void select_exact_kernel(
   const int64_t smin = lay.smin();
   const int64_t gspan = bk * group;
   const int ntile = int(kSelChunk / bk);
+  const int lbk = __builtin_ctzll(uint64_t(bk));  // bk is a power of two
 
   // Key range of this work-group: [kstart, kend).
   const int64_t kstart = smin;
@@ -73,6 +75,13 @@ __global__ __launch_bounds__(256) void select_exact_kernel(
   if (tid < kSelRows) {
     m_run[tid] = -__builtin_inff();
     cnt[tid] = 0;
+    // The reference's causal tile test r > trunc((k_off - off0) / qps), with r
+    // the row inside its BLOCK_SIZE_Q program and off0 = (J - r) * qps, is
+    // k_off < J*qps for r >= 1 and k_off <= (J-1)*qps for r == 0.
+    const int64_t jr = jr0 + tid;
+    const int64_t r = jr % bsq;
+    const int64_t J = J0 + jr;
+    klim[tid] = causal ? ((r == 0) ? (J - 1) * qps + 1 : J * qps) : INT64_MAX;
   }
   __syncthreads();
 
@@ -131,10 +140,14 @@ __global__ __launch_bounds__(256) void select_exact_kernel(
     // ---- Phase B2: running maximum, restarted at every group start ---------
     if (tid < kSelRows) {
       float m = m_run[tid];
+      int64_t next_g = kbase + (gspan - kbase % gspan) % gspan;  // first group start >= kbase
       for (int tl = 0; tl < ntile; ++tl) {
         const int64_t koff = kbase + int64_t(tl) * bk;
         if (koff >= kend) break;
-        if (koff % gspan == 0) m = -__builtin_inff();
+        if (koff == next_g) {
+          m = -__builtin_inff();
+          next_g += gspan;
+        }
         m = __builtin_fmaxf(m, mt[tid * (kSelChunk / 16) + tl]);
         mt[tid * (kSelChunk / 16) + tl] = m;
       }
@@ -148,19 +161,16 @@ __global__ __launch_bounds__(256) void select_exact_kernel(
       for (int i = wave; i < rows_here; i += int(blockDim.x / 64)) {
         const int64_t jr = jr0 + i;
         const int64_t J = J0 + jr;
-        const int64_t qtile = jr / bsq;
-        const int64_t r = jr - qtile * bsq;
-        const int64_t off0 = (J0 + qtile * bsq) * qps;
+        const int64_t lim = klim[i];
         const int64_t row_off = lay.row_offset(bh, jr);
         const int64_t cap = lay.capacity(J);
         int32_t c = cnt[i];
         for (int step = 0; step < kSelChunk / 64; ++step) {
           const int kk = step * 64 + lane;
           const int64_t key = kbase + kk;
-          const int tl = int(kk / bk);
-          const int64_t koff = kbase + int64_t(tl) * bk;
-          bool sel = key < kend;
-          if (sel && causal) sel = r > (koff - off0) / qps;  // C++ '/' truncates
+          const int tl = kk >> lbk;
+          const int64_t koff = kbase + (int64_t(tl) << lbk);
+          bool sel = key < kend && koff < lim;
           if (sel) sel = (sc[i * kSelChunk + kk] + gap) >= mt[i * (kSelChunk / 16) + tl];
           const uint64_t ballot = __ballot(sel);
           const uint32_t below = __builtin_amdgcn_mbcnt_hi(

@@ -29,8 +29,12 @@
 // All exact work of a chunk is batched over its rows into one parallel pass.
 //
 // Work-group: 64 pooled rows of one q head (4 waves), keys in chunks of 256.
-//   A  MFMA scores stay in VGPRs; the K operand rows are permuted so that a
-//      lane holds one whole 16-key segment of one row; segment maxima -> LDS.
+// Each chunk of K is loaded with coalesced 16-byte loads one chunk ahead (in
+// flight while the previous chunk is processed) and stored to LDS in MFMA
+// operand order; every K element is read from HBM/L2 once per work-group.
+//   A  wave w scores keys [64w, 64w+64) of the chunk against all 64 rows; the
+//      scores stay in VGPRs; the K operand rows are permuted so that a lane
+//      holds one whole 16-key segment of one row; segment maxima -> LDS.
 //   B  per row, prefix of tile maxima with group restarts (4 threads per row,
 //      segmented scan) -> M̂ per tile.
 //   C  decisions from the VGPR scores -> selected / ambiguous bit masks.
@@ -50,6 +54,8 @@ constexpr int kMSeg = 16;   // 16-key segments per chunk
 // MFMA row m of the K operand -> key offset inside the 32-key block, such that
 // accumulator element e of lane l holds key 16*(l/32) + e.
 __device__ inline int kperm(int m) { return 16 * ((m >> 2) & 1) + 4 * (m >> 3) + (m & 3); }
+// Inverse of kperm: key offset k (0..31) -> MFMA row.
+__device__ inline int kinv(int k) { return 8 * ((k >> 2) & 3) + 4 * (k >> 4) + (k & 3); }
 
 // Canonical score: sequential fp64 FMAs over d (exact products), one rounding
 // to fp32.  All loads are issued before the dependent FMA chain.
@@ -79,29 +85,37 @@ template <typename T, int D>
 __global__ __launch_bounds__(256) void select_mfma_kernel(
     const T* __restrict__ qs, int64_t sqb, int64_t sqh, int64_t sqn, const T* __restrict__ k,
     int64_t skb, int64_t skh, int64_t sks, int64_t B, int64_t Hq, int64_t Hk, int64_t Sk,
-    int64_t qps, int bk, int64_t group, int causal, int64_t bsq, float gap_scalar,
+    int64_t qps, int bk, uint32_t gspan, int causal, int64_t bsq, float gap_scalar,
     const float* __restrict__ gaps, const float* __restrict__ kmax, RowLayout lay,
     int32_t* __restrict__ counts, int32_t* __restrict__ indices, int64_t nrowsets) {
   using M = Mfma<T>;
   using vec = typename M::vec;
-  constexpr int NS = D / 16;  // MFMA steps over the features
+  constexpr int NS = D / 16;        // MFMA steps over the features
+  constexpr int STR = D + 8;        // LDS row stride (elements): 16-byte aligned rows
+  constexpr int CPR = D / 8;        // 16-byte chunks per row
+  constexpr int KLD = kMKC * CPR / 256;  // K chunks per thread per chunk of keys
 
+  // K chunk, rows stored in MFMA operand order: LDS row 32*blk + m holds key
+  // 32*blk + kperm(m), so the operand reads of a wave hit consecutive rows.
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[kMKC * STR];
+  __shared__ __attribute__((aligned(16))) uint16_t Qs[kMR * STR];   // pooled rows
   __shared__ float tm[kMR][kMSeg + 1];        // segment maxima of MFMA scores
   __shared__ float mh[kMR][kMSeg + 1];        // running maximum at the segment's tile
   __shared__ uint32_t msk[kMR][kMSeg + 1];    // selected (low 16) / ambiguous (high 16)
+  __shared__ uint32_t cmk[kMR][kMSeg + 1];    // running-maximum candidates (16 bits)
   __shared__ int32_t off[kMR][kMSeg + 1];     // output offset of the segment's first key
   __shared__ float rband[kMR], rwin[kMR], ecar[kMR];
   __shared__ int32_t rcnt[kMR], rwork[kMR];
-  __shared__ uint32_t cmk[kMR][kMSeg + 1];    // running-maximum candidates (16 bits)
   __shared__ uint32_t jobs[kMJobs];           // (row << 8) | key offset in chunk
   __shared__ float exv[kMJobs];               // exact scores of the jobs
   __shared__ int32_t jbeg[kMR], jcnt[kMR];
   __shared__ int32_t njobs, pending;
+  __shared__ int32_t klim[kMR];               // causal: keys < klim are allowed
+  __shared__ int64_t rowoff[kMR], rowcap[kMR];
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
   const int l32 = lane & 31, hh = lane >> 5;
-  const int rb = wave & 1, kh = wave >> 1;
 
   const int64_t BH = B * Hq;
   const int64_t rs = nrowsets - 1 - int64_t(blockIdx.x) / BH;  // heavy rows first
@@ -113,7 +127,7 @@ __global__ __launch_bounds__(256) void select_mfma_kernel(
   const float gap = gaps ? gaps[bh] : gap_scalar;
   const float kn = kmax[b * Hk + hk];
   const int64_t smin = lay.smin();
-  const int64_t gspan = int64_t(bk) * group;
+  const int lbk = __builtin_ctz(uint32_t(bk));  // bk is a power of two
   const int64_t kstart = smin;
   int64_t kend = Sk;
   if (causal) {
@@ -123,11 +137,18 @@ __global__ __launch_bounds__(256) void select_mfma_kernel(
   const T* qbase = qs + b * sqb + h * sqh;
   const T* kbh = k + b * skb + hk * skh;
 
-  // ---- per-row setup: norms, bounds, state ---------------------------------
+  // ---- pooled rows -> LDS; per-row norms, bounds, state ---------------------
+  for (int c = tid; c < kMR * CPR; c += 256) {
+    const int row = c / CPR, ch = c % CPR;
+    uint4 v = make_uint4(0, 0, 0, 0);
+    if (row < rows_here) v = *reinterpret_cast<const uint4*>(qbase + (jr0 + row) * sqn + 8 * ch);
+    *reinterpret_cast<uint4*>(&Qs[row * STR + 8 * ch]) = v;
+  }
+  lds_barrier();
   if (tid < kMR) {
     float band = 0.f, win = 0.f;
     if (tid < rows_here) {
-      const T* qr = qbase + (jr0 + tid) * sqn;
+      const T* qr = reinterpret_cast<const T*>(&Qs[tid * STR]);
       double ss = 0.0;
       for (int d = 0; d < D; ++d) {
         const double x = double(to_f32(qr[d]));
@@ -144,183 +165,231 @@ __global__ __launch_bounds__(256) void select_mfma_kernel(
     ecar[tid] = -__builtin_inff();
     rcnt[tid] = 0;
     rwork[tid] = 0;
+    // The reference's causal tile test r > trunc((k_off - off0) / qps), with
+    // r the row inside its BLOCK_SIZE_Q program and off0 = (J - r) * qps, is
+    // k_off < J*qps for r >= 1 and k_off <= (J-1)*qps for r == 0 (C++ '/'
+    // truncates like Triton's signed division).
+    const int64_t jr = jr0 + tid;
+    const int64_t J = J0 + jr;
+    const int64_t r = jr % bsq;
+    int64_t lim = 0x7fffffff;
+    if (causal) lim = (r == 0) ? (J - 1) * qps + 1 : J * qps;
+    klim[tid] = int32_t(lim < 0 ? 0 : (lim > 0x7fffffff ? 0x7fffffff : lim));
+    rowoff[tid] = tid < rows_here ? lay.row_offset(bh, jr) : 0;
+    rowcap[tid] = tid < rows_here ? lay.capacity(J) : 0;
   }
-
-  // Q^T operand: lane holds row rb*32 + l32, features (D/2)*hh + 8*s .. +8.
-  vec qop[NS];
-  {
-    const int row = rb * 32 + l32;
-    const T* qr = qbase + (jr0 + row) * sqn + (D / 2) * hh;
+  // Q^T operands of all 64 rows: row 32*rb + l32, features (D/2)*hh + 8*s.
+  vec qop[2][NS];
 #pragma unroll
-    for (int s = 0; s < NS; ++s) {
-      uint4 raw = make_uint4(0, 0, 0, 0);
-      if (row < rows_here) raw = *reinterpret_cast<const uint4*>(qr + 8 * s);
-      qop[s] = __builtin_bit_cast(vec, raw);
-    }
-  }
-  const int krow_off = kperm(l32);
-  __syncthreads();
+  for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+    for (int s = 0; s < NS; ++s)
+      qop[rb][s] = __builtin_bit_cast(
+          vec, *reinterpret_cast<const uint4*>(&Qs[(rb * 32 + l32) * STR + (D / 2) * hh + 8 * s]));
 
   const int nseg_tile = bk / 16;           // segments per tile
   const int ntile = kMKC / bk;             // tiles per chunk
   const int tpt = ntile / 4;               // tiles per thread in phase B
   const int64_t kfirst = kstart / kMKC * kMKC;
-  // Does the last group of the chunk at kbase continue into the next chunk?
+  // Does the last group of the chunk at kb0 continue into the next chunk?
+  // (key offsets < 2^31; 32-bit arithmetic)
   auto cont_chunk = [&](int64_t kb0) {
-    return ((kb0 + kMKC) % gspan != 0) && (kb0 + kMKC < kend);
+    return (uint32_t(kb0 + kMKC) % gspan != 0u) && (kb0 + kMKC < kend);
   };
+  // Bit t set: tile t of the chunk at kb0 starts a group.
+  auto group_starts = [&](int64_t kb0) {
+    const uint32_t base = uint32_t(kb0);
+    const uint32_t rem = base % gspan;
+    uint32_t b0 = rem ? base + (gspan - rem) : base;
+    uint32_t m = 0;
+    for (; b0 < base + kMKC; b0 += gspan) {
+      m |= 1u << ((b0 - base) >> lbk);
+      if (b0 + gspan < b0) break;  // no wrap-around
+    }
+    return m;
+  };
+  // Coalesced K loads of one chunk: thread t takes 16-byte chunk t + 256*i.
+  uint4 kpre[KLD];
+  auto load_chunk = [&](int64_t kb0) {
+#pragma unroll
+    for (int i = 0; i < KLD; ++i) {
+      const int c = tid + 256 * i;
+      const int64_t key = kb0 + c / CPR;
+      kpre[i] = key < Sk ? *reinterpret_cast<const uint4*>(kbh + key * sks + 8 * (c % CPR))
+                         : make_uint4(0, 0, 0, 0);
+    }
+  };
+  auto store_chunk = [&]() {
+#pragma unroll
+    for (int i = 0; i < KLD; ++i) {
+      const int c = tid + 256 * i;
+      const int kk = c / CPR;                    // key offset in the chunk
+      const int lrow = (kk & ~31) | kinv(kk & 31);
+      *reinterpret_cast<uint4*>(&Ks[lrow * STR + 8 * (c % CPR)]) = kpre[i];
+    }
+  };
+  if (kfirst < kend) load_chunk(kfirst);
 
   for (int64_t kbase = kfirst; kbase < kend; kbase += kMKC) {
+    lds_barrier();  // previous chunk's readers of Ks are done
+    store_chunk();
+    lds_barrier();
+    if (kbase + kMKC < kend) load_chunk(kbase + kMKC);  // in flight until the next chunk
+
     // ================= A: MFMA scores, segment maxima =======================
-    f32x16_t sc[4];
+    // wave w: keys [64w, 64w+64) of the chunk, all 64 rows.
+    f32x16_t sc[2][2];
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
-      const int64_t bbase = kbase + (kh * 4 + kb) * 32;
-      const int64_t key = bbase + krow_off;
+    for (int kb = 0; kb < 2; ++kb) {
+      const int blk = 2 * wave + kb;
       vec kop[NS];
-      const T* kr = kbh + key * sks + (D / 2) * hh;
+      const uint16_t* kr = &Ks[(blk * 32 + l32) * STR + (D / 2) * hh];
 #pragma unroll
-      for (int s = 0; s < NS; ++s) {
-        uint4 raw = make_uint4(0, 0, 0, 0);
-        if (key < Sk) raw = *reinterpret_cast<const uint4*>(kr + 8 * s);
-        kop[s] = __builtin_bit_cast(vec, raw);
+      for (int s = 0; s < NS; ++s)
+        kop[s] = __builtin_bit_cast(vec, *reinterpret_cast<const uint4*>(kr + 8 * s));
+      const int64_t sbase = kbase + blk * 32 + 16 * hh;
+      const bool edge = !(kbase + blk * 32 >= kstart && kbase + blk * 32 + 32 <= kend);
+#pragma unroll
+      for (int rb = 0; rb < 2; ++rb) {
+        f32x16_t acc;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[e] = 0.f;
+#pragma unroll
+        for (int s = 0; s < NS; ++s) acc = M::run(kop[s], qop[rb][s], acc);
+        if (edge) {
+#pragma unroll
+          for (int e = 0; e < 16; ++e)
+            if (sbase + e < kstart || sbase + e >= kend) acc[e] = -__builtin_inff();
+        }
+        float m = acc[0];
+#pragma unroll
+        for (int e = 1; e < 16; ++e) m = __builtin_fmaxf(m, acc[e]);
+        tm[rb * 32 + l32][blk * 2 + hh] = m;
+        sc[rb][kb] = acc;
       }
-      f32x16_t acc;
-#pragma unroll
-      for (int e = 0; e < 16; ++e) acc[e] = 0.f;
-#pragma unroll
-      for (int s = 0; s < NS; ++s) acc = M::run(kop[s], qop[s], acc);
-      const int64_t sbase = bbase + 16 * hh;
-      if (!(bbase >= kstart && bbase + 32 <= kend)) {
-#pragma unroll
-        for (int e = 0; e < 16; ++e)
-          if (sbase + e < kstart || sbase + e >= kend) acc[e] = -__builtin_inff();
-      }
-      float m = acc[0];
-#pragma unroll
-      for (int e = 1; e < 16; ++e) m = __builtin_fmaxf(m, acc[e]);
-      tm[rb * 32 + l32][(kh * 4 + kb) * 2 + hh] = m;
-      sc[kb] = acc;
     }
-    __syncthreads();
+    lds_barrier();
 
     // ================= B: running maximum per tile ==========================
+    const uint32_t gmask = group_starts(kbase);
+    const bool cont = cont_chunk(kbase);
     {
       const int row = tid >> 2, part = tid & 3;
       float lp[4];
       bool lf[4];
       float v = -__builtin_inff();
       bool f = false;
-      for (int i = 0; i < tpt; ++i) {
-        const int t = part * tpt + i;
-        const int64_t koff = kbase + int64_t(t) * bk;
-        float tv = -__builtin_inff();
-        for (int j = 0; j < nseg_tile; ++j) tv = __builtin_fmaxf(tv, tm[row][t * nseg_tile + j]);
-        if (koff % gspan == 0) {
-          v = tv;
-          f = true;
-        } else {
-          v = __builtin_fmaxf(v, tv);
-        }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
         lp[i] = v;
         lf[i] = f;
+        if (i < tpt) {
+          const int t = part * tpt + i;
+          float tv = -__builtin_inff();
+          for (int j = 0; j < nseg_tile; ++j) tv = __builtin_fmaxf(tv, tm[row][t * nseg_tile + j]);
+          if ((gmask >> t) & 1u) {
+            v = tv;
+            f = true;
+          } else {
+            v = __builtin_fmaxf(v, tv);
+          }
+          lp[i] = v;
+          lf[i] = f;
+        }
       }
       // exclusive combine of the aggregates of the row's earlier parts
       const int base_lane = lane & ~3;
       float in_v = ecar[row];
-      bool in_f = false;
       for (int p = 0; p < 4; ++p) {
         const float pv = __shfl(v, base_lane + p);
         const bool pf = __shfl(int(f), base_lane + p) != 0;
-        if (p < part) {
-          if (pf) { in_v = pv; in_f = true; } else { in_v = __builtin_fmaxf(in_v, pv); }
-        }
+        if (p < part) in_v = pf ? pv : __builtin_fmaxf(in_v, pv);
       }
-      (void)in_f;
       float mlast = 0.f;
-      for (int i = 0; i < tpt; ++i) {
-        const int t = part * tpt + i;
-        const float mt = lf[i] ? lp[i] : __builtin_fmaxf(in_v, lp[i]);
-        for (int j = 0; j < nseg_tile; ++j) mh[row][t * nseg_tile + j] = mt;
-        mlast = mt;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if (i < tpt) {
+          const int t = part * tpt + i;
+          const float mt = lf[i] ? lp[i] : __builtin_fmaxf(in_v, lp[i]);
+          for (int j = 0; j < nseg_tile; ++j) mh[row][t * nseg_tile + j] = mt;
+          mlast = mt;
+        }
       }
       // A group continuing into the next chunk needs its maximum carried
       // exactly: flag the row when a tile of that group can hold it.
-      if (part == 3 && row < rows_here && cont_chunk(kbase)) {
+      if (part == 3 && row < rows_here && cont) {
         const float win = rwin[row];
         for (int t = ntile - 1; t >= 0; --t) {
           float tv = -__builtin_inff();
           for (int j = 0; j < nseg_tile; ++j) tv = __builtin_fmaxf(tv, tm[row][t * nseg_tile + j]);
           if (tv >= mlast - win) { atomicOr(&rwork[row], 2); break; }
-          if ((kbase + int64_t(t) * bk) % gspan == 0) break;
+          if ((gmask >> t) & 1u) break;
         }
       }
     }
-    __syncthreads();
+    lds_barrier();
 
     // ================= C: decisions from the VGPR scores ====================
-    {
-      const int row = rb * 32 + l32;
-      const int64_t jr = jr0 + row;
-      const int64_t qtile = jr / bsq;
-      const int64_t r = jr - qtile * bsq;
-      const int64_t off0 = (J0 + qtile * bsq) * qps;
-      const float band = rband[row];
 #pragma unroll
-      for (int kb = 0; kb < 4; ++kb) {
-        const int seg = (kh * 4 + kb) * 2 + hh;
+    for (int rb = 0; rb < 2; ++rb) {
+      const int row = rb * 32 + l32;
+      const int64_t lim = klim[row];
+      const float band = rband[row];
+      const float win = rwin[row];
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        const int seg = (2 * wave + kb) * 2 + hh;
         const int64_t sbase = kbase + seg * 16;
-        const int64_t koff = sbase / bk * bk;  // tile start (tiles are bk-aligned)
+        const int64_t koff = sbase & ~int64_t(bk - 1);  // tile start (tiles are bk-aligned)
         uint32_t sel = 0, amb = 0, cand = 0;
         const bool live = row < rows_here && sbase < kend && sbase + 16 > kstart;
-        bool ok = live;
-        if (ok && causal) ok = r > (koff - off0) / qps;  // truncating division
+        const bool ok = live && koff < lim;
         if (live) {
+          const float mrun = mh[row][seg];
           // keys that may hold the exact running maximum of their tile prefix
           // (masked keys hold -inf and are never candidates)
-          const float cthr = mh[row][seg] - rwin[row];
+          const float cthr = mrun - win;
 #pragma unroll
           for (int e = 0; e < 16; ++e)
-            cand |= uint32_t(sc[kb][e] >= cthr && sc[kb][e] > -__builtin_inff()) << e;
-        }
-        cmk[row][seg] = cand;
-        if (ok) {
-          const float thr = mh[row][seg] - gap;
-          float mind = __builtin_inff();
-#pragma unroll
-          for (int e = 0; e < 16; ++e) {
-            const float d = sc[kb][e] - thr;
-            sel |= uint32_t(d > band) << e;
-            mind = __builtin_fminf(mind, __builtin_fabsf(d));
-          }
-          if (mind <= band) {
+            cand |= uint32_t(sc[rb][kb][e] >= cthr && sc[rb][kb][e] > -__builtin_inff()) << e;
+          if (ok) {
+            const float thr = mrun - gap;
+            float mind = __builtin_inff();
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
-              const float d = sc[kb][e] - thr;
-              amb |= uint32_t(__builtin_fabsf(d) <= band) << e;
+              const float d = sc[rb][kb][e] - thr;
+              sel |= uint32_t(d > band) << e;
+              mind = __builtin_fminf(mind, __builtin_fabsf(d));
             }
-            sel &= ~amb;
-            atomicOr(&rwork[row], 1);
+            if (mind <= band) {
+#pragma unroll
+              for (int e = 0; e < 16; ++e) {
+                const float d = sc[rb][kb][e] - thr;
+                amb |= uint32_t(__builtin_fabsf(d) <= band) << e;
+              }
+              sel &= ~amb;
+              atomicOr(&rwork[row], 1);
+            }
           }
         }
+        cmk[row][seg] = cand;
         msk[row][seg] = sel | (amb << 16);
       }
     }
-    __syncthreads();
+    lds_barrier();
 
     // ================= D: exact resolution (rare) ===========================
     // Rows flagged in B (carried maximum) or C (ambiguous pairs) enqueue their
     // candidate and ambiguous keys; the whole work-group computes the exact
-    // scores; each row then resolves its decisions and carried maximum.
+    // scores from the LDS copies of K and Q; each row then resolves its
+    // decisions and carried maximum.
     if (tid == 0) pending = 0;
-    __syncthreads();
+    lds_barrier();
     if (tid < kMR && tid < rows_here && rwork[tid] != 0) atomicAdd(&pending, 1);
-    __syncthreads();
-    const bool cont = cont_chunk(kbase);
+    lds_barrier();
     while (pending > 0) {
-      __syncthreads();
       if (tid == 0) njobs = 0;
-      __syncthreads();
+      lds_barrier();
       // D1: enqueue.  Wave 0 (one lane per row) scans the rows' job counts;
       // the rows whose jobs fit are served this round, each in a contiguous
       // slot range, so slots [0, njobs) are all written.
@@ -351,27 +420,28 @@ __global__ __launch_bounds__(256) void select_mfma_kernel(
           }
         }
       }
-      __syncthreads();
-      // D2: exact scores, all threads
+      lds_barrier();
+      // D2: exact scores, all threads, operands from LDS
       const int nj = njobs;
-      for (int j = tid; j < nj; j += blockDim.x) {
+      for (int j = tid; j < nj; j += 256) {
         const int row = int(jobs[j] >> 8), kk = int(jobs[j] & 255u);
         const int64_t key = kbase + kk;
+        const int lrow = (kk & ~31) | kinv(kk & 31);
         exv[j] = (row < rows_here && key >= kstart && key < kend)
-                     ? exact_dot<T, D>(qbase + (jr0 + row) * sqn, kbh + key * sks)
+                     ? exact_dot<T, D>(reinterpret_cast<const T*>(&Qs[row * STR]),
+                                       reinterpret_cast<const T*>(&Ks[lrow * STR]))
                      : -__builtin_inff();
       }
-      __syncthreads();
+      lds_barrier();
       // D3: per row resolution
       if (tid < kMR && jcnt[tid] >= 0) {
         const int row = tid;
         const int jb = jbeg[row], jn = jcnt[row];
-        const bool first_open = (kbase % gspan) != 0;  // group began in an earlier chunk
+        const bool first_open = (gmask & 1u) == 0;  // group began in an earlier chunk
         const float e_in = ecar[row];
-        auto group_start_tile = [&](int t) {
-          int g = t;
-          while (g > 0 && (kbase + int64_t(g) * bk) % gspan != 0) --g;
-          return g;
+        auto group_start_tile = [&](int t) {  // highest group start <= t, else 0
+          const uint32_t m = gmask & ((2u << t) - 1u);
+          return m ? 31 - __builtin_clz(m) : 0;
         };
         // running maximum of tiles [g0, t] from exact candidate scores
         auto exact_max = [&](int g0, int t) {
@@ -379,7 +449,7 @@ __global__ __launch_bounds__(256) void select_mfma_kernel(
           for (int j = jb; j < jb + jn; ++j) {
             const int kk = int(jobs[j] & 255u);
             const int seg = kk >> 4, e = kk & 15;
-            const int tt = kk / bk;
+            const int tt = kk >> lbk;
             if (tt >= g0 && tt <= t && ((cmk[row][seg] >> e) & 1u)) m = __builtin_fmaxf(m, exv[j]);
           }
           return m;
@@ -391,7 +461,7 @@ __global__ __launch_bounds__(256) void select_mfma_kernel(
           const float mt = exact_max(group_start_tile(t), t);
           for (int j = jb; j < jb + jn; ++j) {
             const int kk = int(jobs[j] & 255u);
-            if (kk / bk != t) continue;
+            if ((kk >> lbk) != t) continue;
             const int seg = kk >> 4, e = kk & 15;
             const uint32_t w = msk[row][seg];
             if ((w >> (16 + e)) & 1u) {
@@ -400,22 +470,20 @@ __global__ __launch_bounds__(256) void select_mfma_kernel(
             }
           }
         }
-        if (cont) {
-          ecar[row] = exact_max(group_start_tile(ntile - 1), ntile - 1);
-        }
+        if (cont) ecar[row] = exact_max(group_start_tile(ntile - 1), ntile - 1);
         rwork[row] = 0;
       }
-      __syncthreads();
+      lds_barrier();
       if (tid == 0) {
         int left = 0;
         for (int r = 0; r < rows_here; ++r) left += rwork[r] != 0;
         pending = left;
       }
-      __syncthreads();
+      lds_barrier();
     }
     // A group that does not continue hands no maximum to the next chunk.
     if (tid < kMR && !cont) ecar[tid] = -__builtin_inff();
-    __syncthreads();
+    lds_barrier();
 
     // ================= E: output offsets per segment ========================
     {
@@ -441,18 +509,18 @@ __global__ __launch_bounds__(256) void select_mfma_kernel(
       }
       if (part == 3) rcnt[row] = rc + all;
     }
-    __syncthreads();
+    lds_barrier();
 
     // ================= G: ordered stores =====================================
-    {
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
       const int row = rb * 32 + l32;
       if (row < rows_here) {
-        const int64_t jr = jr0 + row;
-        const int64_t row_off = lay.row_offset(bh, jr);
-        const int64_t cap = lay.capacity(J0 + jr);
+        const int64_t row_off = rowoff[row];
+        const int64_t cap = rowcap[row];
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb) {
-          const int seg = (kh * 4 + kb) * 2 + hh;
+        for (int kb = 0; kb < 2; ++kb) {
+          const int seg = (2 * wave + kb) * 2 + hh;
           uint32_t bits = msk[row][seg] & 0xffffu;
           int64_t pos = off[row][seg];
           const int64_t sbase = kbase + seg * 16;
@@ -466,9 +534,9 @@ __global__ __launch_bounds__(256) void select_mfma_kernel(
       }
     }
   }
-  __syncthreads();
+  lds_barrier();
   if (tid < rows_here) {
-    const int64_t cap = lay.capacity(J0 + jr0 + tid);
+    const int64_t cap = rowcap[tid];
     const int32_t c = rcnt[tid];
     counts[bh * nc + jr0 + tid] = (c < cap) ? c : int32_t(cap);
   }
@@ -488,9 +556,13 @@ static hipError_t launch_select_mfma_td(const void* qs, int64_t sqb, int64_t sqh
                                         const RowLayout& lay, int32_t* counts, int32_t* indices,
                                         hipStream_t stream) {
   const int64_t nrowsets = (lay.nc + kMR - 1) / kMR;
+  // Group span in keys, capped at 2^31 (key offsets are below 2^31, so a span
+  // that large has its only boundary at 0 either way).
+  const int64_t gs = (group > (int64_t(1) << 31) / bk) ? (int64_t(1) << 31) : bk * group;
+  const uint32_t gspan32 = uint32_t(gs);
   hipLaunchKernelGGL((select_mfma_kernel<T, D>), dim3(unsigned(nrowsets * B * Hq)), dim3(256), 0,
                      stream, static_cast<const T*>(qs), sqb, sqh, sqn, static_cast<const T*>(k),
-                     skb, skh, sks, B, Hq, Hk, Sk, qps, int(bk), group, causal, bsq, gap, gaps,
+                     skb, skh, sks, B, Hq, Hk, Sk, qps, int(bk), gspan32, causal, bsq, gap, gaps,
                      kmax, lay, counts, indices, nrowsets);
   return hipGetLastError();
 }
