@@ -58,9 +58,9 @@ __global__ __launch_bounds__(QPS * 2, 2) void attn_mfma_kernel(
   const int wave = tid / 64, lane = tid % 64;
   const int l32 = lane % 32, hh = lane / 32;
 
-  const int64_t BH = B * Hq;
-  const int64_t jr = lay.nc - 1 - int64_t(blockIdx.x) / BH;  // heavy blocks first
-  const int64_t bh = int64_t(blockIdx.x) % BH;
+  const WorkOrder wo{lay.nc, B, Hq, Hk};
+  int64_t jr, bh;
+  if (!wo.map_item(blockIdx.x, jr, bh)) return;  // idle block (uniform)
   const int64_t b = bh / Hq, h = bh % Hq, hk = h / (Hq / Hk);
   const int64_t J = lay.J0 + jr;
 
@@ -325,7 +325,7 @@ static hipError_t launch_attn_mfma_tdq(const void* q, const int64_t* sq, const v
                                        float scale_log2, const int32_t* counts,
                                        const int32_t* indices, const RowLayout& lay,
                                        hipStream_t stream) {
-  const int64_t nblocks = lay.nc * B * Hq;
+  const int64_t nblocks = WorkOrder{lay.nc, B, Hq, Hk}.grid_items();
   hipLaunchKernelGGL((attn_mfma_kernel<T, D, QPS>), dim3(unsigned(nblocks)), dim3(QPS * 2), 0,
                      stream, static_cast<const T*>(q), sq[0], sq[1], sq[2],
                      static_cast<const T*>(k), sk[0], sk[1], sk[2], static_cast<const T*>(v),

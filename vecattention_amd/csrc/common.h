@@ -64,6 +64,60 @@ __device__ inline void lds_barrier() {
 }
 
 // ---------------------------------------------------------------------------
+// Work order.  Work-groups are dispatched round-robin over the 8 XCDs of the
+// chip (block i runs on XCD i % 8), each with its own L2.  A work item is
+// (row block jr in [0, nrows), q head bh in [0, B*Hq)); items of one kv head
+// (b, hk) read the same K/V rows, so they are kept on the same XCDs, and each
+// XCD walks its items longest-first (descending jr).  grid_items() is the
+// launch size; map_item() returns false for the few idle blocks of a launch
+// whose kv-group count does not split evenly over the XCDs.
+// ---------------------------------------------------------------------------
+struct WorkOrder {
+  int64_t nrows, B, Hq, Hk;
+  static constexpr int kXcd = 8;
+
+  __host__ __device__ int64_t nkv() const { return B * Hk; }
+  __host__ __device__ int64_t rep() const { return Hq / Hk; }
+  __host__ __device__ int64_t grid_items() const {
+    const int64_t g = nkv();
+    if (kXcd % g == 0) {
+      const int64_t copies = kXcd / g;
+      const int64_t per = (rep() * nrows + copies - 1) / copies;
+      return kXcd * per;
+    }
+    return nrows * B * Hq;
+  }
+  __host__ __device__ bool map_item(int64_t i, int64_t& jr, int64_t& bh) const {
+    const int64_t g = nkv(), r = rep();
+    if (kXcd % g == 0) {  // several XCDs per kv group
+      const int64_t copies = kXcd / g;
+      const int64_t x = i % kXcd, s = i / kXcd;
+      const int64_t grp = x % g, c = x / g;
+      const int64_t j = s * copies + c;
+      if (j >= r * nrows) return false;
+      jr = nrows - 1 - j / r;
+      const int64_t b = grp / Hk, hk = grp % Hk;
+      bh = b * Hq + hk * r + j % r;
+      return true;
+    }
+    if (g % kXcd == 0) {  // several kv groups per XCD
+      const int64_t per = g / kXcd;
+      const int64_t x = i % kXcd, s = i / kXcd;
+      jr = nrows - 1 - s / (per * r);
+      const int64_t rem = s % (per * r);
+      const int64_t grp = x + kXcd * (rem / r);
+      const int64_t b = grp / Hk, hk = grp % Hk;
+      bh = b * Hq + hk * r + rem % r;
+      return true;
+    }
+    const int64_t BH = B * Hq;  // plain longest-first order
+    jr = nrows - 1 - i / BH;
+    bh = i % BH;
+    return true;
+  }
+};
+
+// ---------------------------------------------------------------------------
 // Per-row index lists of the selection ("capacity layout").
 //
 // Row J of a chunk [J0, J0+nc) owns `row_capacity(J)` int32 slots: the number

@@ -117,9 +117,9 @@ __global__ __launch_bounds__(256) void select_mfma_kernel(
   const int wave = tid >> 6, lane = tid & 63;
   const int l32 = lane & 31, hh = lane >> 5;
 
-  const int64_t BH = B * Hq;
-  const int64_t rs = nrowsets - 1 - int64_t(blockIdx.x) / BH;  // heavy rows first
-  const int64_t bh = int64_t(blockIdx.x) % BH;
+  const WorkOrder wo{nrowsets, B, Hq, Hk};
+  int64_t rs, bh;
+  if (!wo.map_item(blockIdx.x, rs, bh)) return;  // idle block (uniform)
   const int64_t b = bh / Hq, h = bh % Hq, hk = h / (Hq / Hk);
   const int64_t jr0 = rs * kMR;
   const int64_t nc = lay.nc, J0 = lay.J0;
@@ -560,7 +560,8 @@ static hipError_t launch_select_mfma_td(const void* qs, int64_t sqb, int64_t sqh
   // that large has its only boundary at 0 either way).
   const int64_t gs = (group > (int64_t(1) << 31) / bk) ? (int64_t(1) << 31) : bk * group;
   const uint32_t gspan32 = uint32_t(gs);
-  hipLaunchKernelGGL((select_mfma_kernel<T, D>), dim3(unsigned(nrowsets * B * Hq)), dim3(256), 0,
+  const int64_t nblocks = WorkOrder{nrowsets, B, Hq, Hk}.grid_items();
+  hipLaunchKernelGGL((select_mfma_kernel<T, D>), dim3(unsigned(nblocks)), dim3(256), 0,
                      stream, static_cast<const T*>(qs), sqb, sqh, sqn, static_cast<const T*>(k),
                      skb, skh, sks, B, Hq, Hk, Sk, qps, int(bk), gspan32, causal, bsq, gap, gaps,
                      kmax, lay, counts, indices, nrowsets);
