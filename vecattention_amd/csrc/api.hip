@@ -252,14 +252,25 @@ static int attn_dispatch(int dtype, const void* q, const int64_t* sq, const void
   const bool mfma_shape = va::attn_mfma_supported(dtype, D, qps);
   const bool mfma_align = aligned(q, sq, 16 / es) && aligned(k, sk, 16 / es) &&
                           aligned(v, sv, 16 / es) && aligned(out, so, 8 / es);
+  // The MFMA kernel gathers K/V rows with 32-bit buffer offsets computed by
+  // 24-bit multiplies: each kv head's rows must span < 2 GiB, keys and row
+  // strides in bytes must stay below 2^24.
+  auto span_ok = [&](const int64_t* s) {
+    return Sk < (int64_t(1) << 24) && s[2] >= 0 && s[2] * es < (int64_t(1) << 24) &&
+           ((Sk - 1) * s[2] + D) * es < (int64_t(1) << 31);
+  };
+  const bool mfma_span = span_ok(sk) && span_ok(sv);
   bool use_mfma = false;
   if (kernel == VA_ATTN_MFMA) {
     if (!mfma_shape)
       return fail(VA_ERR_UNSUPPORTED, "MFMA attention needs bf16/fp16, D in {64,128}, qps in {64,128}");
     if (!mfma_align) return fail(VA_ERR_UNSUPPORTED, "MFMA attention needs 16-byte aligned rows");
+    if (!mfma_span)
+      return fail(VA_ERR_UNSUPPORTED, "MFMA attention needs Sk < 2^24, row strides < 16 MiB and "
+                                      "< 2 GiB of rows per kv head");
     use_mfma = true;
   } else if (kernel == VA_ATTN_AUTO) {
-    use_mfma = mfma_shape && mfma_align;
+    use_mfma = mfma_shape && mfma_align && mfma_span;
   } else if (kernel != VA_ATTN_SIMPLE) {
     return fail(VA_ERR_ARG, "unknown kernel selector %d", kernel);
   }

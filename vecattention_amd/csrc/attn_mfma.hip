@@ -1,21 +1,37 @@
-// Vector-sparse flash-attention prefill on CDNA4 bf16/fp16 MFMA.
+// Vector-sparse flash-attention prefill on CDNA4 (gfx950) bf16/fp16 MFMA.
 //
 // Replaces vllm_flash_attn.sparse_attn_func as called at
 // spattn/src/VecAttention.py:110-121 (semantics restated from
 // spattn/threshold/model_tuner.py:193-216; see keylist.h).  One work-group
-// owns one q-block (QPS rows) of one q head; it walks that block's key list in
-// tiles of 64 keys, gathering the K and V rows of each tile into LDS, and runs
-// an online softmax.  GQA is native: q head h reads kv head h / (Hq / Hk).
+// owns one q-block (QPS rows) of one q head and walks that block's key list in
+// tiles of 64 keys.  GQA is native: q head h reads kv head h / (Hq / Hk).
 //
-// Wave w owns query rows [32w, 32w+32) of the block and computes, per 32-key
-// half of a tile, S^T = K Q^T with v_mfma_f32_32x32x16 (A = K rows from LDS,
-// B = Q^T held in VGPRs for the whole kernel).  In the 32x32 accumulator a lane
-// holds one query (column l%32) and 16 keys, so the row max / row sum of the
-// softmax are in-lane reductions plus one exchange with lane l^32.  The
-// probabilities then feed O^T += V^T P^T directly as the B operand: the k-slot
-// order of the B operand is the accumulator's key order with bits 2 and 3 of
-// the key index swapped, and V is written to LDS transposed (V^T[d][key]) in
-// that permuted key order, so the A operand is one 16-byte LDS read.
+// Data movement.  The K and V rows of a tile are gathered straight into LDS
+// with buffer_load_dwordx4 ... lds (no register staging, no LDS stores): each
+// copy instruction fills 1 KB of LDS, lane i writing bytes [16i, 16i+16), and
+// each lane chooses which 16-byte chunk of which key row it fetches.  Empty
+// slots of a tile and keys outside [0, Sk) use an offset past the buffer's
+// range, which the hardware returns as zeros.  Rows are stored with an XOR
+// swizzle of their 16-byte chunks (chunk c of row R sits at c ^ (R % chunks))
+// so that the MFMA operand reads below are free of bank conflicts.  Two LDS
+// stages: the copies of tile t+1 are in flight while tile t is computed, and a
+// single barrier per tile separates them.  The key ids of tile t+2 are staged
+// in LDS one tile earlier (copied from the index list, or generated for the
+// local blocks).
+//
+// Compute.  Waves form a (row half, key half) grid: wave (rh, kc) owns query
+// rows [32rh, 32rh+32) and keys [32kc, 32kc+32) of every tile, with its own
+// online-softmax state; the two key halves are merged once at the end.
+// S^T = K Q^T uses v_mfma_f32_32x32x16 with A = K rows from LDS and B = Q^T
+// held in VGPRs, so a lane holds one query and 16 keys: the row maximum is an
+// in-lane reduction plus one v_permlane32_swap.  The probabilities feed
+// O^T += V^T P^T directly as the B operand (the accumulator's key order is a
+// valid k-slot order), and the V^T operand is read from the row-major V tile
+// with ds_read_b64_tr_b16, which transposes 16-bit elements across each group
+// of 16 lanes.  The running maximum is only moved when a tile's maximum
+// exceeds it by more than 2^8 in probability, so the O rescale (D/2 multiplies
+// per lane) is rare; probabilities stay below 2^8, far inside fp32 and
+// bf16/fp16 range, and O / l is unchanged by the choice of reference maximum.
 //
 // Algorithmic work per gathered key: 4*D FLOPs per query row (QK^T and PV).
 #include "keylist.h"
@@ -24,14 +40,91 @@
 namespace va {
 
 constexpr int kTileKeys = 64;
+constexpr uint32_t kOutOfRange = 0xfffffff0u;  // voffset past every buffer's range
+constexpr float kRescaleSlack = 8.f;           // log2 of the largest kept probability
 
-// Swap bits 2 and 3 of a key index inside its 16-key group (an involution).
-__device__ inline int perm_key(int kk) {
-  return (kk & ~12) | ((kk & 4) << 1) | ((kk & 8) >> 1);
+typedef __attribute__((address_space(3))) void* lds_void_ptr;
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+
+template <int D, int QPS>
+struct AttnShape {
+  static constexpr int kRowHalves = QPS / 32;
+  static constexpr int kWaves = 2 * kRowHalves;
+  static constexpr int kThreads = 64 * kWaves;
+  static constexpr int kRowBytes = 2 * D;
+  static constexpr int kChunks = D / 8;                      // 16-byte chunks per row
+  static constexpr int kTileBytes = kTileKeys * kRowBytes;   // one K (or V) tile
+  static constexpr int kStageBytes = 2 * kTileBytes;         // K tile, then V tile
+  static constexpr int kRowsPerCopy = 1024 / kRowBytes;      // rows per 1 KB copy
+  static constexpr int kCopiesPerWave = kTileBytes / 1024 / kWaves;  // per operand
+  static constexpr int kMergeBytes = kRowHalves * 64 * (D / 2 + 2) * 4;
+  static constexpr int kDataBytes = 2 * kStageBytes > kMergeBytes ? 2 * kStageBytes : kMergeBytes;
+  static constexpr int kLdsBytes = kDataBytes + 2 * kTileKeys * 4;
+  static_assert(kCopiesPerWave >= 1 && kRowsPerCopy * kCopiesPerWave * kWaves == kTileKeys,
+                "tile copies must split evenly over the waves");
+};
+
+// Buffer resource of a raw buffer (stride 0, 32-bit data format) of `bytes`
+// bytes at `base`: loads at offsets >= bytes return 0.
+// Every field is made wave-uniform explicitly so that the resource lives in
+// SGPRs, as buffer instructions require.
+__device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  const uint64_t lo = uint32_t(__builtin_amdgcn_readfirstlane(int(uint32_t(a))));
+  const uint64_t hi = uint32_t(__builtin_amdgcn_readfirstlane(int(uint32_t(a >> 32))));
+  return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(lo | (hi << 32)), (short)0,
+                                           __builtin_amdgcn_readfirstlane(int(bytes)),
+                                           0x00020000);
 }
 
+// LDS byte address of a pointer into __shared__ memory.
+__device__ inline uint32_t lds_addr(const void* p) {
+  return uint32_t(reinterpret_cast<uintptr_t>((lds_void_ptr)(const_cast<void*>(p))));
+}
+
+// Global -> LDS copies (buffer_load ... lds): lane i writes `size` bytes at LDS
+// address lds + size*i, read from buffer offset voffset.  Issued from inline
+// assembly so that the compiler's memory-counter bookkeeping does not make
+// LDS reads of the other stage wait for these copies; completion is awaited
+// explicitly with vm_lds_barrier().  M0 (the LDS base) is set in the same
+// statement; nothing else in these kernels uses M0.
+__device__ inline void copy16_to_lds(__amdgpu_buffer_rsrc_t r, uint32_t lds, uint32_t voffset) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               :
+               : "s"(__builtin_amdgcn_readfirstlane(int(lds))), "v"(voffset), "s"(r)
+               : "memory");
+}
+__device__ inline void copy4_to_lds(__amdgpu_buffer_rsrc_t r, uint32_t lds, uint32_t voffset) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen lds"
+               :
+               : "s"(__builtin_amdgcn_readfirstlane(int(lds))), "v"(voffset), "s"(r)
+               : "memory");
+}
+
+// Max of x over lanes l and l ^ 32.
+__device__ inline float max_halves(float x) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, x);
+  const auto p = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return __builtin_fmaxf(__builtin_bit_cast(float, (uint32_t)p[0]),
+                         __builtin_bit_cast(float, (uint32_t)p[1]));
+}
+__device__ inline float sum_halves(float x) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, x);
+  const auto p = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return __builtin_bit_cast(float, (uint32_t)p[0]) + __builtin_bit_cast(float, (uint32_t)p[1]);
+}
+
+// Per-tile facts shared by the copy and the compute of a tile: number of
+// valid slots, and for diagonal tiles the offset of slot 0 from the first
+// diagonal key.
+struct TileInfo {
+  int lim;
+  int dshift;
+  bool diag;
+};
+
 template <typename T, int D, int QPS>
-__global__ __launch_bounds__(QPS * 2, 2) void attn_mfma_kernel(
+__global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == kThreads
     const T* __restrict__ q, int64_t sqb, int64_t sqh, int64_t sqs,
     const T* __restrict__ k, int64_t skb, int64_t skh, int64_t sks,
     const T* __restrict__ v, int64_t svb, int64_t svh, int64_t svs,
@@ -39,24 +132,20 @@ __global__ __launch_bounds__(QPS * 2, 2) void attn_mfma_kernel(
     int64_t Hq, int64_t Hk, int64_t Sq, int64_t Sk, int causal, float scale_log2,
     const int32_t* __restrict__ counts, const int32_t* __restrict__ indices,
     RowLayout lay) {
+  using S = AttnShape<D, QPS>;
   using M = Mfma<T>;
   using vec = typename M::vec;
-  constexpr int NT = QPS * 2;              // threads
-  constexpr int KS = D + 8;                // K tile row stride (elements)
-  constexpr int VS = kTileKeys + 8;        // V^T row stride (elements)
-  constexpr int DCH = D / 8;               // 16-byte chunks per row
-  constexpr int KTOTAL = kTileKeys * DCH;          // 16-byte K chunks per tile
-  constexpr int VTOTAL = (kTileKeys / 4) * DCH;    // (key quad, d chunk) units per tile
-  constexpr int KLOADS = (KTOTAL + NT - 1) / NT;   // per thread
-  constexpr int VUNITS = (VTOTAL + NT - 1) / NT;   // per thread
+  constexpr int NCH = S::kChunks;
+  constexpr int RPC = S::kRowsPerCopy;
+  constexpr int H = S::kCopiesPerWave;
 
-  __shared__ __attribute__((aligned(16))) uint16_t Ks[kTileKeys * KS];
-  __shared__ __attribute__((aligned(16))) uint16_t Vt[D * VS];
-  __shared__ int32_t kid[2][kTileKeys];  // key ids of tiles t (slot t & 1)
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[S::kLdsBytes];
+  int32_t* const ids = reinterpret_cast<int32_t*>(smem + S::kDataBytes);  // [2][64]
 
   const int tid = threadIdx.x;
-  const int wave = tid / 64, lane = tid % 64;
+  const int wave = __builtin_amdgcn_readfirstlane(tid / 64), lane = tid % 64;
   const int l32 = lane % 32, hh = lane / 32;
+  const int rh = wave % S::kRowHalves, kc = wave / S::kRowHalves;
 
   const WorkOrder wo{lay.nc, B, Hq, Hk};
   int64_t jr, bh;
@@ -69,249 +158,262 @@ __global__ __launch_bounds__(QPS * 2, 2) void attn_mfma_kernel(
   if (cnt > cap) cnt = cap;
   const int32_t* cols = indices ? indices + lay.row_offset(bh, jr) : nullptr;
   const KeyList kl = KeyList::make(J, QPS, Sk, causal, cnt, cols);
-  const int64_t t_init = (kl.n_init + kTileKeys - 1) / kTileKeys;
-  const int64_t t_diag = (kl.n_diag + kTileKeys - 1) / kTileKeys;
-  const int64_t t_col = (kl.n_col + kTileKeys - 1) / kTileKeys;
-  const int64_t ntiles = t_init + t_diag + t_col;
+  // Every count below fits in 32 bits (the host checks Sk < 2^24).
+  const int n_init = int(kl.n_init), n_diag = int(kl.n_diag), n_col = int(kl.n_col);
+  const int diag0 = int(kl.diag0);
+  const int t_init = (n_init + kTileKeys - 1) / kTileKeys;
+  const int t_diag = (n_diag + kTileKeys - 1) / kTileKeys;
+  const int t_col = (n_col + kTileKeys - 1) / kTileKeys;
+  const int ntiles = t_init + t_diag + t_col;
 
-  // Q^T operand: lane holds row (32*wave + l32), features [16s + 8hh, +8).
-  const int qrow_local = 32 * wave + l32;
+  auto tile_info = [&](int t) -> TileInfo {
+    TileInfo ti;
+    ti.dshift = 0;
+    ti.diag = false;
+    int l;
+    if (t < t_init) {
+      l = n_init - t * kTileKeys;
+    } else if (t < t_init + t_diag) {
+      ti.dshift = (t - t_init) * kTileKeys;
+      l = n_diag - ti.dshift;
+      ti.diag = causal != 0;
+    } else {
+      l = n_col - (t - t_init - t_diag) * kTileKeys;
+    }
+    ti.lim = l > kTileKeys ? kTileKeys : l;
+    return ti;
+  };
+
+  // ---- buffers -------------------------------------------------------------
+  const T* kh = k + b * skb + hk * skh;
+  const T* vh = v + b * svb + hk * svh;
+  const uint32_t krb = uint32_t(sks * 2), vrb = uint32_t(svs * 2);  // row bytes
+  const __amdgpu_buffer_rsrc_t krs = make_rsrc(kh, uint32_t(((Sk - 1) * sks + D) * 2));
+  const __amdgpu_buffer_rsrc_t vrs = make_rsrc(vh, uint32_t(((Sk - 1) * svs + D) * 2));
+  const __amdgpu_buffer_rsrc_t irs = make_rsrc(cols, uint32_t(n_col) * 4u);
+  const uint32_t smem_lds = lds_addr(smem);
+
+  // Copy geometry.  Copy x of this wave fills rows [(wave*H + x)*RPC, +RPC) of
+  // a tile; this lane fetches physical chunk p of row R_x, i.e. logical chunk
+  // p ^ (R_x % NCH).  The H key ids a lane needs sit contiguously in `ids` at
+  // position (wave*RPC + qr)*H + x, where qr = lane / NCH.
+  const int qr = lane / NCH, pc = lane % NCH;
+  int crow[H];
+  uint32_t cchunk[H];
+#pragma unroll
+  for (int x = 0; x < H; ++x) {
+    crow[x] = (wave * H + x) * RPC + qr;
+    cchunk[x] = uint32_t(16 * (pc ^ (crow[x] % NCH)));
+  }
+  const int id_pos = (wave * RPC + qr) * H;
+  // Inverse map for the lanes of wave 0 that write ids: position -> slot.
+  const int w_slot = [&] {
+    const int w = lane / (RPC * H), r = (lane / H) % RPC, x = lane % H;
+    return (w * H + x) * RPC + r;
+  }();
+
+  // Stage the key ids of tile u into ids[slot] (wave 0 only).
+  auto stage_ids = [&](int u, int slot) {
+    int32_t* dst = ids + slot * kTileKeys;
+    if (u < t_init) {
+      dst[lane] = u * kTileKeys + w_slot;
+    } else if (u < t_init + t_diag) {
+      dst[lane] = diag0 + (u - t_init) * kTileKeys + w_slot;
+    } else {
+      const uint32_t p = uint32_t((u - t_init - t_diag) * kTileKeys + w_slot);
+      copy4_to_lds(irs, lds_addr(dst), p * 4u);
+    }
+  };
+
+  // Issue the K and V copies of tile u into stage `st`, ids from ids[slot].
+  auto issue_tile = [&](int u, int st, int slot) {
+    const TileInfo ti = tile_info(u);
+    int32_t key[H];
+#pragma unroll
+    for (int x = 0; x < H; ++x) key[x] = ids[slot * kTileKeys + id_pos + x];
+    const uint32_t kdst = smem_lds + uint32_t(st * S::kStageBytes);
+    const uint32_t vdst = kdst + uint32_t(S::kTileBytes);
+#pragma unroll
+    for (int x = 0; x < H; ++x) {
+      const bool ok = crow[x] < ti.lim && uint32_t(key[x]) < uint32_t(Sk);
+      const uint32_t kof = ok ? __umul24(uint32_t(key[x]), krb) + cchunk[x] : kOutOfRange;
+      const uint32_t vof = ok ? __umul24(uint32_t(key[x]), vrb) + cchunk[x] : kOutOfRange;
+      copy16_to_lds(krs, kdst + uint32_t((wave * H + x) * 1024), kof);
+      copy16_to_lds(vrs, vdst + uint32_t((wave * H + x) * 1024), vof);
+    }
+  };
+
+  // ---- Q^T operand: lane holds row 32rh + l32, features [16s + 8hh, +8) ----
+  const int qrow_local = 32 * rh + l32;
   const int64_t qpos = J * QPS + qrow_local;
   vec qreg[D / 16];
   {
-    const T* qr = q + b * sqb + h * sqh + qpos * sqs;
+    const T* qr_ptr = q + b * sqb + h * sqh + qpos * sqs;
 #pragma unroll
     for (int s = 0; s < D / 16; ++s) {
       uint4 raw = make_uint4(0, 0, 0, 0);
-      if (qpos < Sq) raw = *reinterpret_cast<const uint4*>(qr + 16 * s + 8 * hh);
+      if (qpos < Sq) raw = *reinterpret_cast<const uint4*>(qr_ptr + 16 * s + 8 * hh);
       qreg[s] = __builtin_bit_cast(vec, raw);
     }
+    // Wait for Q here: otherwise the compiler places the wait at the first
+    // MFMA inside the tile loop, where it would also wait for the K/V copies
+    // in flight.
+#pragma unroll
+    for (int s = 0; s < D / 16; ++s) asm volatile("" ::"v"(qreg[s]));
   }
 
-  const T* kh = k + b * skb + hk * skh;
-  const T* vh = v + b * svb + hk * svh;
-
-  // Key of tile-relative slot kk of tile t (-1 if the slot is empty).
-  auto tile_key = [&](int64_t t, int kk) -> int64_t {
-    if (t < t_init) {
-      const int64_t p = t * kTileKeys + kk;
-      return p < kl.n_init ? p : -1;
-    }
-    if (t < t_init + t_diag) {
-      const int64_t p = (t - t_init) * kTileKeys + kk;
-      return p < kl.n_diag ? kl.diag0 + p : -1;
-    }
-    const int64_t p = (t - t_init - t_diag) * kTileKeys + kk;
-    if (p >= kl.n_col) return -1;
-    const int64_t key = kl.cols[p];
-    return (key >= 0 && key < Sk) ? key : -1;  // never read outside K / V
-  };
-
-  uint4 kbuf[KLOADS];
-  uint4 vbuf[VUNITS][4];
-
-  auto load_tile = [&](const int32_t* ids) {
+  // LDS read offsets inside a stage.  K (A operand of S^T): row 32kc + l32,
+  // chunk 2s + hh.  V^T (A operand of O^T) via the transposing read: lane
+  // group g16 = lane / 16 reads rows 32kc + 16sub + 8r + 4hh + j with
+  // j = (lane % 16) / 4, features 32i + 16(g16 % 2) + 4(lane % 4).
+  uint32_t koff[D / 16];
 #pragma unroll
-    for (int x = 0; x < KLOADS; ++x) {
-      const int c = tid + NT * x;
-      if (KTOTAL % NT != 0 && c >= KTOTAL) break;
-      const int kk = c / DCH, dc = c % DCH;
-      const int64_t key = ids[kk];
-      kbuf[x] = key >= 0 ? *reinterpret_cast<const uint4*>(kh + key * sks + dc * 8)
-                         : make_uint4(0, 0, 0, 0);
-    }
+  for (int s = 0; s < D / 16; ++s) {
+    const int R = 32 * kc + l32;
+    koff[s] = uint32_t(R * S::kRowBytes + 16 * ((2 * s + hh) ^ (R % NCH)));
+  }
+  uint32_t voff[D / 32][2];
+  {
+    const int j = (lane % 16) / 4, g2 = 2 * ((lane / 16) % 2) + (lane % 4) / 2;
 #pragma unroll
-    for (int x = 0; x < VUNITS; ++x) {
-      const int u = tid + NT * x;
-      if (VTOTAL % NT != 0 && u >= VTOTAL) break;
-      const int kq = u % (kTileKeys / 4), dc = u / (kTileKeys / 4);
+    for (int i = 0; i < D / 32; ++i)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int64_t key = ids[4 * kq + i];
-        vbuf[x][i] = key >= 0 ? *reinterpret_cast<const uint4*>(vh + key * svs + dc * 8)
-                              : make_uint4(0, 0, 0, 0);
+      for (int r = 0; r < 2; ++r) {
+        const int R = 32 * kc + 8 * r + 4 * hh + j;  // + 16 sub (a multiple of NCH)
+        const int c = 4 * i + g2;
+        voff[i][r] = uint32_t(S::kTileBytes + R * S::kRowBytes + 16 * (c ^ (R % NCH)) +
+                              8 * (lane % 2));
       }
-    }
-  };
-  auto store_tile = [&]() {
-#pragma unroll
-    for (int x = 0; x < KLOADS; ++x) {
-      const int c = tid + NT * x;
-      if (KTOTAL % NT != 0 && c >= KTOTAL) break;
-      const int kk = c / DCH, dc = c % DCH;
-      *reinterpret_cast<uint4*>(&Ks[kk * KS + dc * 8]) = kbuf[x];
-    }
-#pragma unroll
-    for (int x = 0; x < VUNITS; ++x) {
-      const int u = tid + NT * x;
-      if (VTOTAL % NT != 0 && u >= VTOTAL) break;
-      const int kq = u % (kTileKeys / 4), dc = u / (kTileKeys / 4);
-      const int pos = perm_key(4 * kq);  // quads stay contiguous under the swap
-      const uint16_t* e0 = reinterpret_cast<const uint16_t*>(&vbuf[x][0]);
-      const uint16_t* e1 = reinterpret_cast<const uint16_t*>(&vbuf[x][1]);
-      const uint16_t* e2 = reinterpret_cast<const uint16_t*>(&vbuf[x][2]);
-      const uint16_t* e3 = reinterpret_cast<const uint16_t*>(&vbuf[x][3]);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        uint2 w;
-        w.x = uint32_t(e0[e]) | (uint32_t(e1[e]) << 16);
-        w.y = uint32_t(e2[e]) | (uint32_t(e3[e]) << 16);
-        *reinterpret_cast<uint2*>(&Vt[(dc * 8 + e) * VS + pos]) = w;
-      }
-    }
-  };
+  }
 
   f32x16_t o[D / 32];
 #pragma unroll
   for (int i = 0; i < D / 32; ++i)
 #pragma unroll
     for (int e = 0; e < 16; ++e) o[i][e] = 0.f;
-  float m_run = -__builtin_inff(), l_run = 0.f;
+  float mc = -__builtin_inff();  // running maximum, scaled (log2) units
+  float lsum = 0.f;              // this lane's share of the row sum
 
-  // Key ids run two tiles ahead of the K/V gathers: the id of tile t+2 is
-  // read from the index list one iteration before it is needed.
-  int32_t nid = -1;
-  if (ntiles > 0) {
-    if (tid < kTileKeys) {
-      kid[0][tid] = int32_t(tile_key(0, tid));
-      kid[1][tid] = ntiles > 1 ? int32_t(tile_key(1, tid)) : -1;
-      nid = ntiles > 2 ? int32_t(tile_key(2, tid)) : -1;
-    }
-    lds_barrier();
-    load_tile(kid[0]);
-    store_tile();
-    lds_barrier();
-  }
-
-  for (int64_t t = 0; t < ntiles; ++t) {
-    const bool more = (t + 1) < ntiles;
-    if (more) load_tile(kid[(t + 1) & 1]);  // in flight while this tile computes
-
-    // ---- S^T = K Q^T for the two 32-key halves -----------------------------
-    f32x16_t s[2];
+  auto compute_tile = [&](int t, const unsigned char* stage) {
+    const TileInfo ti = tile_info(t);
+    f32x16_t s;
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
+    for (int e = 0; e < 16; ++e) s[e] = 0.f;
 #pragma unroll
-      for (int e = 0; e < 16; ++e) s[kb][e] = 0.f;
-      const uint16_t* krow = &Ks[(kb * 32 + l32) * KS + 8 * hh];
-#pragma unroll
-      for (int st = 0; st < D / 16; ++st) {
-        const vec a = __builtin_bit_cast(vec, *reinterpret_cast<const uint4*>(krow + 16 * st));
-        s[kb] = M::run(a, qreg[st], s[kb]);
-      }
+    for (int st = 0; st < D / 16; ++st) {
+      const vec a = __builtin_bit_cast(vec, *reinterpret_cast<const uint4*>(stage + koff[st]));
+      s = M::run(a, qreg[st], s);
     }
-
-    // ---- masking: empty slots, causal diagonal ------------------------------
-    int lim;      // valid slots in this tile
-    int dshift;   // for diagonal tiles: key - diag0 = dshift + slot
-    bool diag = false;
-    if (t < t_init) {
-      const int64_t l = kl.n_init - t * kTileKeys;
-      lim = l > kTileKeys ? kTileKeys : int(l);
-      dshift = 0;
-    } else if (t < t_init + t_diag) {
-      dshift = int(t - t_init) * kTileKeys;
-      const int64_t l = kl.n_diag - dshift;
-      lim = l > kTileKeys ? kTileKeys : int(l);
-      diag = causal != 0;
-    } else {
-      const int64_t l = kl.n_col - (t - t_init - t_diag) * kTileKeys;
-      lim = l > kTileKeys ? kTileKeys : int(l);
-      dshift = 0;
-    }
+    // Masking: empty slots, causal diagonal.  Slot of s[e]: 32kc + 8(e/4) + 4hh + e%4.
     float tmax = -__builtin_inff();
-    if (!diag && lim == kTileKeys) {  // full tile, nothing masked
+    if (!ti.diag && ti.lim == kTileKeys) {
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const float x = s[kb][e] * scale_log2;
-          s[kb][e] = x;
-          tmax = __builtin_fmaxf(tmax, x);
-        }
+      for (int e = 0; e < 16; ++e) tmax = __builtin_fmaxf(tmax, s[e]);
     } else {
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const int slot = kb * 32 + 8 * (e / 4) + 4 * hh + (e % 4);
-          bool ok = slot < lim;
-          if (diag) ok = ok && (dshift + slot <= qrow_local);
-          const float x = ok ? s[kb][e] * scale_log2 : -__builtin_inff();
-          s[kb][e] = x;
-          tmax = __builtin_fmaxf(tmax, x);
-        }
-      }
-    }
-    tmax = __builtin_fmaxf(tmax, __shfl_xor(tmax, 32));
-    const float m_new = __builtin_fmaxf(m_run, tmax);
-    const float m_use = (m_new == -__builtin_inff()) ? 0.f : m_new;
-    const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
-    float lsum = 0.f;
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
-        const float p = __builtin_amdgcn_exp2f(s[kb][e] - m_use);
-        s[kb][e] = p;
-        lsum += p;
+        const int slot = 32 * kc + 8 * (e / 4) + 4 * hh + (e % 4);
+        bool ok = slot < ti.lim;
+        if (ti.diag) ok = ok && (ti.dshift + slot <= qrow_local);
+        s[e] = ok ? s[e] : -__builtin_inff();
+        tmax = __builtin_fmaxf(tmax, s[e]);
       }
     }
-    lsum += __shfl_xor(lsum, 32);
-    l_run = l_run * alpha + lsum;
-    m_run = m_new;
-    if (__ballot(alpha != 1.f)) {  // some row's maximum moved
+    const float tsc = max_halves(tmax) * scale_log2;
+    if (__builtin_amdgcn_ballot_w64(tsc > mc + kRescaleSlack)) {  // some row's maximum moved
+      const float mnew = __builtin_fmaxf(mc, tsc);
+      const float alpha = (mnew == mc) ? 1.f : __builtin_amdgcn_exp2f(mc - mnew);
 #pragma unroll
       for (int i = 0; i < D / 32; ++i)
 #pragma unroll
         for (int e = 0; e < 16; ++e) o[i][e] *= alpha;
+      lsum *= alpha;
+      mc = mnew;
     }
-
-    // ---- O^T += V^T P^T ------------------------------------------------------
+    const float mneg = (mc == -__builtin_inff()) ? 0.f : -mc;
 #pragma unroll
-    for (int st = 0; st < 4; ++st) {
-      const int kb = st / 2, sub = st % 2;
+    for (int e = 0; e < 16; ++e) {
+      const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[e], scale_log2, mneg));
+      s[e] = p;
+      lsum += p;
+    }
+    // O^T += V^T P^T, 16 keys per step: k-slot 8hh + e of step sub is key
+    // 32kc + 16sub + 8(e/4) + 4hh + e%4, i.e. accumulator entries 8sub .. 8sub+7.
+#pragma unroll
+    for (int sub = 0; sub < 2; ++sub) {
       float pv[8];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        pv[e] = s[kb][4 * (2 * sub) + e];
-        pv[4 + e] = s[kb][4 * (2 * sub + 1) + e];
-      }
+      for (int e = 0; e < 8; ++e) pv[e] = s[8 * sub + e];
       const vec bfrag = M::pack(pv);
 #pragma unroll
       for (int i = 0; i < D / 32; ++i) {
-        const uint16_t* vrow = &Vt[(i * 32 + l32) * VS + 16 * st + 8 * hh];
-        const vec a = __builtin_bit_cast(vec, *reinterpret_cast<const uint4*>(vrow));
-        o[i] = M::run(a, bfrag, o[i]);
+        const unsigned char* p0 = stage + voff[i][0] + sub * 16 * S::kRowBytes;
+        const unsigned char* p1 = stage + voff[i][1] + sub * 16 * S::kRowBytes;
+        const s16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) s16x4_t*)(p0));
+        const s16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) s16x4_t*)(p1));
+        const s16x4_t both[2] = {lo, hi};
+        o[i] = M::run(__builtin_bit_cast(vec, both), bfrag, o[i]);
       }
     }
+  };
 
-    __syncthreads();  // K/V of tile t+1 have arrived; Ks/Vt of tile t are free
-    if (tid < kTileKeys) {
-      kid[t & 1][tid] = nid;  // ids of tile t+2 (slot t & 1 was consumed by load_tile(t))
-      nid = (t + 3 < ntiles) ? int32_t(tile_key(t + 3, tid)) : -1;
+  // ---- pipeline ------------------------------------------------------------
+  if (ntiles > 0) {
+    if (wave == 0) {
+      stage_ids(0, 0);
+      if (ntiles > 1) stage_ids(1, 1);
     }
-    if (more) store_tile();
-    lds_barrier();
+    vm_lds_barrier();
+    issue_tile(0, 0, 0);
+  }
+  for (int t = 0; t < ntiles; ++t) {
+    vm_lds_barrier();  // tile t landed in stage t&1; stage (t+1)&1 and ids slot t&1 are free
+    if (t + 1 < ntiles) issue_tile(t + 1, (t + 1) & 1, (t + 1) & 1);
+    if (wave == 0 && t + 2 < ntiles) stage_ids(t + 2, t & 1);
+    compute_tile(t, smem + (t & 1) * S::kStageBytes);
   }
 
-  // ---- epilogue: O / l, four consecutive features per store ----------------
-  if (qpos < Sq) {
-    const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
-    T* orow = out + b * sob + h * soh + qpos * sos;
+  // ---- merge the two key halves, normalise, store --------------------------
+  lds_barrier();  // every wave is done with the stages
+  float* mo = reinterpret_cast<float*>(smem) + rh * 64 * (D / 2 + 2);
+  if (kc == 1) {
 #pragma unroll
-    for (int i = 0; i < D / 32; ++i) {
+    for (int i = 0; i < D / 32; ++i)
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int d0 = i * 32 + 8 * g + 4 * hh;
-        uint2 w;
-        const T e0 = Round<T>::store(o[i][4 * g + 0] * inv);
-        const T e1 = Round<T>::store(o[i][4 * g + 1] * inv);
-        const T e2 = Round<T>::store(o[i][4 * g + 2] * inv);
-        const T e3 = Round<T>::store(o[i][4 * g + 3] * inv);
-        w.x = uint32_t(e0.bits) | (uint32_t(e1.bits) << 16);
-        w.y = uint32_t(e2.bits) | (uint32_t(e3.bits) << 16);
-        *reinterpret_cast<uint2*>(orow + d0) = w;
+      for (int g = 0; g < 4; ++g)
+        *reinterpret_cast<float4*>(mo + ((4 * i + g) * 64 + lane) * 4) =
+            make_float4(o[i][4 * g], o[i][4 * g + 1], o[i][4 * g + 2], o[i][4 * g + 3]);
+    mo[64 * (D / 2) + lane] = mc;
+    mo[64 * (D / 2) + 64 + lane] = lsum;
+  }
+  lds_barrier();
+  if (kc == 0) {
+    const float m1 = mo[64 * (D / 2) + lane], l1 = mo[64 * (D / 2) + 64 + lane];
+    const float m = __builtin_fmaxf(mc, m1);
+    const float a0 = (mc == m) ? 1.f : __builtin_amdgcn_exp2f(mc - m);
+    const float a1 = (m1 == m) ? 1.f : __builtin_amdgcn_exp2f(m1 - m);
+    const float l = sum_halves(lsum * a0 + l1 * a1);
+    const float inv = l > 0.f ? 1.f / l : 0.f;
+    const float c0 = a0 * inv, c1 = a1 * inv;
+    if (qpos < Sq) {
+      T* orow = out + b * sob + h * soh + qpos * sos;
+#pragma unroll
+      for (int i = 0; i < D / 32; ++i) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const float4 x1 = *reinterpret_cast<const float4*>(mo + ((4 * i + g) * 64 + lane) * 4);
+          const int d0 = i * 32 + 8 * g + 4 * hh;
+          const T e0 = Round<T>::store(o[i][4 * g + 0] * c0 + x1.x * c1);
+          const T e1 = Round<T>::store(o[i][4 * g + 1] * c0 + x1.y * c1);
+          const T e2 = Round<T>::store(o[i][4 * g + 2] * c0 + x1.z * c1);
+          const T e3 = Round<T>::store(o[i][4 * g + 3] * c0 + x1.w * c1);
+          uint2 w;
+          w.x = uint32_t(e0.bits) | (uint32_t(e1.bits) << 16);
+          w.y = uint32_t(e2.bits) | (uint32_t(e3.bits) << 16);
+          *reinterpret_cast<uint2*>(orow + d0) = w;
+        }
       }
     }
   }
@@ -326,7 +428,8 @@ static hipError_t launch_attn_mfma_tdq(const void* q, const int64_t* sq, const v
                                        const int32_t* indices, const RowLayout& lay,
                                        hipStream_t stream) {
   const int64_t nblocks = WorkOrder{lay.nc, B, Hq, Hk}.grid_items();
-  hipLaunchKernelGGL((attn_mfma_kernel<T, D, QPS>), dim3(unsigned(nblocks)), dim3(QPS * 2), 0,
+  hipLaunchKernelGGL((attn_mfma_kernel<T, D, QPS>), dim3(unsigned(nblocks)),
+                     dim3(AttnShape<D, QPS>::kThreads), 0,
                      stream, static_cast<const T*>(q), sq[0], sq[1], sq[2],
                      static_cast<const T*>(k), sk[0], sk[1], sk[2], static_cast<const T*>(v),
                      sv[0], sv[1], sv[2], static_cast<T*>(out), so[0], so[1], so[2], B, Hq, Hk,

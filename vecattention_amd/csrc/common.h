@@ -63,6 +63,13 @@ __device__ inline void lds_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
+// Work-group barrier after this wave's global loads into LDS
+// (buffer_load ... lds) and its LDS operations have completed: afterwards the
+// LDS data written by every wave's copies is visible to all waves.
+__device__ inline void vm_lds_barrier() {
+  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 // ---------------------------------------------------------------------------
 // Work order.  Work-groups are dispatched round-robin over the 8 XCDs of the
 // chip (block i runs on XCD i % 8), each with its own L2.  A work item is
