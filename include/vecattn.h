@@ -43,7 +43,7 @@ enum {
 };
 
 enum { VA_ATTN_AUTO = 0, VA_ATTN_MFMA = 1, VA_ATTN_SIMPLE = 2 };
-enum { VA_SEL_AUTO = 0, VA_SEL_EXACT = 1, VA_SEL_MFMA = 2 };
+enum { VA_SEL_AUTO = 0, VA_SEL_EXACT = 1, VA_SEL_MFMA = 2, VA_SEL_WAVE = 3 };
 
 /* Library version (major*10000 + minor*100 + patch). */
 int va_version(void);
@@ -87,7 +87,12 @@ int va_pool(int dtype, const void* q, int64_t B, int64_t H, int64_t S, int64_t D
  *   VA_SEL_MFMA  : bf16/fp16 MFMA scores with a certified error band and exact
  *                  fp64 recomputation inside the band (D in {64,128},
  *                  k_local_size in {16,32,64}); needs `scratch`;
- *   VA_SEL_AUTO  : MFMA when supported and scratch is given, else exact.
+ *   VA_SEL_WAVE  : the same certified scheme organised one wave per 32 rows
+ *                  (additionally k_local_size * group_k_block a multiple of
+ *                  64, Sk < 2^24, < 2 GiB of key rows per kv head); needs
+ *                  `scratch`;
+ *   VA_SEL_AUTO  : WAVE, else MFMA, when supported and scratch is given, else
+ *                  exact.
  * scratch: device fp32 buffer of va_select_scratch_floats(B, Hk) floats (key
  * norms), or NULL.
  */

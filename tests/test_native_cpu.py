@@ -86,6 +86,8 @@ def test_select_argument_errors_before_launch(L):
     assert _null_select(L, D=512) == nat.VA_ERR_UNSUPPORTED
     assert _null_select(L, kernel=nat.VA_SEL_MFMA) == nat.VA_ERR_ARG            # no scratch
     assert _null_select(L, kernel=nat.VA_SEL_MFMA, dtype=nat.VA_F32) == nat.VA_ERR_UNSUPPORTED
+    assert _null_select(L, kernel=nat.VA_SEL_WAVE) == nat.VA_ERR_ARG            # no scratch
+    assert _null_select(L, kernel=nat.VA_SEL_WAVE, G=5) == nat.VA_ERR_UNSUPPORTED  # span 80 keys
     assert _null_select(L, kernel=9) == nat.VA_ERR_ARG
 
 

@@ -16,7 +16,7 @@ LIB_PATH = os.path.join(_HERE, "libvecattn.so")
 VA_F32, VA_BF16, VA_F16 = 0, 1, 2
 VA_OK, VA_ERR_ARG, VA_ERR_UNSUPPORTED, VA_ERR_HIP, VA_ERR_WORKSPACE = 0, -1, -2, -3, -4
 VA_ATTN_AUTO, VA_ATTN_MFMA, VA_ATTN_SIMPLE = 0, 1, 2
-VA_SEL_AUTO, VA_SEL_EXACT, VA_SEL_MFMA = 0, 1, 2
+VA_SEL_AUTO, VA_SEL_EXACT, VA_SEL_MFMA, VA_SEL_WAVE = 0, 1, 2, 3
 
 _DTYPES = {torch.float32: VA_F32, torch.bfloat16: VA_BF16, torch.float16: VA_F16}
 

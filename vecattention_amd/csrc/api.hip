@@ -33,6 +33,13 @@ hipError_t launch_select_mfma(int dtype, const void* qs, int64_t sqb, int64_t sq
                               int64_t bk, int64_t group, int causal, int64_t bsq, float gap,
                               const float* gaps, const float* kmax, const RowLayout& lay,
                               int32_t* counts, int32_t* indices, hipStream_t stream);
+bool select_wave_supported(int dtype, int64_t D, int64_t bk, int64_t group);
+hipError_t launch_select_wave(int dtype, const void* qs, int64_t sqb, int64_t sqh, int64_t sqn,
+                              const void* k, int64_t skb, int64_t skh, int64_t sks, int64_t B,
+                              int64_t Hq, int64_t Hk, int64_t Sk, int64_t D, int64_t qps,
+                              int64_t bk, int64_t group, int causal, int64_t bsq, float gap,
+                              const float* gaps, const float* kmax, const RowLayout& lay,
+                              int32_t* counts, int32_t* indices, hipStream_t stream);
 int64_t key_norm_scratch_floats(int64_t B, int64_t Hk);
 hipError_t launch_key_norm(int dtype, const void* k, int64_t skb, int64_t skh, int64_t sks,
                            int64_t B, int64_t Hk, int64_t Sk, int64_t D, float* scratch,
@@ -163,24 +170,40 @@ int64_t va_select_scratch_floats(int64_t B, int64_t Hk) {
   return va::key_norm_scratch_floats(B, Hk);
 }
 
-// Selection with the key norms (MFMA path) already in scratch[0 .. B*Hk).
+// A group longer than the key range is a single group: any value covering
+// every tile gives the same selection.  Capped so that bk * group stays small,
+// and to a multiple of 4 tiles so that the capped span stays a multiple of 64
+// keys (the wave kernel starts groups at 64-key chunk boundaries).
+static int64_t effective_group(int64_t group, int64_t Sk, int64_t bk) {
+  const int64_t gmax = (cdiv(Sk, bk) + 1 + 3) / 4 * 4;
+  return group > gmax ? gmax : group;
+}
+
+enum SelKernel { kSelExact = VA_SEL_EXACT, kSelMfma = VA_SEL_MFMA, kSelWave = VA_SEL_WAVE };
+
+// Selection with the key norms (MFMA paths) already in kmax[0 .. B*Hk).
 static int select_impl(int dtype, const void* qs, int64_t sqb, int64_t sqh, int64_t sqn,
                        const void* k, int64_t skb, int64_t skh, int64_t sks, int64_t B,
                        int64_t Hq, int64_t Hk, int64_t Sk, int64_t D, int64_t qps, int64_t bk,
                        int64_t group, int causal, int wo_init, int64_t J0, int64_t nc,
                        int64_t bsq, float gap, const float* gaps, int64_t dense_stride,
-                       int32_t* counts, int32_t* indices, bool use_mfma, const float* kmax,
+                       int32_t* counts, int32_t* indices, SelKernel which, const float* kmax,
                        hipStream_t stream) {
   const va::RowLayout lay = make_layout(J0, nc, qps, Sk, causal, wo_init, dense_stride);
-  // A group longer than the key range is one group; cap it so bk * group fits.
-  if (group > cdiv(Sk, bk) + 1) group = cdiv(Sk, bk) + 1;
-  hipError_t e =
-      use_mfma ? va::launch_select_mfma(dtype, qs, sqb, sqh, sqn, k, skb, skh, sks, B, Hq, Hk, Sk,
-                                        D, qps, bk, group, causal, bsq, gap, gaps, kmax, lay,
-                                        counts, indices, stream)
-               : va::launch_select_exact(dtype, qs, sqb, sqh, sqn, k, skb, skh, sks, B, Hq, Hk,
-                                         Sk, D, qps, bk, group, causal, bsq, gap, gaps, lay,
-                                         counts, indices, stream);
+  group = effective_group(group, Sk, bk);
+  hipError_t e;
+  if (which == kSelWave)
+    e = va::launch_select_wave(dtype, qs, sqb, sqh, sqn, k, skb, skh, sks, B, Hq, Hk, Sk, D, qps,
+                               bk, group, causal, bsq, gap, gaps, kmax, lay, counts, indices,
+                               stream);
+  else if (which == kSelMfma)
+    e = va::launch_select_mfma(dtype, qs, sqb, sqh, sqn, k, skb, skh, sks, B, Hq, Hk, Sk, D, qps,
+                               bk, group, causal, bsq, gap, gaps, kmax, lay, counts, indices,
+                               stream);
+  else
+    e = va::launch_select_exact(dtype, qs, sqb, sqh, sqn, k, skb, skh, sks, B, Hq, Hk, Sk, D,
+                                qps, bk, group, causal, bsq, gap, gaps, lay, counts, indices,
+                                stream);
   return hip_check(e, "select launch");
 }
 
@@ -191,6 +214,17 @@ static bool select_mfma_ok(int dtype, const void* qs, int64_t sqb, int64_t sqh, 
   return va::select_mfma_supported(dtype, D, bk) && reinterpret_cast<uintptr_t>(qs) % 16 == 0 &&
          reinterpret_cast<uintptr_t>(k) % 16 == 0 && sqb % a == 0 && sqh % a == 0 &&
          sqn % a == 0 && skb % a == 0 && skh % a == 0 && sks % a == 0;
+}
+
+// The wave kernel copies K rows into LDS with 32-bit buffer offsets computed
+// from keys up to Sk + 64: each kv head's rows (and one chunk past the end)
+// must span < 2 GiB, and rows must not overlap (sks >= D).
+static bool select_wave_ok(int dtype, const void* qs, int64_t sqb, int64_t sqh, int64_t sqn,
+                           const void* k, int64_t skb, int64_t skh, int64_t sks, int64_t Sk,
+                           int64_t D, int64_t bk, int64_t group) {
+  return select_mfma_ok(dtype, qs, sqb, sqh, sqn, k, skb, skh, sks, D, bk) &&
+         va::select_wave_supported(dtype, D, bk, effective_group(group, Sk, bk)) && sks >= D &&
+         Sk < (int64_t(1) << 24) && (Sk + 64) * sks * esize(dtype) < (int64_t(1) << 31);
 }
 
 int va_select(int dtype, const void* qs, int64_t sqb, int64_t sqh, int64_t sqn,
@@ -209,29 +243,36 @@ int va_select(int dtype, const void* qs, int64_t sqb, int64_t sqh, int64_t sqn,
   const bool have_scratch = scratch != nullptr &&
                             scratch_floats >= va::key_norm_scratch_floats(B, Hk);
   const bool mfma_ok = select_mfma_ok(dtype, qs, sqb, sqh, sqn, k, skb, skh, sks, D, bk);
-  bool use_mfma;
+  const bool wave_ok =
+      select_wave_ok(dtype, qs, sqb, sqh, sqn, k, skb, skh, sks, Sk, D, bk, group);
+  SelKernel which;
   if (kernel == VA_SEL_EXACT) {
-    use_mfma = false;
-  } else if (kernel == VA_SEL_MFMA) {
-    if (!mfma_ok)
+    which = kSelExact;
+  } else if (kernel == VA_SEL_MFMA || kernel == VA_SEL_WAVE) {
+    if (kernel == VA_SEL_MFMA && !mfma_ok)
       return fail(VA_ERR_UNSUPPORTED,
                   "MFMA selection needs bf16/fp16, D in {64,128}, k_local_size in {16,32,64} "
                   "and 16-byte aligned rows");
+    if (kernel == VA_SEL_WAVE && !wave_ok)
+      return fail(VA_ERR_UNSUPPORTED,
+                  "wave selection needs bf16/fp16, D in {64,128}, k_local_size in {16,32,64}, "
+                  "k_local_size * group_k_block a multiple of 64, 16-byte aligned rows, "
+                  "Sk < 2^24 and < 2 GiB of key rows per kv head");
     if (!have_scratch) return fail(VA_ERR_ARG, "MFMA selection needs scratch");
-    use_mfma = true;
+    which = kernel == VA_SEL_WAVE ? kSelWave : kSelMfma;
   } else if (kernel == VA_SEL_AUTO) {
-    use_mfma = mfma_ok && have_scratch;
+    which = (wave_ok && have_scratch) ? kSelWave : (mfma_ok && have_scratch) ? kSelMfma : kSelExact;
   } else {
     return fail(VA_ERR_ARG, "unknown selection kernel %d", kernel);
   }
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (use_mfma) {
+  if (which != kSelExact) {
     rc = hip_check(va::launch_key_norm(dtype, k, skb, skh, sks, B, Hk, Sk, D, scratch, st),
                    "key norm launch");
     if (rc) return rc;
   }
   rc = select_impl(dtype, qs, sqb, sqh, sqn, k, skb, skh, sks, B, Hq, Hk, Sk, D, qps, bk, group,
-                   causal, wo_init, J0, nc, bsq, gap, gaps, dense_stride, counts, indices, use_mfma,
+                   causal, wo_init, J0, nc, bsq, gap, gaps, dense_stride, counts, indices, which,
                    scratch, st);
   return rc ? rc : ok();
 }
@@ -375,8 +416,13 @@ int va_prefill(int dtype, const void* q, int64_t sqb, int64_t sqh, int64_t sqs, 
   rc = check_select_args(dtype, qs, k, B, Hq, Hk, Sk, D, qps, bk, group, causal, causal, 0,
                          cdiv(Sq, qps), bsq);
   if (rc) return rc;
-  const bool use_mfma = select_mfma_ok(dtype, qs, Hq * nqb * D, nqb * D, D, k, skb, skh, sks, D, bk);
-  if (use_mfma) {
+  const SelKernel which =
+      select_wave_ok(dtype, qs, Hq * nqb * D, nqb * D, D, k, skb, skh, sks, Sk, D, bk, group)
+          ? kSelWave
+      : select_mfma_ok(dtype, qs, Hq * nqb * D, nqb * D, D, k, skb, skh, sks, D, bk)
+          ? kSelMfma
+          : kSelExact;
+  if (which != kSelExact) {
     rc = hip_check(va::launch_key_norm(dtype, k, skb, skh, sks, B, Hk, Sk, D, knorm, st),
                    "key norm launch");
     if (rc) return rc;
@@ -389,7 +435,7 @@ int va_prefill(int dtype, const void* q, int64_t sqb, int64_t sqh, int64_t sqs, 
     const void* qs_chunk = static_cast<const char*>(qs) + J0 * D * es;
     rc = select_impl(dtype, qs_chunk, Hq * nqb * D, nqb * D, D, k, skb, skh, sks, B, Hq, Hk, Sk,
                      D, qps, bk, group, causal, causal, J0, nc, bsq, gap, gaps, 0, counts, indices,
-                     use_mfma, knorm, st);
+                     which, knorm, st);
     if (rc) return rc;
     rc = va_sparse_attn(dtype, q, sqb, sqh, sqs, k, skb, skh, sks, v, svb, svh, svs, out, sob,
                         soh, sos, B, Hq, Hk, Sq, Sk, D, qps, causal, causal, J0, nc, 0, counts,

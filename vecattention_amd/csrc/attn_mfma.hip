@@ -35,6 +35,7 @@
 //
 // Algorithmic work per gathered key: 4*D FLOPs per query row (QK^T and PV).
 #include "keylist.h"
+#include "lanes.h"
 #include "mfma.h"
 
 namespace va {
@@ -43,7 +44,6 @@ constexpr int kTileKeys = 64;
 constexpr uint32_t kOutOfRange = 0xfffffff0u;  // voffset past every buffer's range
 constexpr float kRescaleSlack = 8.f;           // log2 of the largest kept probability
 
-typedef __attribute__((address_space(3))) void* lds_void_ptr;
 typedef short s16x4_t __attribute__((ext_vector_type(4)));
 
 template <int D, int QPS>
@@ -63,56 +63,6 @@ struct AttnShape {
   static_assert(kCopiesPerWave >= 1 && kRowsPerCopy * kCopiesPerWave * kWaves == kTileKeys,
                 "tile copies must split evenly over the waves");
 };
-
-// Buffer resource of a raw buffer (stride 0, 32-bit data format) of `bytes`
-// bytes at `base`: loads at offsets >= bytes return 0.
-// Every field is made wave-uniform explicitly so that the resource lives in
-// SGPRs, as buffer instructions require.
-__device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
-  const uint64_t a = reinterpret_cast<uint64_t>(base);
-  const uint64_t lo = uint32_t(__builtin_amdgcn_readfirstlane(int(uint32_t(a))));
-  const uint64_t hi = uint32_t(__builtin_amdgcn_readfirstlane(int(uint32_t(a >> 32))));
-  return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(lo | (hi << 32)), (short)0,
-                                           __builtin_amdgcn_readfirstlane(int(bytes)),
-                                           0x00020000);
-}
-
-// LDS byte address of a pointer into __shared__ memory.
-__device__ inline uint32_t lds_addr(const void* p) {
-  return uint32_t(reinterpret_cast<uintptr_t>((lds_void_ptr)(const_cast<void*>(p))));
-}
-
-// Global -> LDS copies (buffer_load ... lds): lane i writes `size` bytes at LDS
-// address lds + size*i, read from buffer offset voffset.  Issued from inline
-// assembly so that the compiler's memory-counter bookkeeping does not make
-// LDS reads of the other stage wait for these copies; completion is awaited
-// explicitly with vm_lds_barrier().  M0 (the LDS base) is set in the same
-// statement; nothing else in these kernels uses M0.
-__device__ inline void copy16_to_lds(__amdgpu_buffer_rsrc_t r, uint32_t lds, uint32_t voffset) {
-  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
-               :
-               : "s"(__builtin_amdgcn_readfirstlane(int(lds))), "v"(voffset), "s"(r)
-               : "memory");
-}
-__device__ inline void copy4_to_lds(__amdgpu_buffer_rsrc_t r, uint32_t lds, uint32_t voffset) {
-  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen lds"
-               :
-               : "s"(__builtin_amdgcn_readfirstlane(int(lds))), "v"(voffset), "s"(r)
-               : "memory");
-}
-
-// Max of x over lanes l and l ^ 32.
-__device__ inline float max_halves(float x) {
-  const uint32_t u = __builtin_bit_cast(uint32_t, x);
-  const auto p = __builtin_amdgcn_permlane32_swap(u, u, false, false);
-  return __builtin_fmaxf(__builtin_bit_cast(float, (uint32_t)p[0]),
-                         __builtin_bit_cast(float, (uint32_t)p[1]));
-}
-__device__ inline float sum_halves(float x) {
-  const uint32_t u = __builtin_bit_cast(uint32_t, x);
-  const auto p = __builtin_amdgcn_permlane32_swap(u, u, false, false);
-  return __builtin_bit_cast(float, (uint32_t)p[0]) + __builtin_bit_cast(float, (uint32_t)p[1]);
-}
 
 // Per-tile facts shared by the copy and the compute of a tile: number of
 // valid slots, and for diagonal tiles the offset of slot 0 from the first

@@ -1,0 +1,74 @@
+// Wave-level helpers for gfx950 kernels: global -> LDS copies through buffer
+// resources, and exchanges between the two 32-lane halves of a wave.
+#pragma once
+#include "common.h"
+
+namespace va {
+
+typedef __attribute__((address_space(3))) void* lds_void_ptr;
+
+// Buffer resource of a raw buffer (stride 0, 32-bit data format) of `bytes`
+// bytes at `base`: loads at offsets >= bytes return 0.
+// Every field is made wave-uniform explicitly so that the resource lives in
+// SGPRs, as buffer instructions require.
+__device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  const uint64_t lo = uint32_t(__builtin_amdgcn_readfirstlane(int(uint32_t(a))));
+  const uint64_t hi = uint32_t(__builtin_amdgcn_readfirstlane(int(uint32_t(a >> 32))));
+  return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(lo | (hi << 32)), (short)0,
+                                           __builtin_amdgcn_readfirstlane(int(bytes)),
+                                           0x00020000);
+}
+
+// LDS byte address of a pointer into __shared__ memory.
+__device__ inline uint32_t lds_addr(const void* p) {
+  return uint32_t(reinterpret_cast<uintptr_t>((lds_void_ptr)(const_cast<void*>(p))));
+}
+
+// Global -> LDS copies (buffer_load ... lds): lane i writes `size` bytes at LDS
+// address lds + size*i, read from buffer offset voffset.  Issued from inline
+// assembly so that the compiler's memory-counter bookkeeping does not make
+// LDS reads of the other stage wait for these copies; completion is awaited
+// explicitly with vm_lds_barrier().  M0 (the LDS base) is set in the same
+// statement; nothing else in these kernels uses M0.
+__device__ inline void copy16_to_lds(__amdgpu_buffer_rsrc_t r, uint32_t lds, uint32_t voffset) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               :
+               : "s"(__builtin_amdgcn_readfirstlane(int(lds))), "v"(voffset), "s"(r)
+               : "memory");
+}
+__device__ inline void copy4_to_lds(__amdgpu_buffer_rsrc_t r, uint32_t lds, uint32_t voffset) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen lds"
+               :
+               : "s"(__builtin_amdgcn_readfirstlane(int(lds))), "v"(voffset), "s"(r)
+               : "memory");
+}
+
+// Max of x over lanes l and l ^ 32.
+__device__ inline float max_halves(float x) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, x);
+  const auto p = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return __builtin_fmaxf(__builtin_bit_cast(float, (uint32_t)p[0]),
+                         __builtin_bit_cast(float, (uint32_t)p[1]));
+}
+__device__ inline float sum_halves(float x) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, x);
+  const auto p = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return __builtin_bit_cast(float, (uint32_t)p[0]) + __builtin_bit_cast(float, (uint32_t)p[1]);
+}
+
+// Cross-lane helpers read other lanes' registers: call them where the whole
+// wave is active (never under a divergent branch or short-circuit operand).
+
+// Value of x held by lane l ^ 32.  The two results of v_permlane32_swap(x, x)
+// hold x[l] and x[l ^ 32] in every lane; XOR-ing both with x leaves the
+// partner's value whichever result carries which.
+__device__ inline uint32_t other_half(uint32_t x) {
+  const auto p = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+  return uint32_t(p[0]) ^ uint32_t(p[1]) ^ x;
+}
+__device__ inline float other_half(float x) {
+  return __builtin_bit_cast(float, other_half(__builtin_bit_cast(uint32_t, x)));
+}
+
+}  // namespace va

@@ -1,0 +1,521 @@
+// TilingSelect on bf16/fp16 MFMA, one wave per 32 pooled rows, certified
+// decisions.
+//
+// Same rule and output as select_exact.hip (spattn/src/kernels/
+// vecattention_kernels.py:206-272 / :275-345): per pooled row, keys visited in
+// tiles of BK, a running maximum restarted every G tiles and updated with the
+// whole tile's maximum before the compare, key c selected iff
+// fp32(s_c + gap) >= m, the truncating causal tile mask, keys past the end
+// neither selected nor counted.  The selected sets are bit-identical to the
+// canonical rule (sequential fp64 dot products rounded once to fp32).
+//
+// Organisation.  A work-group holds 4 waves and 128 consecutive pooled rows of
+// one q head; wave w owns rows [32w, 32w+32).  The keys are walked in chunks
+// of 64 (two 32-key blocks); each chunk of K is copied into LDS once for the
+// work-group (buffer_load ... lds, two stages, the next chunk in flight while
+// the current one is scored) and read by all four waves.  Within a wave the
+// keys are visited in order, so each row's running maximum is a register:
+// there is no cross-wave exchange at all.
+//
+// Scores.  S^T = K Q^T with v_mfma_f32_32x32x16: A = 32 key rows from LDS,
+// B = the wave's 32 pooled rows held in VGPRs for the whole kernel.  The key
+// rows of a block are stored in LDS permuted (row m holds key kperm(m)) so
+// that the accumulator of lane l holds row l % 32 and the 16 consecutive keys
+// 16 * (l / 32) + e: for BK = 16 a lane holds exactly one tile.
+//
+// Certified decisions.  For a row q and key k the MFMA score s^ satisfies
+// |s^ - s| <= delta with delta = (2*(D/16 + 2) + 1) * 2^-23 * ||q|| * Kmax
+// (see select_mfma.hip for the derivation and the calibration on gfx950).
+// A key is selected outright when s^ exceeds m^ - gap by more than a band of
+// 2*delta plus rounding slack, rejected when it is below by more, and is
+// "ambiguous" otherwise.  The exact decision needs the exact score (fp64
+// recomputation) and the exact running maximum M.  M can only be attained by
+// keys whose s^ is within `win` (>= 2*delta) of m^ at their own tile, so each
+// row keeps a short list of the tiles that contained such keys ("near-max
+// tiles"); when a row meets an ambiguous key, the exact scores of its listed
+// tiles are computed once and folded into an exact running maximum for the
+// rest of the group, and the list is cleared.  Everything exact runs on the
+// rare path of the wave that needs it.
+//
+// Output.  Each lane writes its selected keys straight to the row's index
+// list (ascending: the low half's tile before the high half's).
+#include "lanes.h"
+#include "mfma.h"
+
+namespace va {
+
+constexpr int kWRows = 32;         // pooled rows per wave
+constexpr int kWWaves = 4;         // waves per work-group
+constexpr int kWChunk = 64;        // keys per chunk
+constexpr int kWList = 16;         // near-max tiles per row
+
+// MFMA row m of the K operand -> key offset inside the 32-key block, such that
+// accumulator element e of lane l holds key 16*(l/32) + e.
+__device__ inline int wkperm(int m) { return 16 * ((m >> 2) & 1) + 4 * (m >> 3) + (m & 3); }
+
+// Canonical score from global memory: sequential fp64 FMAs over d (exact
+// products), one rounding to fp32.
+template <typename T, int D>
+__device__ inline float exact_dot_global(const T* __restrict__ q, const T* __restrict__ k) {
+  uint4 qr[D / 8], kr[D / 8];
+#pragma unroll
+  for (int c = 0; c < D / 8; ++c) {
+    qr[c] = *reinterpret_cast<const uint4*>(q + 8 * c);
+    kr[c] = *reinterpret_cast<const uint4*>(k + 8 * c);
+  }
+  double acc = 0.0;
+#pragma unroll
+  for (int c = 0; c < D / 8; ++c) {
+    const T* qv = reinterpret_cast<const T*>(&qr[c]);
+    const T* kv = reinterpret_cast<const T*>(&kr[c]);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc = __builtin_fma(double(to_f32(qv[e])), double(to_f32(kv[e])), acc);
+  }
+  return float(acc);
+}
+
+__device__ inline float max16(const f32x16_t& a) {
+  float m = __builtin_fmaxf(a[0], a[1]);
+#pragma unroll
+  for (int e = 2; e < 16; ++e) m = __builtin_fmaxf(m, a[e]);
+  return m;
+}
+
+template <typename T, int D, int BK>
+__global__ __launch_bounds__(256, 2) void select_wave_kernel(
+    const T* __restrict__ qs, int64_t sqb, int64_t sqh, int64_t sqn, const T* __restrict__ k,
+    int64_t skb, int64_t skh, int64_t sks, int64_t B, int64_t Hq, int64_t Hk, int64_t Sk,
+    int64_t qps, uint32_t gspan, int causal, int64_t bsq, float gap_scalar,
+    const float* __restrict__ gaps, const float* __restrict__ kmax, RowLayout lay,
+    int32_t* __restrict__ counts, int32_t* __restrict__ indices, int64_t nrowsets) {
+  using M = Mfma<T>;
+  using vec = typename M::vec;
+  constexpr int NS = D / 16;                    // MFMA steps over the features
+  constexpr int ROWB = 2 * D;                   // bytes per key row
+  constexpr int NCH = D / 8;                    // 16-byte chunks per row
+  constexpr int STAGE = kWChunk * ROWB;         // bytes of one chunk of K
+  constexpr int RPC = 1024 / ROWB;              // rows per 1 KB copy
+  constexpr int H = STAGE / 1024 / kWWaves;     // copies per wave per chunk
+  static_assert(H >= 1 && H * kWWaves * RPC == kWChunk, "chunk copies must split over the waves");
+  static_assert(BK == 16 || BK == 32 || BK == 64, "tile size");
+
+  __shared__ __attribute__((aligned(1024))) unsigned char kst[2 * STAGE];
+  __shared__ int32_t nml[kWWaves][kWRows][kWList];        // near-max tiles per row
+  __shared__ float exr[kWWaves][kWRows];                  // exact max of folded tiles
+  __shared__ float tmx[kWWaves][kWList];                  // rare path: exact tile maxima
+  __shared__ uint32_t ambm[kWWaves][kWRows][4];           // rare path: ambiguous keys
+  __shared__ int32_t ambk[kWWaves][128];                  // rare path: keys [0,64), flags [64,128)
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid / 64), lane = tid % 64;
+  const int l32 = lane % 32, hh = lane / 32;
+
+  const WorkOrder wo{nrowsets, B, Hq, Hk};
+  int64_t rs, bh;
+  if (!wo.map_item(blockIdx.x, rs, bh)) return;  // idle block (uniform)
+  const int64_t b = bh / Hq, h = bh % Hq, hk = h / (Hq / Hk);
+  const int64_t nc = lay.nc, J0 = lay.J0;
+  const int64_t jr_wave = rs * (kWWaves * kWRows) + kWRows * wave;  // first row of this wave
+  const int64_t jr = jr_wave + l32;
+  const bool valid = jr < nc;
+  const float gap = gaps ? gaps[bh] : gap_scalar;
+  const float kn = kmax[b * Hk + hk];
+  const int smin = int(lay.smin());
+  const int sk = int(Sk);  // < 2^24 (host check)
+
+  // Causal tile limit of a row: tiles with start < lim are selectable.  The
+  // reference's test r > trunc((k_off - off0) / qps), r the row inside its
+  // BLOCK_SIZE_Q program and off0 = (J - r) * qps, is k_off < J*qps for
+  // r >= 1 and k_off <= (J-1)*qps for r == 0.
+  auto row_lim = [&](int64_t row) -> int {
+    if (!causal) return 0x7fffffff;
+    const int64_t J = J0 + row, r = row % bsq;
+    const int64_t lim = (r == 0) ? (J - 1) * qps + 1 : J * qps;
+    return int(lim < 0 ? 0 : (lim > 0x7fffffff ? 0x7fffffff : lim));
+  };
+  // Key range a row set needs: up to the end of its last selectable tile.
+  auto range_end = [&](int64_t last_row) -> int {
+    if (!causal) return sk;
+    const int64_t lim = row_lim(last_row);
+    const int64_t e = (lim + BK - 1) / BK * BK;
+    return int(e < Sk ? e : Sk);
+  };
+  const int64_t nvalid_wave = nc - jr_wave < kWRows ? nc - jr_wave : kWRows;
+  const int64_t nvalid_wg = nc - rs * (kWWaves * kWRows) < kWWaves * kWRows
+                                ? nc - rs * (kWWaves * kWRows)
+                                : kWWaves * kWRows;
+  const int wave_end = nvalid_wave > 0 ? range_end(jr_wave + nvalid_wave - 1) : 0;
+  const int wg_end = range_end(rs * (kWWaves * kWRows) + nvalid_wg - 1);
+  const int lim = valid ? row_lim(jr) : 0;
+
+  // ---- pooled rows: B operand (row l32, features [16s + 8hh, +8)) ---------
+  const T* qrow = qs + b * sqb + h * sqh + jr * sqn;
+  vec qreg[NS];
+  double ss = 0.0;
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    uint4 raw = make_uint4(0, 0, 0, 0);
+    if (valid) raw = *reinterpret_cast<const uint4*>(qrow + 16 * s + 8 * hh);
+    qreg[s] = __builtin_bit_cast(vec, raw);
+    const T* e8 = reinterpret_cast<const T*>(&raw);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const double x = double(to_f32(e8[e]));
+      ss = __builtin_fma(x, x, ss);
+    }
+  }
+  // Norm bound of the row (both halves of the features), rounded up.
+  {
+    const uint64_t u = __builtin_bit_cast(uint64_t, ss);
+    const uint32_t lo = other_half(uint32_t(u)), hi = other_half(uint32_t(u >> 32));
+    ss += __builtin_bit_cast(double, (uint64_t(hi) << 32) | lo);
+  }
+  float band, win;
+  {
+    const double A = __builtin_sqrt(ss) * (1.0 + 0x1p-20) * double(kn) * (1.0 + 0x1p-20);
+    const double delta = double(2 * (D / 16 + 2) + 1) * 0x1p-23 * A;
+    const double ag = __builtin_fabs(double(gap));
+    band = float(1.25 * (2.0 * delta + 6.0 * 0x1p-24 * (A + ag)) + 1e-28);
+    win = float(1.25 * (2.0 * delta + 4.0 * 0x1p-24 * A) + 1e-28);
+  }
+
+  // ---- output of this lane's row ------------------------------------------
+  int32_t* const orow = indices + (valid ? lay.row_offset(bh, jr) : 0);
+  const int cap = valid ? int(lay.capacity(J0 + jr)) : 0;
+  int rowcnt = 0;   // keys selected so far for this row
+  int listcnt = 0;  // near-max tiles listed for this row
+  float m = -__builtin_inff();  // MFMA running maximum of the row
+
+  // ---- K copies --------------------------------------------------------------
+  const T* kh = k + b * skb + hk * skh;
+  const uint32_t krb = uint32_t(sks * 2);
+  const __amdgpu_buffer_rsrc_t krs = make_rsrc(kh, uint32_t(((Sk - 1) * sks + D) * 2));
+  const uint32_t kst_lds = lds_addr(kst);
+  // Copy x of this wave fills LDS rows [(wave*H + x)*RPC, +RPC) of a stage;
+  // LDS row R of block R/32 holds key 32*(R/32) + wkperm(R % 32); this lane
+  // fetches physical chunk p of row R, i.e. logical chunk p ^ (R % NCH).
+  uint32_t coff[H];
+#pragma unroll
+  for (int x = 0; x < H; ++x) {
+    const int R = (wave * H + x) * RPC + lane / NCH;
+    const int key = 32 * (R / 32) + wkperm(R % 32);
+    coff[x] = uint32_t(key) * krb + uint32_t(16 * ((lane % NCH) ^ (R % NCH)));
+  }
+  auto issue_chunk = [&](int kb0, int st) {
+    const uint32_t base = uint32_t(kb0) * krb;
+#pragma unroll
+    for (int x = 0; x < H; ++x)
+      copy16_to_lds(krs, kst_lds + uint32_t(st * STAGE + (wave * H + x) * 1024), base + coff[x]);
+  };
+  // A operand of step s for block b: LDS row 32b + l32, chunk 2s + hh.
+  uint32_t aoff[NS];
+#pragma unroll
+  for (int s = 0; s < NS; ++s)
+    aoff[s] = uint32_t(l32 * ROWB + 16 * ((2 * s + hh) ^ (l32 % NCH)));
+  auto score = [&](int st, f32x16_t* out) {
+    const unsigned char* stage = kst + st * STAGE;
+#pragma unroll
+    for (int bb = 0; bb < 2; ++bb) {
+      f32x16_t a2;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) a2[e] = 0.f;
+#pragma unroll
+      for (int s = 0; s < NS; ++s) {
+        const vec a = __builtin_bit_cast(
+            vec, *reinterpret_cast<const uint4*>(stage + bb * 32 * ROWB + aoff[s]));
+        a2 = M::run(a, qreg[s], a2);
+      }
+      out[bb] = a2;
+    }
+  };
+
+  // The first visited chunk need not start a group: start with no folded tiles.
+  if (hh == 0) exr[wave][l32] = -__builtin_inff();
+  ambk[wave][64 + lane] = 0;  // resolved flags start cleared
+
+  // Append this lane's selected keys of block bb (bits over keys key0 + e).
+  auto append = [&](int kb0, int bb, uint32_t bt) {
+    const int cnt = __builtin_popcount(bt);
+    const int ocnt = int(other_half(uint32_t(cnt)));
+    int pos = rowcnt + (hh ? ocnt : 0);
+    const int key0 = kb0 + 32 * bb + 16 * hh;
+    while (bt) {
+      const int e = __builtin_ctz(bt);
+      bt &= bt - 1;
+      if (pos < cap) orow[pos] = key0 + e;
+      ++pos;
+    }
+    rowcnt += cnt + ocnt;
+  };
+
+  // ---- chunk loop -------------------------------------------------------------
+  // Software pipeline: in iteration c the MFMA scores of chunk c+1 are computed
+  // (stage (c+1)&1) while the decisions of chunk c run on the VALU, and the
+  // copy of chunk c+2 is in flight into stage c&1.
+  const int kfirst = smin / kWChunk * kWChunk;
+  const int nchunks = wg_end > kfirst ? (wg_end - kfirst + kWChunk - 1) / kWChunk : 0;
+  f32x16_t acc[2], nxt[2];
+  if (nchunks > 0) {
+    issue_chunk(kfirst, 0);
+    if (nchunks > 1) issue_chunk(kfirst + kWChunk, 1);
+    vm_lds_barrier();
+    if (kfirst < wave_end) score(0, acc);
+  }
+  for (int c = 0; c < nchunks; ++c) {
+    const int kb0 = kfirst + c * kWChunk;
+    const int st = c & 1;
+    vm_lds_barrier();  // chunk c+1 landed; every wave has scored chunk c (stage st is free)
+    if (c + 2 < nchunks) issue_chunk(kb0 + 2 * kWChunk, st);
+    if (c + 1 < nchunks && kb0 + kWChunk < wave_end) score(st ^ 1, nxt);
+    if (kb0 < wave_end) {  // this wave's rows still need keys (uniform)
+      if (kb0 < smin || kb0 + kWChunk > sk) {  // keys outside [smin, Sk) are not visited
+#pragma unroll
+        for (int bb = 0; bb < 2; ++bb)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            const int key = kb0 + 32 * bb + 16 * hh + e;
+            if (key < smin || key >= sk) acc[bb][e] = -__builtin_inff();
+          }
+      }
+      if (uint32_t(kb0) % gspan == 0u) {  // a group starts with this chunk
+        m = -__builtin_inff();
+        listcnt = 0;
+        if (hh == 0) exr[wave][l32] = -__builtin_inff();
+      }
+
+      // ---- running maximum per tile -------------------------------------------
+      // A tile is worth listing only for a valid row, before the row's causal
+      // limit (later tiles select nothing), and when it holds a visited key.
+      bool live[2];
+#pragma unroll
+      for (int bb = 0; bb < 2; ++bb) {
+        const int koff = BK == 16 ? kb0 + 32 * bb + 16 * hh : (BK == 32 ? kb0 + 32 * bb : kb0);
+        live[bb] = valid && koff < lim && koff + BK > smin && koff < sk;
+      }
+      const float tm0 = max16(acc[0]), tm1 = max16(acc[1]);
+      const float om0 = other_half(tm0), om1 = other_half(tm1);
+      float mt[2];  // running max at this lane's tile of each block
+      int rec[2];   // this lane lists the tile as near-max
+      int nrec;     // tiles the row lists in this chunk
+      int rpos[2];  // list positions of this lane's tiles
+      {
+        const float t00 = hh ? om0 : tm0, t01 = hh ? tm0 : om0;
+        const float t10 = hh ? om1 : tm1, t11 = hh ? tm1 : om1;
+        if (BK == 16) {
+          const float r00 = __builtin_fmaxf(m, t00), r01 = __builtin_fmaxf(r00, t01);
+          const float r10 = __builtin_fmaxf(r01, t10), r11 = __builtin_fmaxf(r10, t11);
+          mt[0] = hh ? r01 : r00;
+          mt[1] = hh ? r11 : r10;
+          m = r11;
+          rec[0] = (live[0] && tm0 >= mt[0] - win) ? 1 : 0;
+          rec[1] = (live[1] && tm1 >= mt[1] - win) ? 1 : 0;
+          const uint32_t orc = other_half(uint32_t(rec[0] | (rec[1] << 1)));
+          const int f00 = hh ? int(orc & 1u) : rec[0], f01 = hh ? rec[0] : int(orc & 1u);
+          const int f10 = hh ? int(orc >> 1) : rec[1], f11 = hh ? rec[1] : int(orc >> 1);
+          rpos[0] = listcnt + (hh ? f00 : 0);
+          rpos[1] = listcnt + f00 + f01 + (hh ? f10 : 0);
+          nrec = f00 + f01 + f10 + f11;
+        } else if (BK == 32) {
+          const float bm0 = __builtin_fmaxf(t00, t01), bm1 = __builtin_fmaxf(t10, t11);
+          const float r0 = __builtin_fmaxf(m, bm0), r1 = __builtin_fmaxf(r0, bm1);
+          mt[0] = r0;
+          mt[1] = r1;
+          m = r1;
+          const int g0 = (live[0] && bm0 >= r0 - win) ? 1 : 0;
+          const int g1 = (live[1] && bm1 >= r1 - win) ? 1 : 0;
+          rec[0] = hh == 0 ? g0 : 0;
+          rec[1] = hh == 0 ? g1 : 0;
+          rpos[0] = listcnt;
+          rpos[1] = listcnt + g0;
+          nrec = g0 + g1;
+        } else {
+          const float cm = __builtin_fmaxf(__builtin_fmaxf(t00, t01), __builtin_fmaxf(t10, t11));
+          const float r = __builtin_fmaxf(m, cm);
+          mt[0] = mt[1] = r;
+          m = r;
+          const int g = (live[0] && cm >= r - win) ? 1 : 0;
+          rec[0] = hh == 0 ? g : 0;
+          rec[1] = 0;
+          rpos[0] = rpos[1] = listcnt;
+          nrec = g;
+        }
+      }
+#pragma unroll
+      for (int bb = 0; bb < 2; ++bb)
+        if (rec[bb]) {
+          const int tk = BK == 16 ? kb0 + 32 * bb + 16 * hh : (BK == 32 ? kb0 + 32 * bb : kb0);
+          nml[wave][l32][rpos[bb]] = tk / BK;
+        }
+      listcnt += nrec;
+
+      // ---- decisions ------------------------------------------------------------
+      // d = s^ - (m^ - gap): selected outright when d > band, ambiguous when
+      // |d| <= band; tiles past the causal limit select nothing.
+      uint32_t bits[2];
+      float mid[2];
+      bool amb_lane = false;
+#pragma unroll
+      for (int bb = 0; bb < 2; ++bb) {
+        const int koff = BK == 16 ? kb0 + 32 * bb + 16 * hh : (BK == 32 ? kb0 + 32 * bb : kb0);
+        const bool ok = valid && koff < lim;
+        mid[bb] = ok ? mt[bb] - gap : __builtin_inff();
+        uint32_t bt = 0;
+        float dmin = __builtin_inff();
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const float d = acc[bb][e] - mid[bb];
+          bt |= uint32_t(d > band) << e;
+          dmin = __builtin_fminf(dmin, __builtin_fabsf(d));
+        }
+        bits[bb] = bt;
+        amb_lane = amb_lane || (dmin <= band);
+      }
+      if (__builtin_amdgcn_ballot_w64(amb_lane || listcnt > kWList - 4) != 0) {
+        // ---- rare path: exact resolution, one row at a time ----------------------
+        // Row r's jobs: every key of its listed tiles, then its ambiguous keys;
+        // the exact tile maxima give the exact running maximum at each
+        // ambiguous key's tile.
+#pragma unroll
+        for (int bb = 0; bb < 2; ++bb) {
+          uint32_t x = 0;
+#pragma unroll
+          for (int e = 0; e < 16; ++e) x |= uint32_t(__builtin_fabsf(acc[bb][e] - mid[bb]) <= band) << e;
+          ambm[wave][l32][2 * bb + hh] = x;
+        }
+        // (no short-circuit: the lane exchange must run with the whole wave active)
+        const bool row_amb = (uint32_t(amb_lane) | other_half(uint32_t(amb_lane))) != 0u;
+        uint64_t need = __builtin_amdgcn_ballot_w64(hh == 0 && (row_amb || listcnt > kWList - 4));
+        uint32_t ovr[2] = {0u, 0u};
+        while (need) {
+          const int r = __builtin_ctzll(need);
+          need &= need - 1;
+          const int n = __builtin_amdgcn_readlane(listcnt, r);
+          const T* qr = qs + b * sqb + h * sqh + (jr_wave + r) * sqn;
+          // Ambiguous keys of row r, as chunk offsets 32b + 16hh + e (64 bits).
+          const uint64_t a64 = uint64_t(ambm[wave][r][0]) | (uint64_t(ambm[wave][r][1]) << 16) |
+                               (uint64_t(ambm[wave][r][2]) << 32) |
+                               (uint64_t(ambm[wave][r][3]) << 48);
+          if ((a64 >> lane) & 1u)
+            ambk[wave][__builtin_amdgcn_mbcnt_hi(uint32_t(a64 >> 32),
+                                                 __builtin_amdgcn_mbcnt_lo(uint32_t(a64), 0))] =
+                kb0 + lane;
+          const int ntile = n * BK, njobs = ntile + __builtin_popcountll(a64);
+          float E0 = exr[wave][r];
+          uint64_t take = 0;
+          for (int p = 0; p < njobs; p += 64) {
+            const int j = p + lane;
+            int key = -1;
+            if (j < ntile) key = nml[wave][r][j / BK] * BK + j % BK;
+            else if (j < njobs) key = ambk[wave][j - ntile];
+            float ex = -__builtin_inff();
+            if (key >= smin && key < sk) ex = exact_dot_global<T, D>(qr, kh + int64_t(key) * sks);
+            // exact maxima of the listed tiles (groups of BK lanes)
+            float tx = j < ntile ? ex : -__builtin_inff();
+#pragma unroll
+            for (int o = 1; o < BK; o <<= 1) tx = __builtin_fmaxf(tx, __shfl_xor(tx, o));
+            if (j < ntile && j % BK == 0) tmx[wave][j / BK] = tx;
+            // decisions of the ambiguous keys of this pass (all tile maxima
+            // come from this or earlier passes)
+            bool tk = false;
+            if (j >= ntile && j < njobs) {
+              const int t = key / BK;
+              float E = E0;
+              for (int i = 0; i < n; ++i)
+                if (nml[wave][r][i] <= t) E = __builtin_fmaxf(E, tmx[wave][i]);
+              tk = (ex + gap) >= E;
+            }
+            // Fold: bit (key - kb0) of the row's resolved selections.
+            if (tk) ambk[wave][64 + key - kb0] = 1;
+          }
+          // Gather the resolved bits: lane l reads the flag of chunk offset l.
+          const int fl = (a64 >> lane) & 1u ? ambk[wave][64 + lane] : 0;
+          take = __builtin_amdgcn_ballot_w64(fl == 1);
+          if ((a64 >> lane) & 1u) ambk[wave][64 + lane] = 0;
+          // This lane's quarter (2*bb + hh) of row r.
+          if (l32 == r) {
+            ovr[0] |= uint32_t(take >> (16 * hh)) & 0xffffu;
+            ovr[1] |= uint32_t(take >> (32 + 16 * hh)) & 0xffffu;
+          }
+          // Fold the listed tiles into the row's exact maximum.
+          float E = E0;
+          for (int i = 0; i < n; ++i) E = __builtin_fmaxf(E, tmx[wave][i]);
+          if (lane == 0) exr[wave][r] = E;
+          if (l32 == r) listcnt = 0;
+        }
+        bits[0] |= ovr[0];
+        bits[1] |= ovr[1];
+      }
+      append(kb0, 0, bits[0]);
+      append(kb0, 1, bits[1]);
+    }
+#pragma unroll
+    for (int bb = 0; bb < 2; ++bb) acc[bb] = nxt[bb];
+  }
+
+  if (valid && hh == 0) counts[bh * nc + jr] = rowcnt < cap ? rowcnt : cap;
+}
+
+bool select_wave_supported(int dtype, int64_t D, int64_t bk, int64_t group) {
+  return (dtype == kBF16 || dtype == kF16) && (D == 64 || D == 128) &&
+         (bk == 16 || bk == 32 || bk == 64) && (bk * group) % kWChunk == 0;
+}
+
+template <typename T, int D, int BK>
+static hipError_t launch_select_wave_tdb(const void* qs, int64_t sqb, int64_t sqh, int64_t sqn,
+                                         const void* k, int64_t skb, int64_t skh, int64_t sks,
+                                         int64_t B, int64_t Hq, int64_t Hk, int64_t Sk,
+                                         int64_t qps, int64_t group, int causal, int64_t bsq,
+                                         float gap, const float* gaps, const float* kmax,
+                                         const RowLayout& lay, int32_t* counts, int32_t* indices,
+                                         hipStream_t stream) {
+  const int64_t nrowsets = (lay.nc + kWWaves * kWRows - 1) / (kWWaves * kWRows);
+  // Group span in keys, capped at 2^31 (key offsets are below 2^24, so a span
+  // that large has its only boundary at 0 either way).
+  const int64_t gs = (group > (int64_t(1) << 31) / BK) ? (int64_t(1) << 31) : BK * group;
+  const int64_t nblocks = WorkOrder{nrowsets, B, Hq, Hk}.grid_items();
+  hipLaunchKernelGGL((select_wave_kernel<T, D, BK>), dim3(unsigned(nblocks)), dim3(256), 0,
+                     stream, static_cast<const T*>(qs), sqb, sqh, sqn, static_cast<const T*>(k),
+                     skb, skh, sks, B, Hq, Hk, Sk, qps, uint32_t(gs), causal, bsq, gap, gaps, kmax,
+                     lay, counts, indices, nrowsets);
+  return hipGetLastError();
+}
+
+template <typename T, int D>
+static hipError_t launch_select_wave_td(int64_t bk, const void* qs, int64_t sqb, int64_t sqh,
+                                        int64_t sqn, const void* k, int64_t skb, int64_t skh,
+                                        int64_t sks, int64_t B, int64_t Hq, int64_t Hk, int64_t Sk,
+                                        int64_t qps, int64_t group, int causal, int64_t bsq,
+                                        float gap, const float* gaps, const float* kmax,
+                                        const RowLayout& lay, int32_t* counts, int32_t* indices,
+                                        hipStream_t stream) {
+#define VA_SELW_BK(BB)                                                                          \
+  if (bk == BB)                                                                                 \
+    return launch_select_wave_tdb<T, D, BB>(qs, sqb, sqh, sqn, k, skb, skh, sks, B, Hq, Hk, Sk, \
+                                            qps, group, causal, bsq, gap, gaps, kmax, lay,      \
+                                            counts, indices, stream);
+  VA_SELW_BK(16)
+  VA_SELW_BK(32)
+  VA_SELW_BK(64)
+#undef VA_SELW_BK
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_select_wave(int dtype, const void* qs, int64_t sqb, int64_t sqh, int64_t sqn,
+                              const void* k, int64_t skb, int64_t skh, int64_t sks, int64_t B,
+                              int64_t Hq, int64_t Hk, int64_t Sk, int64_t D, int64_t qps,
+                              int64_t bk, int64_t group, int causal, int64_t bsq, float gap,
+                              const float* gaps, const float* kmax, const RowLayout& lay,
+                              int32_t* counts, int32_t* indices, hipStream_t stream) {
+#define VA_SELW_CASE(TT, DD)                                                                 \
+  return launch_select_wave_td<TT, DD>(bk, qs, sqb, sqh, sqn, k, skb, skh, sks, B, Hq, Hk, \
+                                       Sk, qps, group, causal, bsq, gap, gaps, kmax, lay,    \
+                                       counts, indices, stream);
+  if (dtype == kBF16 && D == 128) { VA_SELW_CASE(bf16_t, 128) }
+  if (dtype == kBF16 && D == 64) { VA_SELW_CASE(bf16_t, 64) }
+  if (dtype == kF16 && D == 128) { VA_SELW_CASE(f16_t, 128) }
+  if (dtype == kF16 && D == 64) { VA_SELW_CASE(f16_t, 64) }
+#undef VA_SELW_CASE
+  return hipErrorInvalidValue;
+}
+
+}  // namespace va

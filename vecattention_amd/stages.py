@@ -72,8 +72,8 @@ def select_rows(qs_chunk, k, J0, gap, gaps, causal, q_pooling_size, k_local_size
     """TilingSelect for the pooled rows of one chunk.
 
     qs_chunk: (B, Hq, nc, D) scaled pooled rows J0 .. J0+nc-1 (any strides,
-    features contiguous); k: (B, Hk, Sk, D).  `kernel`: VA_SEL_AUTO (MFMA when
-    supported), VA_SEL_EXACT or VA_SEL_MFMA.
+    features contiguous); k: (B, Hk, Sk, D).  `kernel`: VA_SEL_AUTO (a certified
+    MFMA kernel when supported), VA_SEL_EXACT, VA_SEL_MFMA or VA_SEL_WAVE.
     Returns (counts (B, Hq, nc) int32, indices int32 in the index layout).
     """
     if qs_chunk.stride(-1) != 1:
