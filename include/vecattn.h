@@ -104,6 +104,29 @@ int va_select(int dtype, const void* qs, int64_t sqb, int64_t sqh, int64_t sqn,
               int32_t* counts, int32_t* indices, int kernel, float* scratch,
               int64_t scratch_floats, void* stream);
 
+/*
+ * Split selection ("key segments"), the form va_prefill uses internally: the
+ * keys are cut into segments of segment_keys keys (a multiple of 64 and of the
+ * group span k_local_size*group_k_block, at most 64 segments) that are
+ * selected independently.  Segment s of row J writes its keys in ascending
+ * order from slot max(s*segment_keys, smin) - smin of the row's index layout
+ * and its count to counts[((b*Hq + h)*nc + (J - J0))*nseg + s], nseg =
+ * ceil(Sk / segment_keys); a row's list is the concatenation of its segments.
+ * Needs the VA_SEL_WAVE kernel's conditions and `scratch`.  No counterpart
+ * in the reference (its single launch writes dense rows); the selected sets
+ * are the reference rule's, as for va_select.
+ * va_select_segment_keys returns the segment length va_prefill uses, 0 when
+ * the groups are too long to split, or -1 on invalid sizes.
+ */
+int64_t va_select_segment_keys(int64_t Sk, int64_t k_local_size, int64_t group_k_block);
+int va_select_segments(int dtype, const void* qs, int64_t sqb, int64_t sqh, int64_t sqn,
+                       const void* k, int64_t skb, int64_t skh, int64_t sks, int64_t B,
+                       int64_t Hq, int64_t Hk, int64_t Sk, int64_t D, int64_t q_pooling_size,
+                       int64_t k_local_size, int64_t group_k_block, int causal, int wo_init,
+                       int64_t J0, int64_t nc, int64_t bsq, float gap, const float* gaps,
+                       int64_t dense_stride, int64_t segment_keys, int32_t* counts,
+                       int32_t* indices, float* scratch, int64_t scratch_floats, void* stream);
+
 /* fp32 scratch floats va_select's MFMA kernel needs (B*Hk key-norm slots). */
 int64_t va_select_scratch_floats(int64_t B, int64_t Hk);
 
@@ -134,6 +157,20 @@ int va_sparse_attn(int dtype, const void* q, int64_t sqb, int64_t sqh, int64_t s
                    int64_t Sk, int64_t D, int64_t q_pooling_size, int causal, int wo_init,
                    int64_t J0, int64_t nc, int64_t dense_stride, const int32_t* counts,
                    const int32_t* indices, float softmax_scale, int kernel, void* stream);
+
+/*
+ * va_sparse_attn on the segmented lists of va_select_segments (counts of shape
+ * (B, Hq, nc, ceil(Sk/segment_keys))); MFMA kernel only.  No counterpart in
+ * the reference: it is the second half of va_prefill's chunk step.
+ */
+int va_sparse_attn_segments(int dtype, const void* q, int64_t sqb, int64_t sqh, int64_t sqs,
+                            const void* k, int64_t skb, int64_t skh, int64_t sks, const void* v,
+                            int64_t svb, int64_t svh, int64_t svs, void* out, int64_t sob,
+                            int64_t soh, int64_t sos, int64_t B, int64_t Hq, int64_t Hk,
+                            int64_t Sq, int64_t Sk, int64_t D, int64_t q_pooling_size,
+                            int causal, int wo_init, int64_t J0, int64_t nc,
+                            int64_t dense_stride, int64_t segment_keys, const int32_t* counts,
+                            const int32_t* indices, float softmax_scale, void* stream);
 
 /* Bytes of device workspace va_prefill needs (256-byte aligned segments). */
 int64_t va_prefill_workspace_size(int dtype, int64_t B, int64_t Hq, int64_t Sq, int64_t Sk,

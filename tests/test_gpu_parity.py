@@ -159,6 +159,51 @@ def test_select_bit_exact(device, case, kernel):
     assert total_sel > 0
 
 
+SEGMENT_CASES = [
+    # name, Hq, Hk, S, D, dtype, causal, bk, G, keep, segk, chunk_rows
+    ("causal-G16-seg256", 4, 2, 2048, 128, torch.bfloat16, True, 16, 16, 0.10, 256, None),
+    ("causal-G16-seg512-chunked", 4, 1, 3000, 128, torch.bfloat16, True, 16, 16, 0.10, 512, 12),
+    ("noncausal-bk32-G4-seg128", 2, 2, 1500, 64, torch.float16, False, 32, 4, 0.15, 128, None),
+    ("causal-gap0-seg256", 2, 1, 2048, 128, torch.bfloat16, True, 16, 16, None, 256, None),
+]
+
+
+@pytest.mark.parametrize("case", SEGMENT_CASES, ids=[c[0] for c in SEGMENT_CASES])
+def test_select_segments_bit_exact(device, case):
+    # The split selection that VecAttention_prefill runs: per-segment lists,
+    # concatenated, equal the oracle's rows.
+    name, Hq, Hk, S, D, dtype, causal, bk, G, keep, segk, chunk_rows = case
+    note("select segments", name)
+    q, k, _ = make_inputs(1, Hq, Hk, S, D, dtype, seed=S + segk)
+    if keep is None:
+        gaps = np.zeros(Hq, np.float32)
+    else:
+        gaps = orc.gap_from_threshold(calibrated_threshold(keep, q, k, 64, bk, G, causal), 1, Hq)
+    _, qs_cpu = orc.pool(q, 64, DTN[dtype])
+    nqb = qs_cpu.shape[2]
+    qs, _ = stages.pool_scaled(q.to(device), 64)
+    kd = k.to(device)
+    smin = 64 if causal else 0
+    step = chunk_rows or nqb
+    for J0 in range(0, nqb, step):
+        nc = min(step, nqb - J0)
+        want_c, want = orc.select(qs_cpu, k, J0, nc, gaps, 64, bk, G, causal, causal, 64)
+        cnt, idx = stages.select_segments(qs[:, :, J0:J0 + nc], kd, J0, float(gaps[0]), None,
+                                          causal, 64, bk, G, causal, segk)
+        cnt = cnt.cpu().numpy()
+        idx = idx.cpu().numpy()
+        nseg = cnt.shape[-1]
+        for h in range(Hq):
+            for jr in range(nc):
+                o = stages.row_offset(S, 64, causal, causal, J0, nc, h, jr)
+                parts = []
+                for sg in range(nseg):
+                    slot = max(sg * segk, smin) - smin
+                    parts.append(idx[o + slot:o + slot + cnt[0, h, jr, sg]])
+                got = np.concatenate(parts)
+                assert np.array_equal(got, want[0][h][jr]), (name, h, J0 + jr)
+
+
 def test_select_per_head_gaps_and_dense_layout(device):
     note("select per-head dense")
     B, Hq, Hk, S, D = 2, 4, 2, 1024, 128

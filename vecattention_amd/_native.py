@@ -37,12 +37,20 @@ SIGNATURES = {
     "va_select": (_int, [_int, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _i64, _i64, _i64,
                          _i64, _i64, _i64, _i64, _i64, _int, _int, _i64, _i64, _i64, _f32, _vp,
                          _i64, _vp, _vp, _int, _vp, _i64, _vp]),
+    "va_select_segment_keys": (_i64, [_i64, _i64, _i64]),
+    "va_select_segments": (_int, [_int, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _i64, _i64,
+                                  _i64, _i64, _i64, _i64, _i64, _i64, _int, _int, _i64, _i64, _i64,
+                                  _f32, _vp, _i64, _i64, _vp, _vp, _vp, _i64, _vp]),
     "va_select_scratch_floats": (_i64, [_i64, _i64]),
     "va_select_index_capacity": (_i64, [_i64, _i64, _i64, _i64, _int, _int, _i64, _i64, _i64]),
     "va_select_row_offset": (_i64, [_i64, _i64, _int, _int, _i64, _i64, _i64, _i64, _i64]),
     "va_sparse_attn": (_int, [_int, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _vp, _i64, _i64,
                               _i64, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                               _i64, _int, _int, _i64, _i64, _i64, _vp, _vp, _f32, _int, _vp]),
+    "va_sparse_attn_segments": (_int, [_int, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _vp,
+                                       _i64, _i64, _i64, _vp, _i64, _i64, _i64, _i64, _i64, _i64,
+                                       _i64, _i64, _i64, _i64, _int, _int, _i64, _i64, _i64, _i64,
+                                       _vp, _vp, _f32, _vp]),
     "va_prefill_workspace_size": (_i64, [_int, _i64, _i64, _i64, _i64, _i64, _i64, _int, _i64]),
     "va_prefill": (_int, [_int, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _vp, _i64, _i64,
                           _i64, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _f32,

@@ -39,7 +39,9 @@ hipError_t launch_select_wave(int dtype, const void* qs, int64_t sqb, int64_t sq
                               int64_t Hq, int64_t Hk, int64_t Sk, int64_t D, int64_t qps,
                               int64_t bk, int64_t group, int causal, int64_t bsq, float gap,
                               const float* gaps, const float* kmax, const RowLayout& lay,
-                              int32_t* counts, int32_t* indices, hipStream_t stream);
+                              int32_t* counts, int32_t* indices, int64_t segk,
+                              hipStream_t stream);
+int64_t select_wave_segment_keys(int64_t Sk, int64_t bk, int64_t group);
 int64_t key_norm_scratch_floats(int64_t B, int64_t Hk);
 hipError_t launch_key_norm(int dtype, const void* k, int64_t skb, int64_t skh, int64_t sks,
                            int64_t B, int64_t Hk, int64_t Sk, int64_t D, float* scratch,
@@ -49,7 +51,7 @@ hipError_t launch_attn_mfma(int dtype, int64_t D, int64_t qps, const void* q, co
                             void* out, const int64_t* so, int64_t B, int64_t Hq, int64_t Hk,
                             int64_t Sq, int64_t Sk, int causal, float scale_log2,
                             const int32_t* counts, const int32_t* indices, const RowLayout& lay,
-                            hipStream_t stream);
+                            int nseg, int segk, hipStream_t stream);
 }  // namespace va
 
 namespace {
@@ -81,6 +83,7 @@ bool dtype_ok(int dtype) { return dtype == VA_F32 || dtype == VA_BF16 || dtype =
 bool pow2(int64_t x) { return x > 0 && (x & (x - 1)) == 0; }
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
+constexpr int64_t kMaxSegments = 64;  // key segments of a split selection
 
 va::RowLayout make_layout(int64_t J0, int64_t nc, int64_t qps, int64_t Sk, int causal,
                           int wo_init, int64_t dense_stride) {
@@ -188,14 +191,14 @@ static int select_impl(int dtype, const void* qs, int64_t sqb, int64_t sqh, int6
                        int64_t group, int causal, int wo_init, int64_t J0, int64_t nc,
                        int64_t bsq, float gap, const float* gaps, int64_t dense_stride,
                        int32_t* counts, int32_t* indices, SelKernel which, const float* kmax,
-                       hipStream_t stream) {
+                       int64_t segk, hipStream_t stream) {
   const va::RowLayout lay = make_layout(J0, nc, qps, Sk, causal, wo_init, dense_stride);
   group = effective_group(group, Sk, bk);
   hipError_t e;
   if (which == kSelWave)
     e = va::launch_select_wave(dtype, qs, sqb, sqh, sqn, k, skb, skh, sks, B, Hq, Hk, Sk, D, qps,
                                bk, group, causal, bsq, gap, gaps, kmax, lay, counts, indices,
-                               stream);
+                               segk, stream);
   else if (which == kSelMfma)
     e = va::launch_select_mfma(dtype, qs, sqb, sqh, sqn, k, skb, skh, sks, B, Hq, Hk, Sk, D, qps,
                                bk, group, causal, bsq, gap, gaps, kmax, lay, counts, indices,
@@ -273,8 +276,78 @@ int va_select(int dtype, const void* qs, int64_t sqb, int64_t sqh, int64_t sqn,
   }
   rc = select_impl(dtype, qs, sqb, sqh, sqn, k, skb, skh, sks, B, Hq, Hk, Sk, D, qps, bk, group,
                    causal, wo_init, J0, nc, bsq, gap, gaps, dense_stride, counts, indices, which,
-                   scratch, st);
+                   scratch, 0, st);
   return rc ? rc : ok();
+}
+
+// Segments of the split selection.  The segment length must be a multiple of
+// the 64-key chunk and of the group span, with at most 64 segments.
+int64_t va_select_segment_keys(int64_t Sk, int64_t k_local_size, int64_t group_k_block) {
+  if (Sk <= 0 || k_local_size <= 0 || group_k_block <= 0) return -1;
+  return va::select_wave_segment_keys(Sk, k_local_size,
+                                      effective_group(group_k_block, Sk, k_local_size));
+}
+
+int va_select_segments(int dtype, const void* qs, int64_t sqb, int64_t sqh, int64_t sqn,
+                       const void* k, int64_t skb, int64_t skh, int64_t sks, int64_t B,
+                       int64_t Hq, int64_t Hk, int64_t Sk, int64_t D, int64_t qps, int64_t bk,
+                       int64_t group, int causal, int wo_init, int64_t J0, int64_t nc, int64_t bsq,
+                       float gap, const float* gaps, int64_t dense_stride, int64_t segment_keys,
+                       int32_t* counts, int32_t* indices, float* scratch, int64_t scratch_floats,
+                       void* stream) {
+  int rc = check_select_args(dtype, qs, k, B, Hq, Hk, Sk, D, qps, bk, group, causal, wo_init, J0,
+                             nc, bsq);
+  if (rc) return rc;
+  if (!counts || !indices) return fail(VA_ERR_ARG, "null output pointer");
+  if (dense_stride < 0 || (dense_stride > 0 && dense_stride < Sk))
+    return fail(VA_ERR_ARG, "invalid dense_stride");
+  if (!select_wave_ok(dtype, qs, sqb, sqh, sqn, k, skb, skh, sks, Sk, D, bk, group))
+    return fail(VA_ERR_UNSUPPORTED, "segmented selection needs the wave selection kernel");
+  const int64_t gs = bk * effective_group(group, Sk, bk);
+  if (segment_keys <= 0 || segment_keys % 64 || segment_keys % gs ||
+      cdiv(Sk, segment_keys) > 64)
+    return fail(VA_ERR_ARG, "segment_keys %lld: need a multiple of 64 and of the group span "
+                            "(%lld keys), at most 64 segments",
+                (long long)segment_keys, (long long)gs);
+  if (!scratch || scratch_floats < va::key_norm_scratch_floats(B, Hk))
+    return fail(VA_ERR_ARG, "segmented selection needs scratch");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  rc = hip_check(va::launch_key_norm(dtype, k, skb, skh, sks, B, Hk, Sk, D, scratch, st),
+                 "key norm launch");
+  if (rc) return rc;
+  rc = select_impl(dtype, qs, sqb, sqh, sqn, k, skb, skh, sks, B, Hq, Hk, Sk, D, qps, bk, group,
+                   causal, wo_init, J0, nc, bsq, gap, gaps, dense_stride, counts, indices,
+                   kSelWave, scratch, segment_keys, st);
+  return rc ? rc : ok();
+}
+
+// Whether the MFMA attention kernel can run these operands: bf16/fp16, D in
+// {64,128}, qps in {64,128}, 16-byte aligned rows, and K/V rows it can gather
+// with 32-bit buffer offsets computed by 24-bit multiplies (each kv head's
+// rows span < 2 GiB, keys and row strides in bytes below 2^24).
+struct AttnMfmaCheck {
+  bool shape, align, span;
+  bool ok() const { return shape && align && span; }
+};
+static AttnMfmaCheck attn_mfma_check(int dtype, const void* q, const int64_t* sq, const void* k,
+                                     const int64_t* sk, const void* v, const int64_t* sv,
+                                     const void* out, const int64_t* so, int64_t Sk, int64_t D,
+                                     int64_t qps) {
+  const int64_t es = esize(dtype);
+  auto aligned = [&](const void* p, const int64_t* s, int64_t a) {
+    return reinterpret_cast<uintptr_t>(p) % 16 == 0 && s[0] % a == 0 && s[1] % a == 0 &&
+           s[2] % a == 0;
+  };
+  auto span_ok = [&](const int64_t* s) {
+    return Sk < (int64_t(1) << 24) && s[2] >= 0 && s[2] * es < (int64_t(1) << 24) &&
+           ((Sk - 1) * s[2] + D) * es < (int64_t(1) << 31);
+  };
+  AttnMfmaCheck c;
+  c.shape = va::attn_mfma_supported(dtype, D, qps);
+  c.align = aligned(q, sq, 16 / es) && aligned(k, sk, 16 / es) && aligned(v, sv, 16 / es) &&
+            aligned(out, so, 8 / es);
+  c.span = span_ok(sk) && span_ok(sv);
+  return c;
 }
 
 static int attn_dispatch(int dtype, const void* q, const int64_t* sq, const void* k,
@@ -282,25 +355,11 @@ static int attn_dispatch(int dtype, const void* q, const int64_t* sq, const void
                          const int64_t* so, int64_t B, int64_t Hq, int64_t Hk, int64_t Sq,
                          int64_t Sk, int64_t D, int64_t qps, int causal,
                          const va::RowLayout& lay, const int32_t* counts,
-                         const int32_t* indices, float softmax_scale, int kernel,
-                         hipStream_t stream) {
+                         const int32_t* indices, float softmax_scale, int kernel, int nseg,
+                         int64_t segk, hipStream_t stream) {
   const float scale_log2 = softmax_scale * 1.4426950408889634f;
-  const int64_t es = esize(dtype);
-  auto aligned = [&](const void* p, const int64_t* s, int64_t a) {
-    return reinterpret_cast<uintptr_t>(p) % 16 == 0 && s[0] % a == 0 && s[1] % a == 0 &&
-           s[2] % a == 0;
-  };
-  const bool mfma_shape = va::attn_mfma_supported(dtype, D, qps);
-  const bool mfma_align = aligned(q, sq, 16 / es) && aligned(k, sk, 16 / es) &&
-                          aligned(v, sv, 16 / es) && aligned(out, so, 8 / es);
-  // The MFMA kernel gathers K/V rows with 32-bit buffer offsets computed by
-  // 24-bit multiplies: each kv head's rows must span < 2 GiB, keys and row
-  // strides in bytes must stay below 2^24.
-  auto span_ok = [&](const int64_t* s) {
-    return Sk < (int64_t(1) << 24) && s[2] >= 0 && s[2] * es < (int64_t(1) << 24) &&
-           ((Sk - 1) * s[2] + D) * es < (int64_t(1) << 31);
-  };
-  const bool mfma_span = span_ok(sk) && span_ok(sv);
+  const AttnMfmaCheck chk = attn_mfma_check(dtype, q, sq, k, sk, v, sv, out, so, Sk, D, qps);
+  const bool mfma_shape = chk.shape, mfma_align = chk.align, mfma_span = chk.span;
   bool use_mfma = false;
   if (kernel == VA_ATTN_MFMA) {
     if (!mfma_shape)
@@ -316,23 +375,26 @@ static int attn_dispatch(int dtype, const void* q, const int64_t* sq, const void
     return fail(VA_ERR_ARG, "unknown kernel selector %d", kernel);
   }
   if (!use_mfma && qps > 1024) return fail(VA_ERR_UNSUPPORTED, "q_pooling_size > 1024");
+  if (!use_mfma && nseg > 1)
+    return fail(VA_ERR_UNSUPPORTED, "segmented key lists need the MFMA attention kernel");
   hipError_t e = use_mfma
                      ? va::launch_attn_mfma(dtype, D, qps, q, sq, k, sk, v, sv, out, so, B, Hq,
                                             Hk, Sq, Sk, causal, scale_log2, counts, indices, lay,
-                                            stream)
+                                            nseg, int(segk), stream)
                      : va::launch_attn_simple(dtype, q, sq, k, sk, v, sv, out, so, B, Hq, Hk, Sq,
                                               Sk, D, qps, causal, scale_log2, counts, indices,
                                               lay, stream);
   return hip_check(e, "attention launch");
 }
 
-int va_sparse_attn(int dtype, const void* q, int64_t sqb, int64_t sqh, int64_t sqs,
-                   const void* k, int64_t skb, int64_t skh, int64_t sks, const void* v,
-                   int64_t svb, int64_t svh, int64_t svs, void* out, int64_t sob, int64_t soh,
-                   int64_t sos, int64_t B, int64_t Hq, int64_t Hk, int64_t Sq, int64_t Sk,
-                   int64_t D, int64_t qps, int causal, int wo_init, int64_t J0, int64_t nc,
-                   int64_t dense_stride, const int32_t* counts, const int32_t* indices,
-                   float softmax_scale, int kernel, void* stream) {
+static int sparse_attn_impl(int dtype, const void* q, int64_t sqb, int64_t sqh, int64_t sqs,
+                            const void* k, int64_t skb, int64_t skh, int64_t sks, const void* v,
+                            int64_t svb, int64_t svh, int64_t svs, void* out, int64_t sob,
+                            int64_t soh, int64_t sos, int64_t B, int64_t Hq, int64_t Hk,
+                            int64_t Sq, int64_t Sk, int64_t D, int64_t qps, int causal,
+                            int wo_init, int64_t J0, int64_t nc, int64_t dense_stride,
+                            const int32_t* counts, const int32_t* indices, float softmax_scale,
+                            int kernel, int nseg, int64_t segk, void* stream) {
   if (!dtype_ok(dtype)) return fail(VA_ERR_ARG, "unknown dtype %d", dtype);
   if (!q || !k || !v || !out) return fail(VA_ERR_ARG, "null tensor pointer");
   if ((counts == nullptr) != (indices == nullptr))
@@ -348,9 +410,39 @@ int va_sparse_attn(int dtype, const void* q, int64_t sqb, int64_t sqh, int64_t s
                 so[3] = {sob, soh, sos};
   const va::RowLayout lay = make_layout(J0, nc, qps, Sk, causal, wo_init, dense_stride);
   int rc = attn_dispatch(dtype, q, sq, k, sk, v, sv, out, so, B, Hq, Hk, Sq, Sk, D, qps, causal,
-                         lay, counts, indices, softmax_scale, kernel,
+                         lay, counts, indices, softmax_scale, kernel, nseg, segk,
                          static_cast<hipStream_t>(stream));
   return rc ? rc : ok();
+}
+
+int va_sparse_attn(int dtype, const void* q, int64_t sqb, int64_t sqh, int64_t sqs,
+                   const void* k, int64_t skb, int64_t skh, int64_t sks, const void* v,
+                   int64_t svb, int64_t svh, int64_t svs, void* out, int64_t sob, int64_t soh,
+                   int64_t sos, int64_t B, int64_t Hq, int64_t Hk, int64_t Sq, int64_t Sk,
+                   int64_t D, int64_t qps, int causal, int wo_init, int64_t J0, int64_t nc,
+                   int64_t dense_stride, const int32_t* counts, const int32_t* indices,
+                   float softmax_scale, int kernel, void* stream) {
+  return sparse_attn_impl(dtype, q, sqb, sqh, sqs, k, skb, skh, sks, v, svb, svh, svs, out, sob,
+                          soh, sos, B, Hq, Hk, Sq, Sk, D, qps, causal, wo_init, J0, nc,
+                          dense_stride, counts, indices, softmax_scale, kernel, 1, 0, stream);
+}
+
+int va_sparse_attn_segments(int dtype, const void* q, int64_t sqb, int64_t sqh, int64_t sqs,
+                            const void* k, int64_t skb, int64_t skh, int64_t sks, const void* v,
+                            int64_t svb, int64_t svh, int64_t svs, void* out, int64_t sob,
+                            int64_t soh, int64_t sos, int64_t B, int64_t Hq, int64_t Hk,
+                            int64_t Sq, int64_t Sk, int64_t D, int64_t qps, int causal,
+                            int wo_init, int64_t J0, int64_t nc, int64_t dense_stride,
+                            int64_t segment_keys, const int32_t* counts, const int32_t* indices,
+                            float softmax_scale, void* stream) {
+  if (!counts || !indices) return fail(VA_ERR_ARG, "null counts / indices");
+  if (segment_keys <= 0 || segment_keys % 64 || cdiv(Sk, segment_keys) > kMaxSegments)
+    return fail(VA_ERR_ARG, "segment_keys %lld: need a positive multiple of 64, at most %lld "
+                            "segments", (long long)segment_keys, (long long)kMaxSegments);
+  return sparse_attn_impl(dtype, q, sqb, sqh, sqs, k, skb, skh, sks, v, svb, svh, svs, out, sob,
+                          soh, sos, B, Hq, Hk, Sq, Sk, D, qps, causal, wo_init, J0, nc,
+                          dense_stride, counts, indices, softmax_scale, VA_ATTN_MFMA,
+                          int(cdiv(Sk, segment_keys)), segment_keys, stream);
 }
 
 // Workspace of va_prefill: [scaled pooled q][counts][indices], 256-byte aligned.
@@ -361,7 +453,7 @@ static void prefill_segments(int dtype, int64_t B, int64_t Hq, int64_t Sq, int64
   const int64_t nqb = cdiv(Sq, qps);
   *qs_bytes = align256(B * Hq * nqb * D * esize(dtype));
   const int64_t nc_max = cdiv(chunk < Sq ? chunk : Sq, qps);
-  *cnt_bytes = align256(B * Hq * nc_max * 4);
+  *cnt_bytes = align256(B * Hq * nc_max * 4 * kMaxSegments);  // per-segment counts
   int64_t idx_max = 0;
   for (int64_t i = 0; i < Sq; i += chunk) {
     const int64_t rows = (Sq - i < chunk) ? (Sq - i) : chunk;
@@ -427,6 +519,17 @@ int va_prefill(int dtype, const void* q, int64_t sqb, int64_t sqh, int64_t sqs, 
                    "key norm launch");
     if (rc) return rc;
   }
+  // Split the selection into key segments when the wave kernel and the MFMA
+  // attention (which reads the segmented lists) both run.
+  int64_t segk = 0;
+  {
+    const int64_t sq[3] = {sqb, sqh, sqs}, sk[3] = {skb, skh, sks}, sv[3] = {svb, svh, svs},
+                  so[3] = {sob, soh, sos};
+    if (which == kSelWave &&
+        attn_mfma_check(dtype, q, sq, k, sk, v, sv, out, so, Sk, D, qps).ok())
+      segk = va::select_wave_segment_keys(Sk, bk, effective_group(group, Sk, bk));
+  }
+  const int nseg = segk > 0 ? int(cdiv(Sk, segk)) : 1;
   const float scale = float(1.0 / std::sqrt(double(D)));
   for (int64_t i = 0; i < Sq; i += chunk_size) {
     const int64_t rows = (Sq - i < chunk_size) ? (Sq - i) : chunk_size;
@@ -435,11 +538,11 @@ int va_prefill(int dtype, const void* q, int64_t sqb, int64_t sqh, int64_t sqs, 
     const void* qs_chunk = static_cast<const char*>(qs) + J0 * D * es;
     rc = select_impl(dtype, qs_chunk, Hq * nqb * D, nqb * D, D, k, skb, skh, sks, B, Hq, Hk, Sk,
                      D, qps, bk, group, causal, causal, J0, nc, bsq, gap, gaps, 0, counts, indices,
-                     which, knorm, st);
+                     which, knorm, segk, st);
     if (rc) return rc;
-    rc = va_sparse_attn(dtype, q, sqb, sqh, sqs, k, skb, skh, sks, v, svb, svh, svs, out, sob,
-                        soh, sos, B, Hq, Hk, Sq, Sk, D, qps, causal, causal, J0, nc, 0, counts,
-                        indices, scale, VA_ATTN_AUTO, st);
+    rc = sparse_attn_impl(dtype, q, sqb, sqh, sqs, k, skb, skh, sks, v, svb, svh, svs, out, sob,
+                          soh, sos, B, Hq, Hk, Sq, Sk, D, qps, causal, causal, J0, nc, 0, counts,
+                          indices, scale, VA_ATTN_AUTO, nseg, segk, st);
     if (rc) return rc;
   }
   return ok();

@@ -41,6 +41,7 @@
 namespace va {
 
 constexpr int kTileKeys = 64;
+constexpr int kMaxSegments = 64;  // key segments of a split selection (a wave's lanes)
 constexpr uint32_t kOutOfRange = 0xfffffff0u;  // voffset past every buffer's range
 constexpr float kRescaleSlack = 8.f;           // log2 of the largest kept probability
 
@@ -81,7 +82,7 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
     T* __restrict__ out, int64_t sob, int64_t soh, int64_t sos, int64_t B,
     int64_t Hq, int64_t Hk, int64_t Sq, int64_t Sk, int causal, float scale_log2,
     const int32_t* __restrict__ counts, const int32_t* __restrict__ indices,
-    RowLayout lay) {
+    RowLayout lay, int nseg, int segk) {
   using S = AttnShape<D, QPS>;
   using M = Mfma<T>;
   using vec = typename M::vec;
@@ -103,8 +104,55 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
   const int64_t b = bh / Hq, h = bh % Hq, hk = h / (Hq / Hk);
   const int64_t J = lay.J0 + jr;
 
-  int64_t cnt = counts ? counts[bh * lay.nc + jr] : 0;
+  // ---- Q^T operand: lane holds row 32rh + l32, features [16s + 8hh, +8) ----
+  // (loads issued first; their latency overlaps the list bookkeeping below)
+  const int qrow_local = 32 * rh + l32;
+  const int64_t qpos = J * QPS + qrow_local;
+  vec qreg[D / 16];
+  {
+    const T* qr_ptr = q + b * sqb + h * sqh + qpos * sqs;
+#pragma unroll
+    for (int s = 0; s < D / 16; ++s) {
+      uint4 raw = make_uint4(0, 0, 0, 0);
+      if (qpos < Sq) raw = *reinterpret_cast<const uint4*>(qr_ptr + 16 * s + 8 * hh);
+      qreg[s] = __builtin_bit_cast(vec, raw);
+    }
+  }
+
+  // Selected columns.  With nseg > 1 the row's list comes in key segments:
+  // segment s holds counts[.., s] keys from slot max(s*segk, smin) - smin of
+  // the row (see select_wave.hip).  Lane s of wave 0 keeps sv = the exclusive
+  // prefix of the segment counts (the column where segment s starts), so
+  // column p of the concatenated list is slot seg_slot(s) + p - sv[s] for the
+  // last s with sv[s] <= p.
+  __shared__ int32_t segtot;
+  int sv = 0x7fffffff;
   const int64_t cap = lay.capacity(J);
+  const int smin = int(lay.smin());
+  auto seg_slot = [&](int sg) { return (sg * segk > smin ? sg * segk : smin) - smin; };
+  int64_t cnt = 0;
+  if (counts && nseg <= 1) {
+    cnt = counts[bh * lay.nc + jr];
+  } else if (counts) {
+    if (wave == 0) {  // whole wave: the scan exchanges lanes
+      int c = 0;
+      if (lane < nseg) {
+        c = counts[(bh * lay.nc + jr) * nseg + lane];
+        const int room = int(cap) - seg_slot(lane);
+        c = c < 0 ? 0 : (c > room ? (room > 0 ? room : 0) : c);
+      }
+      int incl = c;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int y = __shfl_up(incl, o);
+        if (lane >= o) incl += y;
+      }
+      if (lane < nseg) sv = incl - c;
+      if (lane == nseg - 1) segtot = incl;
+    }
+    lds_barrier();
+    cnt = segtot;
+  }
   if (cnt > cap) cnt = cap;
   const int32_t* cols = indices ? indices + lay.row_offset(bh, jr) : nullptr;
   const KeyList kl = KeyList::make(J, QPS, Sk, causal, cnt, cols);
@@ -140,7 +188,8 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
   const uint32_t krb = uint32_t(sks * 2), vrb = uint32_t(svs * 2);  // row bytes
   const __amdgpu_buffer_rsrc_t krs = make_rsrc(kh, uint32_t(((Sk - 1) * sks + D) * 2));
   const __amdgpu_buffer_rsrc_t vrs = make_rsrc(vh, uint32_t(((Sk - 1) * svs + D) * 2));
-  const __amdgpu_buffer_rsrc_t irs = make_rsrc(cols, uint32_t(n_col) * 4u);
+  const __amdgpu_buffer_rsrc_t irs =
+      make_rsrc(cols, uint32_t(nseg > 1 ? (cap > 0 ? cap : 0) : n_col) * 4u);
   const uint32_t smem_lds = lds_addr(smem);
 
   // Copy geometry.  Copy x of this wave fills rows [(wave*H + x)*RPC, +RPC) of
@@ -170,8 +219,25 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
     } else if (u < t_init + t_diag) {
       dst[lane] = diag0 + (u - t_init) * kTileKeys + w_slot;
     } else {
-      const uint32_t p = uint32_t((u - t_init - t_diag) * kTileKeys + w_slot);
-      copy4_to_lds(irs, lds_addr(dst), p * 4u);
+      const int p = (u - t_init - t_diag) * kTileKeys + w_slot;
+      uint32_t off = uint32_t(p) * 4u;
+      if (nseg > 1) {  // whole wave 0: segment lookup across lanes
+        // segment of the tile's first column, then the boundaries inside the tile
+        const int p0 = p - w_slot;
+        const int sg0 = __builtin_popcountll(
+            __builtin_amdgcn_ballot_w64(lane >= 1 && lane < nseg && sv <= p0));
+        int sg = sg0, start = __builtin_amdgcn_readlane(sv, sg0);
+        for (int sn = sg0 + 1; sn < nseg; ++sn) {
+          const int bnd = __builtin_amdgcn_readlane(sv, sn);
+          if (bnd > p0 + kTileKeys - 1) break;
+          if (p >= bnd) {
+            sg = sn;
+            start = bnd;
+          }
+        }
+        off = p < n_col ? uint32_t(seg_slot(sg) + p - start) * 4u : kOutOfRange;
+      }
+      copy4_to_lds(irs, lds_addr(dst), off);
     }
   };
 
@@ -193,24 +259,10 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
     }
   };
 
-  // ---- Q^T operand: lane holds row 32rh + l32, features [16s + 8hh, +8) ----
-  const int qrow_local = 32 * rh + l32;
-  const int64_t qpos = J * QPS + qrow_local;
-  vec qreg[D / 16];
-  {
-    const T* qr_ptr = q + b * sqb + h * sqh + qpos * sqs;
+  // Wait for Q here: otherwise the compiler places the wait at the first MFMA
+  // inside the tile loop, where it would also wait for the K/V copies in flight.
 #pragma unroll
-    for (int s = 0; s < D / 16; ++s) {
-      uint4 raw = make_uint4(0, 0, 0, 0);
-      if (qpos < Sq) raw = *reinterpret_cast<const uint4*>(qr_ptr + 16 * s + 8 * hh);
-      qreg[s] = __builtin_bit_cast(vec, raw);
-    }
-    // Wait for Q here: otherwise the compiler places the wait at the first
-    // MFMA inside the tile loop, where it would also wait for the K/V copies
-    // in flight.
-#pragma unroll
-    for (int s = 0; s < D / 16; ++s) asm volatile("" ::"v"(qreg[s]));
-  }
+  for (int s = 0; s < D / 16; ++s) asm volatile("" ::"v"(qreg[s]));
 
   // LDS read offsets inside a stage.  K (A operand of S^T): row 32kc + l32,
   // chunk 2s + hh.  V^T (A operand of O^T) via the transposing read: lane
@@ -375,15 +427,15 @@ static hipError_t launch_attn_mfma_tdq(const void* q, const int64_t* sq, const v
                                        void* out, const int64_t* so, int64_t B, int64_t Hq,
                                        int64_t Hk, int64_t Sq, int64_t Sk, int causal,
                                        float scale_log2, const int32_t* counts,
-                                       const int32_t* indices, const RowLayout& lay,
-                                       hipStream_t stream) {
+                                       const int32_t* indices, const RowLayout& lay, int nseg,
+                                       int segk, hipStream_t stream) {
   const int64_t nblocks = WorkOrder{lay.nc, B, Hq, Hk}.grid_items();
   hipLaunchKernelGGL((attn_mfma_kernel<T, D, QPS>), dim3(unsigned(nblocks)),
                      dim3(AttnShape<D, QPS>::kThreads), 0,
                      stream, static_cast<const T*>(q), sq[0], sq[1], sq[2],
                      static_cast<const T*>(k), sk[0], sk[1], sk[2], static_cast<const T*>(v),
                      sv[0], sv[1], sv[2], static_cast<T*>(out), so[0], so[1], so[2], B, Hq, Hk,
-                     Sq, Sk, causal, scale_log2, counts, indices, lay);
+                     Sq, Sk, causal, scale_log2, counts, indices, lay, nseg, segk);
   return hipGetLastError();
 }
 
@@ -393,12 +445,13 @@ static hipError_t launch_attn_mfma_t(int64_t D, int64_t qps, const void* q, cons
                                      const int64_t* sv, void* out, const int64_t* so, int64_t B,
                                      int64_t Hq, int64_t Hk, int64_t Sq, int64_t Sk, int causal,
                                      float scale_log2, const int32_t* counts,
-                                     const int32_t* indices, const RowLayout& lay,
-                                     hipStream_t stream) {
+                                     const int32_t* indices, const RowLayout& lay, int nseg,
+                                     int segk, hipStream_t stream) {
 #define VA_ATTN_CASE(DD, QQ)                                                                   \
   if (D == DD && qps == QQ)                                                                    \
     return launch_attn_mfma_tdq<T, DD, QQ>(q, sq, k, sk, v, sv, out, so, B, Hq, Hk, Sq, Sk,   \
-                                           causal, scale_log2, counts, indices, lay, stream);
+                                           causal, scale_log2, counts, indices, lay, nseg,    \
+                                           segk, stream);
   VA_ATTN_CASE(64, 64)
   VA_ATTN_CASE(128, 64)
   VA_ATTN_CASE(64, 128)
@@ -416,13 +469,13 @@ hipError_t launch_attn_mfma(int dtype, int64_t D, int64_t qps, const void* q, co
                             void* out, const int64_t* so, int64_t B, int64_t Hq, int64_t Hk,
                             int64_t Sq, int64_t Sk, int causal, float scale_log2,
                             const int32_t* counts, const int32_t* indices, const RowLayout& lay,
-                            hipStream_t stream) {
+                            int nseg, int segk, hipStream_t stream) {
   if (dtype == kBF16)
     return launch_attn_mfma_t<bf16_t>(D, qps, q, sq, k, sk, v, sv, out, so, B, Hq, Hk, Sq, Sk,
-                                      causal, scale_log2, counts, indices, lay, stream);
+                                      causal, scale_log2, counts, indices, lay, nseg, segk, stream);
   if (dtype == kF16)
     return launch_attn_mfma_t<f16_t>(D, qps, q, sq, k, sk, v, sv, out, so, B, Hq, Hk, Sq, Sk,
-                                     causal, scale_log2, counts, indices, lay, stream);
+                                     causal, scale_log2, counts, indices, lay, nseg, segk, stream);
   return hipErrorInvalidValue;
 }
 

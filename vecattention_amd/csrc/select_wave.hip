@@ -87,7 +87,8 @@ __global__ __launch_bounds__(256, 2) void select_wave_kernel(
     int64_t skb, int64_t skh, int64_t sks, int64_t B, int64_t Hq, int64_t Hk, int64_t Sk,
     int64_t qps, uint32_t gspan, int causal, int64_t bsq, float gap_scalar,
     const float* __restrict__ gaps, const float* __restrict__ kmax, RowLayout lay,
-    int32_t* __restrict__ counts, int32_t* __restrict__ indices, int64_t nrowsets) {
+    int32_t* __restrict__ counts, int32_t* __restrict__ indices, int64_t nrowsets, int segk,
+    int nseg) {
   using M = Mfma<T>;
   using vec = typename M::vec;
   constexpr int NS = D / 16;                    // MFMA steps over the features
@@ -110,9 +111,11 @@ __global__ __launch_bounds__(256, 2) void select_wave_kernel(
   const int wave = __builtin_amdgcn_readfirstlane(tid / 64), lane = tid % 64;
   const int l32 = lane % 32, hh = lane / 32;
 
-  const WorkOrder wo{nrowsets, B, Hq, Hk};
-  int64_t rs, bh;
-  if (!wo.map_item(blockIdx.x, rs, bh)) return;  // idle block (uniform)
+  const WorkOrder wo{nrowsets * nseg, B, Hq, Hk};
+  int64_t item, bh;
+  if (!wo.map_item(blockIdx.x, item, bh)) return;  // idle block (uniform)
+  const int64_t rs = item / nseg;    // row set
+  const int seg = int(item % nseg);  // key segment [seg*segk, (seg+1)*segk)
   const int64_t b = bh / Hq, h = bh % Hq, hk = h / (Hq / Hk);
   const int64_t nc = lay.nc, J0 = lay.J0;
   const int64_t jr_wave = rs * (kWWaves * kWRows) + kWRows * wave;  // first row of this wave
@@ -144,8 +147,13 @@ __global__ __launch_bounds__(256, 2) void select_wave_kernel(
   const int64_t nvalid_wg = nc - rs * (kWWaves * kWRows) < kWWaves * kWRows
                                 ? nc - rs * (kWWaves * kWRows)
                                 : kWWaves * kWRows;
-  const int wave_end = nvalid_wave > 0 ? range_end(jr_wave + nvalid_wave - 1) : 0;
-  const int wg_end = range_end(rs * (kWWaves * kWRows) + nvalid_wg - 1);
+  // Keys of this work item: the row set's range clipped to the segment.
+  const int seg_lo = seg * segk;
+  const int seg_hi = nseg > 1 ? seg_lo + segk : 0x7fffffff;
+  int wave_end = nvalid_wave > 0 ? range_end(jr_wave + nvalid_wave - 1) : 0;
+  int wg_end = range_end(rs * (kWWaves * kWRows) + nvalid_wg - 1);
+  if (wave_end > seg_hi) wave_end = seg_hi;
+  if (wg_end > seg_hi) wg_end = seg_hi;
   const int lim = valid ? row_lim(jr) : 0;
 
   // ---- pooled rows: B operand (row l32, features [16s + 8hh, +8)) ---------
@@ -180,8 +188,11 @@ __global__ __launch_bounds__(256, 2) void select_wave_kernel(
   }
 
   // ---- output of this lane's row ------------------------------------------
-  int32_t* const orow = indices + (valid ? lay.row_offset(bh, jr) : 0);
-  const int cap = valid ? int(lay.capacity(J0 + jr)) : 0;
+  // Segment seg writes its keys from slot max(seg_lo, smin) - smin of the row,
+  // the slot of its first selectable key: segments never overlap.
+  const int seg_slot = (seg_lo > smin ? seg_lo : smin) - smin;
+  int32_t* const orow = indices + (valid ? lay.row_offset(bh, jr) + seg_slot : 0);
+  const int cap = valid ? int(lay.capacity(J0 + jr)) - seg_slot : 0;
   int rowcnt = 0;   // keys selected so far for this row
   int listcnt = 0;  // near-max tiles listed for this row
   float m = -__builtin_inff();  // MFMA running maximum of the row
@@ -252,7 +263,7 @@ __global__ __launch_bounds__(256, 2) void select_wave_kernel(
   // Software pipeline: in iteration c the MFMA scores of chunk c+1 are computed
   // (stage (c+1)&1) while the decisions of chunk c run on the VALU, and the
   // copy of chunk c+2 is in flight into stage c&1.
-  const int kfirst = smin / kWChunk * kWChunk;
+  const int kfirst = (smin > seg_lo ? smin : seg_lo) / kWChunk * kWChunk;
   const int nchunks = wg_end > kfirst ? (wg_end - kfirst + kWChunk - 1) / kWChunk : 0;
   f32x16_t acc[2], nxt[2];
   if (nchunks > 0) {
@@ -452,7 +463,20 @@ __global__ __launch_bounds__(256, 2) void select_wave_kernel(
     for (int bb = 0; bb < 2; ++bb) acc[bb] = nxt[bb];
   }
 
-  if (valid && hh == 0) counts[bh * nc + jr] = rowcnt < cap ? rowcnt : cap;
+  if (valid && hh == 0) counts[(bh * nc + jr) * nseg + seg] = rowcnt < cap ? rowcnt : (cap > 0 ? cap : 0);
+}
+
+// Key segments of the split selection: a length that is a multiple of the
+// group span (so every segment starts a group and carries no state in) and of
+// the 64-key chunk; 0 when the groups are too long to split.
+int64_t select_wave_segment_keys(int64_t Sk, int64_t bk, int64_t group) {
+  constexpr int64_t kTarget = 4096, kMaxSeg = 64;
+  const int64_t gs = bk * group;
+  if (gs % kWChunk != 0 || gs >= Sk) return 0;
+  int64_t want = (Sk + kMaxSeg - 1) / kMaxSeg;  // at most 64 segments
+  if (want < kTarget) want = kTarget;
+  const int64_t segk = (want + gs - 1) / gs * gs;
+  return segk < Sk ? segk : 0;
 }
 
 bool select_wave_supported(int dtype, int64_t D, int64_t bk, int64_t group) {
@@ -467,16 +491,17 @@ static hipError_t launch_select_wave_tdb(const void* qs, int64_t sqb, int64_t sq
                                          int64_t qps, int64_t group, int causal, int64_t bsq,
                                          float gap, const float* gaps, const float* kmax,
                                          const RowLayout& lay, int32_t* counts, int32_t* indices,
-                                         hipStream_t stream) {
+                                         int64_t segk, hipStream_t stream) {
   const int64_t nrowsets = (lay.nc + kWWaves * kWRows - 1) / (kWWaves * kWRows);
+  const int64_t nseg = segk > 0 ? (Sk + segk - 1) / segk : 1;
   // Group span in keys, capped at 2^31 (key offsets are below 2^24, so a span
   // that large has its only boundary at 0 either way).
   const int64_t gs = (group > (int64_t(1) << 31) / BK) ? (int64_t(1) << 31) : BK * group;
-  const int64_t nblocks = WorkOrder{nrowsets, B, Hq, Hk}.grid_items();
+  const int64_t nblocks = WorkOrder{nrowsets * nseg, B, Hq, Hk}.grid_items();
   hipLaunchKernelGGL((select_wave_kernel<T, D, BK>), dim3(unsigned(nblocks)), dim3(256), 0,
                      stream, static_cast<const T*>(qs), sqb, sqh, sqn, static_cast<const T*>(k),
                      skb, skh, sks, B, Hq, Hk, Sk, qps, uint32_t(gs), causal, bsq, gap, gaps, kmax,
-                     lay, counts, indices, nrowsets);
+                     lay, counts, indices, nrowsets, int(segk > 0 ? segk : 0), int(nseg));
   return hipGetLastError();
 }
 
@@ -487,12 +512,12 @@ static hipError_t launch_select_wave_td(int64_t bk, const void* qs, int64_t sqb,
                                         int64_t qps, int64_t group, int causal, int64_t bsq,
                                         float gap, const float* gaps, const float* kmax,
                                         const RowLayout& lay, int32_t* counts, int32_t* indices,
-                                        hipStream_t stream) {
+                                        int64_t segk, hipStream_t stream) {
 #define VA_SELW_BK(BB)                                                                          \
   if (bk == BB)                                                                                 \
     return launch_select_wave_tdb<T, D, BB>(qs, sqb, sqh, sqn, k, skb, skh, sks, B, Hq, Hk, Sk, \
                                             qps, group, causal, bsq, gap, gaps, kmax, lay,      \
-                                            counts, indices, stream);
+                                            counts, indices, segk, stream);
   VA_SELW_BK(16)
   VA_SELW_BK(32)
   VA_SELW_BK(64)
@@ -505,11 +530,12 @@ hipError_t launch_select_wave(int dtype, const void* qs, int64_t sqb, int64_t sq
                               int64_t Hq, int64_t Hk, int64_t Sk, int64_t D, int64_t qps,
                               int64_t bk, int64_t group, int causal, int64_t bsq, float gap,
                               const float* gaps, const float* kmax, const RowLayout& lay,
-                              int32_t* counts, int32_t* indices, hipStream_t stream) {
+                              int32_t* counts, int32_t* indices, int64_t segk,
+                              hipStream_t stream) {
 #define VA_SELW_CASE(TT, DD)                                                                 \
   return launch_select_wave_td<TT, DD>(bk, qs, sqb, sqh, sqn, k, skb, skh, sks, B, Hq, Hk, \
                                        Sk, qps, group, causal, bsq, gap, gaps, kmax, lay,    \
-                                       counts, indices, stream);
+                                       counts, indices, segk, stream);
   if (dtype == kBF16 && D == 128) { VA_SELW_CASE(bf16_t, 128) }
   if (dtype == kBF16 && D == 64) { VA_SELW_CASE(bf16_t, 64) }
   if (dtype == kF16 && D == 128) { VA_SELW_CASE(f16_t, 128) }

@@ -102,9 +102,47 @@ def select_rows(qs_chunk, k, J0, gap, gaps, causal, q_pooling_size, k_local_size
     return counts, indices
 
 
+def segment_keys(Sk, k_local_size, group_k_block):
+    """Segment length of the split selection (0: the groups are too long to split)."""
+    return int(nat.lib().va_select_segment_keys(Sk, k_local_size, group_k_block))
+
+
+def select_segments(qs_chunk, k, J0, gap, gaps, causal, q_pooling_size, k_local_size,
+                    group_k_block, wo_init, segk, bsq=None, dense_stride=0):
+    """Split TilingSelect (the form VecAttention_prefill runs): keys cut into
+    segments of `segk` keys selected independently.  Returns (counts
+    (B, Hq, nc, nseg) int32, indices int32): segment s of a row writes from slot
+    max(s*segk, smin) - smin of the row in the index layout.
+    """
+    if qs_chunk.stride(-1) != 1:
+        qs_chunk = qs_chunk.contiguous()
+    if k.stride(-1) != 1:
+        k = k.contiguous()
+    B, Hq, nc, D = qs_chunk.shape
+    Hk, Sk = k.shape[1], k.shape[2]
+    if bsq is None:
+        bsq = reference_block_size_q(q_pooling_size, k_local_size, group_k_block, D, causal)
+    nseg = -(-Sk // segk)
+    cap = index_capacity(B, Hq, Sk, q_pooling_size, causal, wo_init, J0, nc, dense_stride)
+    counts = torch.empty(B, Hq, nc, nseg, dtype=torch.int32, device=k.device)
+    indices = torch.empty(max(cap, 1), dtype=torch.int32, device=k.device)
+    nscr = int(nat.lib().va_select_scratch_floats(B, Hk))
+    scratch = torch.empty(max(nscr, 1), dtype=torch.float32, device=k.device)
+    with torch.cuda.device(k.device):
+        rc = nat.lib().va_select_segments(
+            nat.dtype_code(k), nat.ptr(qs_chunk), qs_chunk.stride(0), qs_chunk.stride(1),
+            qs_chunk.stride(2), nat.ptr(k), k.stride(0), k.stride(1), k.stride(2), B, Hq, Hk, Sk, D,
+            q_pooling_size, k_local_size, group_k_block, int(causal), int(wo_init), J0, nc, bsq,
+            float(gap), nat.ptr(gaps), dense_stride, segk, nat.ptr(counts), nat.ptr(indices),
+            nat.ptr(scratch), nscr, _stream(k))
+    nat.check("va_select_segments", rc)
+    return counts, indices
+
+
 def sparse_attention(q, k, v, out, J0, nc, counts, indices, causal, q_pooling_size, wo_init=None,
-                     dense_stride=0, softmax_scale=None, kernel=nat.VA_ATTN_AUTO):
-    """Vector-sparse attention of q-block rows [J0, J0+nc) into `out` (B, Hq, Sq, D)."""
+                     dense_stride=0, softmax_scale=None, kernel=nat.VA_ATTN_AUTO, segk=0):
+    """Vector-sparse attention of q-block rows [J0, J0+nc) into `out` (B, Hq, Sq, D).
+    With segk > 0, (counts, indices) are the segmented lists of select_segments."""
     q = q if q.stride(-1) == 1 else q.contiguous()
     k = k if k.stride(-1) == 1 else k.contiguous()
     v = v if v.stride(-1) == 1 else v.contiguous()
@@ -114,6 +152,16 @@ def sparse_attention(q, k, v, out, J0, nc, counts, indices, causal, q_pooling_si
         wo_init = causal
     if softmax_scale is None:
         softmax_scale = 1.0 / math.sqrt(D)
+    if segk:
+        with torch.cuda.device(q.device):
+            rc = nat.lib().va_sparse_attn_segments(
+                nat.dtype_code(q), nat.ptr(q), q.stride(0), q.stride(1), q.stride(2), nat.ptr(k),
+                k.stride(0), k.stride(1), k.stride(2), nat.ptr(v), v.stride(0), v.stride(1),
+                v.stride(2), nat.ptr(out), out.stride(0), out.stride(1), out.stride(2), B, Hq, Hk,
+                Sq, Sk, D, q_pooling_size, int(causal), int(wo_init), J0, nc, dense_stride, segk,
+                nat.ptr(counts), nat.ptr(indices), float(softmax_scale), _stream(q))
+        nat.check("va_sparse_attn_segments", rc)
+        return out
     with torch.cuda.device(q.device):
         rc = nat.lib().va_sparse_attn(
             nat.dtype_code(q), nat.ptr(q), q.stride(0), q.stride(1), q.stride(2), nat.ptr(k),
@@ -169,5 +217,6 @@ def fuse_qk_softmax_minp_wo_causal(
 
 __all__ = [
     "average_vector", "fuse_qk_softmax_minp_wo_causal", "pool_scaled", "select_rows",
-    "sparse_attention", "index_capacity", "row_offset", "threshold_to_gap",
+    "sparse_attention", "index_capacity", "row_offset", "threshold_to_gap", "segment_keys",
+    "select_segments",
 ]
