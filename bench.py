@@ -44,6 +44,8 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--stage-reps", type=int, default=5)
     ap.add_argument("--extra-json", default=None, help="append the result line to this file too")
+    ap.add_argument("--threshold", type=float, default=None,
+                    help="use this threshold instead of calibrating one to the keep ratio")
     return ap.parse_args()
 
 
@@ -263,7 +265,7 @@ def main():
     S, Sk = q.shape[2], k.shape[2]
     out = torch.empty_like(q)
 
-    th = calibrate_threshold(wl, q, k, v, out)
+    th = args.threshold if args.threshold is not None else calibrate_threshold(wl, q, k, v, out)
     gap = -math.log(th + 1e-9)
     print(f"[bench] threshold {th:.6g} (gap {gap:.6g})", file=sys.stderr, flush=True)
 
@@ -272,7 +274,7 @@ def main():
     names = ["p0", "p1"] + [f"{p}_{c}" for c in range(nch) for p in ("s0", "s1", "a1")]
     t_pool, t_sel, t_attn = [], [], []
     counts = None
-    for r in range(args.stage_reps + 1):
+    for r in range(max(args.stage_reps, 1) + 1):
         ev = {n: torch.cuda.Event(enable_timing=True) for n in names}
         counts = run_stages(wl, q, k, v, gap, out, ev)
         torch.cuda.synchronize()
