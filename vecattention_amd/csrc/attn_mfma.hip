@@ -12,7 +12,7 @@
 // each lane chooses which 16-byte chunk of which key row it fetches.  Empty
 // slots of a tile and keys outside [0, Sk) use an offset past the buffer's
 // range, which the hardware returns as zeros.  Rows are stored with an XOR
-// swizzle of their 16-byte chunks (chunk c of row R sits at c ^ (R % chunks))
+// swizzle of their 16-byte chunks (chunk c of row R sits at c ^ swizzle(R))
 // so that the MFMA operand reads below are free of bank conflicts.  Two LDS
 // stages: the copies of tile t+1 are in flight while tile t is computed, and a
 // single barrier per tile separates them.  The key ids of tile t+2 are staged
@@ -34,6 +34,8 @@
 // bf16/fp16 range, and O / l is unchanged by the choice of reference maximum.
 //
 // Algorithmic work per gathered key: 4*D FLOPs per query row (QK^T and PV).
+#include <type_traits>
+
 #include "keylist.h"
 #include "lanes.h"
 #include "mfma.h"
@@ -68,6 +70,30 @@ struct AttnShape {
 // Per-tile facts shared by the copy and the compute of a tile: number of
 // valid slots, and for diagonal tiles the offset of slot 0 from the first
 // diagonal key.
+// XOR swizzle of the 16-byte chunks of tile row R.  The LDS serves 256 bytes
+// per clock from 64 four-byte banks: a ds_read_b128 is served 16 lanes at a
+// time, a ds_read_b64_tr_b16 32 lanes at a time.  Rows R and R + 256 / (2D)
+// start on the same bank, so m = (R * 2D / 256) mod NCH numbers the rows of a
+// 256-byte bank period, and the swizzle is m with its bits rotated right by
+// log2(NCH) - 2:
+//  - the K reads (16 consecutive rows, one logical chunk) need m -> swizzle
+//    to be a bijection, which any rotation is;
+//  - the V^T reads (rows R0 + j, j < 4, R0 % 4 == 0, logical chunks 4i + g,
+//    g < 4) need the four rows to differ in swizzle bits 2.., which the
+//    rotation gives by moving the low bits of m there.
+template <int D>
+__device__ inline int chunk_swizzle(int R) {
+  constexpr int NCH = D / 8;
+  if constexpr (NCH == 16) {
+    const int m = R % 16;
+    return ((m & 3) << 2) | (m >> 2);
+  } else {
+    static_assert(NCH == 8, "D must be 64 or 128");
+    const int m = (R / 2) % 8;
+    return ((m & 1) << 2) | (m >> 1);
+  }
+}
+
 struct TileInfo {
   int lim;
   int dshift;
@@ -194,16 +220,13 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
 
   // Copy geometry.  Copy x of this wave fills rows [(wave*H + x)*RPC, +RPC) of
   // a tile; this lane fetches physical chunk p of row R_x, i.e. logical chunk
-  // p ^ (R_x % NCH).  The H key ids a lane needs sit contiguously in `ids` at
+  // p ^ chunk_swizzle(R_x).  The H key ids a lane needs sit contiguously in `ids` at
   // position (wave*RPC + qr)*H + x, where qr = lane / NCH.
   const int qr = lane / NCH, pc = lane % NCH;
-  int crow[H];
   uint32_t cchunk[H];
 #pragma unroll
-  for (int x = 0; x < H; ++x) {
-    crow[x] = (wave * H + x) * RPC + qr;
-    cchunk[x] = uint32_t(16 * (pc ^ (crow[x] % NCH)));
-  }
+  for (int x = 0; x < H; ++x)
+    cchunk[x] = uint32_t(16 * (pc ^ chunk_swizzle<D>((wave * H + x) * RPC + qr)));
   const int id_pos = (wave * RPC + qr) * H;
   // Inverse map for the lanes of wave 0 that write ids: position -> slot.
   const int w_slot = [&] {
@@ -211,7 +234,18 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
     return (w * H + x) * RPC + r;
   }();
 
-  // Stage the key ids of tile u into ids[slot] (wave 0 only).
+  // Stage the key ids of tile u into ids[slot] (wave 0 only; tiles are staged
+  // in increasing order).  Column positions of the selected list map to index
+  // slots through a scalar segment cursor: segment sc holds positions
+  // [sv[sc], sc_next) at slots position + sc_base.  Positions only grow from
+  // tile to tile, so the cursor moves forward once per segment (empty
+  // segments are stepped over), and a tile with no segment boundary inside
+  // it costs one add per lane.
+  const int kNoBoundary = 0x7fffffff;
+  auto boundary = [&](int sg) {  // start of segment sg (wave 0), or none
+    return sg < nseg ? __builtin_amdgcn_readlane(sv, sg) : kNoBoundary;
+  };
+  int sc = 0, sc_base = 0, sc_next = nseg > 1 ? boundary(1) : kNoBoundary;
   auto stage_ids = [&](int u, int slot) {
     int32_t* dst = ids + slot * kTileKeys;
     if (u < t_init) {
@@ -219,44 +253,51 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
     } else if (u < t_init + t_diag) {
       dst[lane] = diag0 + (u - t_init) * kTileKeys + w_slot;
     } else {
-      const int p = (u - t_init - t_diag) * kTileKeys + w_slot;
-      uint32_t off = uint32_t(p) * 4u;
-      if (nseg > 1) {  // whole wave 0: segment lookup across lanes
-        // segment of the tile's first column, then the boundaries inside the tile
-        const int p0 = p - w_slot;
-        const int sg0 = __builtin_popcountll(
-            __builtin_amdgcn_ballot_w64(lane >= 1 && lane < nseg && sv <= p0));
-        int sg = sg0, start = __builtin_amdgcn_readlane(sv, sg0);
-        for (int sn = sg0 + 1; sn < nseg; ++sn) {
-          const int bnd = __builtin_amdgcn_readlane(sv, sn);
-          if (bnd > p0 + kTileKeys - 1) break;
-          if (p >= bnd) {
-            sg = sn;
-            start = bnd;
-          }
-        }
-        off = p < n_col ? uint32_t(seg_slot(sg) + p - start) * 4u : kOutOfRange;
+      const int p0 = (u - t_init - t_diag) * kTileKeys, p = p0 + w_slot;
+      while (sc_next <= p0) {  // the tile starts past segment sc
+        ++sc;
+        sc_base = seg_slot(sc) - sc_next;
+        sc_next = boundary(sc + 1);
       }
+      int base = sc_base;
+      const int pend = (p0 + kTileKeys < n_col ? p0 + kTileKeys : n_col) - 1;  // last position
+      if (sc_next <= pend) {  // boundaries inside the tile
+        int sg = sc, b = sc_next;
+        while (b <= pend) {
+          ++sg;
+          if (p >= b) base = seg_slot(sg) - b;
+          b = boundary(sg + 1);
+        }
+      }
+      const uint32_t off = p < n_col ? uint32_t(p + base) * 4u : kOutOfRange;
       copy4_to_lds(irs, lds_addr(dst), off);
     }
   };
 
-  // Issue the K and V copies of tile u into stage `st`, ids from ids[slot].
-  auto issue_tile = [&](int u, int st, int slot) {
-    const TileInfo ti = tile_info(u);
+  // Copy offsets of tile u: for each of this lane's H copies, the byte offset
+  // of its 16-byte chunk in K (kof) and V (vof), from the key ids in ids slot
+  // idslot.  Rows past the tile's key count, keys outside [0, Sk) and every
+  // row of a tile past the end of the list get an out-of-range offset (their
+  // copies write zeros into a slot that is masked or never read).
+  auto copy_offsets = [&](int u, int idslot, uint32_t (&kof)[H], uint32_t (&vof)[H]) {
+    const int lim = tile_info(u).lim;
     int32_t key[H];
 #pragma unroll
-    for (int x = 0; x < H; ++x) key[x] = ids[slot * kTileKeys + id_pos + x];
-    const uint32_t kdst = smem_lds + uint32_t(st * S::kStageBytes);
-    const uint32_t vdst = kdst + uint32_t(S::kTileBytes);
+    for (int x = 0; x < H; ++x) key[x] = ids[idslot * kTileKeys + id_pos + x];
 #pragma unroll
     for (int x = 0; x < H; ++x) {
-      const bool ok = crow[x] < ti.lim && uint32_t(key[x]) < uint32_t(Sk);
-      const uint32_t kof = ok ? __umul24(uint32_t(key[x]), krb) + cchunk[x] : kOutOfRange;
-      const uint32_t vof = ok ? __umul24(uint32_t(key[x]), vrb) + cchunk[x] : kOutOfRange;
-      copy16_to_lds(krs, kdst + uint32_t((wave * H + x) * 1024), kof);
-      copy16_to_lds(vrs, vdst + uint32_t((wave * H + x) * 1024), vof);
+      // row (wave*H + x)*RPC + qr of the tile holds a key when it is below lim
+      const bool ok = (qr < lim - (wave * H + x) * RPC) & (uint32_t(key[x]) < uint32_t(Sk));
+      kof[x] = ok ? __umul24(uint32_t(key[x]), krb) + cchunk[x] : kOutOfRange;
+      vof[x] = ok ? __umul24(uint32_t(key[x]), vrb) + cchunk[x] : kOutOfRange;
     }
+  };
+  // Copy x of this wave into the K or V tile at LDS address base.
+  auto copy_k = [&](uint32_t base, int x, uint32_t off) {
+    copy16_to_lds(krs, base + uint32_t((wave * H + x) * 1024), off);
+  };
+  auto copy_v = [&](uint32_t base, int x, uint32_t off) {
+    copy16_to_lds(vrs, base + uint32_t((wave * H + x) * 1024), off);
   };
 
   // Wait for Q here: otherwise the compiler places the wait at the first MFMA
@@ -264,7 +305,7 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
 #pragma unroll
   for (int s = 0; s < D / 16; ++s) asm volatile("" ::"v"(qreg[s]));
 
-  // LDS read offsets inside a stage.  K (A operand of S^T): row 32kc + l32,
+  // LDS read offsets inside a K or V tile.  K (A operand of S^T): row 32kc + l32,
   // chunk 2s + hh.  V^T (A operand of O^T) via the transposing read: lane
   // group g16 = lane / 16 reads rows 32kc + 16sub + 8r + 4hh + j with
   // j = (lane % 16) / 4, features 32i + 16(g16 % 2) + 4(lane % 4).
@@ -272,7 +313,7 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
 #pragma unroll
   for (int s = 0; s < D / 16; ++s) {
     const int R = 32 * kc + l32;
-    koff[s] = uint32_t(R * S::kRowBytes + 16 * ((2 * s + hh) ^ (R % NCH)));
+    koff[s] = uint32_t(R * S::kRowBytes + 16 * ((2 * s + hh) ^ chunk_swizzle<D>(R)));
   }
   uint32_t voff[D / 32][2];
   {
@@ -281,9 +322,9 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
     for (int i = 0; i < D / 32; ++i)
 #pragma unroll
       for (int r = 0; r < 2; ++r) {
-        const int R = 32 * kc + 8 * r + 4 * hh + j;  // + 16 sub (a multiple of NCH)
+        const int R = 32 * kc + 8 * r + 4 * hh + j;  // + 16 sub (same swizzle)
         const int c = 4 * i + g2;
-        voff[i][r] = uint32_t(S::kTileBytes + R * S::kRowBytes + 16 * (c ^ (R % NCH)) +
+        voff[i][r] = uint32_t(R * S::kRowBytes + 16 * (c ^ chunk_swizzle<D>(R)) +
                               8 * (lane % 2));
       }
   }
@@ -294,91 +335,181 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
 #pragma unroll
     for (int e = 0; e < 16; ++e) o[i][e] = 0.f;
   float mc = -__builtin_inff();  // running maximum, scaled (log2) units
-  float lsum = 0.f;              // this lane's share of the row sum
+  // Row sums of the probabilities, accumulated on the matrix cores: an MFMA
+  // with an all-ones A operand and the PV step's B operand (P^T) adds, to
+  // every entry of lane l's accumulator, the sum over the step's 16 keys of
+  // row l % 32.  Entry 0 is the one kept (the rescale touches only it).  The
+  // sum is over the bf16/fp16-rounded probabilities that also weight V.
+  f32x16_t lacc;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) lacc[e] = 0.f;
+  const vec ones = [] {
+    float one[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) one[e] = 1.f;
+    return M::pack(one);
+  }();
 
-  auto compute_tile = [&](int t, const unsigned char* stage) {
-    const TileInfo ti = tile_info(t);
+  // S^T of one tile: 8 (D/16) MFMAs with K rows from the K slot at kbuf.
+  auto qk = [&](const unsigned char* kbuf) {
     f32x16_t s;
 #pragma unroll
     for (int e = 0; e < 16; ++e) s[e] = 0.f;
 #pragma unroll
     for (int st = 0; st < D / 16; ++st) {
-      const vec a = __builtin_bit_cast(vec, *reinterpret_cast<const uint4*>(stage + koff[st]));
+      const vec a = __builtin_bit_cast(vec, *reinterpret_cast<const uint4*>(kbuf + koff[st]));
       s = M::run(a, qreg[st], s);
     }
-    // Masking: empty slots, causal diagonal.  Slot of s[e]: 32kc + 8(e/4) + 4hh + e%4.
-    float tmax = -__builtin_inff();
-    if (!ti.diag && ti.lim == kTileKeys) {
-#pragma unroll
-      for (int e = 0; e < 16; ++e) tmax = __builtin_fmaxf(tmax, s[e]);
-    } else {
+    return s;
+  };
+  // Mask tile u's scores (empty slots, causal diagonal; every slot of a tile
+  // past the end of the list) and return the tile maximum of this lane's row
+  // in scaled (log2) units.  Slot of s[e]: 32kc + 8(e/4) + 4hh + e%4.
+  auto mask_max = [&](int u, f32x16_t& s) {
+    const TileInfo ti = tile_info(u);
+    if (ti.diag || ti.lim < kTileKeys) {  // rare: partial, diagonal or empty tiles
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         const int slot = 32 * kc + 8 * (e / 4) + 4 * hh + (e % 4);
-        bool ok = slot < ti.lim;
-        if (ti.diag) ok = ok && (ti.dshift + slot <= qrow_local);
+        const bool ok = (slot < ti.lim) & (!ti.diag | (ti.dshift + slot <= qrow_local));
         s[e] = ok ? s[e] : -__builtin_inff();
-        tmax = __builtin_fmaxf(tmax, s[e]);
       }
     }
-    const float tsc = max_halves(tmax) * scale_log2;
-    if (__builtin_amdgcn_ballot_w64(tsc > mc + kRescaleSlack)) {  // some row's maximum moved
+    float tmax = -__builtin_inff();
+#pragma unroll
+    for (int e = 0; e < 16; ++e) tmax = __builtin_fmaxf(tmax, s[e]);
+    return max_halves(tmax) * scale_log2;
+  };
+  // Move the running maximum when some row's tile maximum exceeds it by more
+  // than the slack (rare): rescale O and the row sums.
+  auto rescale = [&](float tsc) {
+    if (__builtin_amdgcn_ballot_w64(tsc > mc + kRescaleSlack)) {
       const float mnew = __builtin_fmaxf(mc, tsc);
       const float alpha = (mnew == mc) ? 1.f : __builtin_amdgcn_exp2f(mc - mnew);
 #pragma unroll
       for (int i = 0; i < D / 32; ++i)
 #pragma unroll
         for (int e = 0; e < 16; ++e) o[i][e] *= alpha;
-      lsum *= alpha;
+      lacc[0] *= alpha;
       mc = mnew;
     }
-    const float mneg = (mc == -__builtin_inff()) ? 0.f : -mc;
-#pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[e], scale_log2, mneg));
-      s[e] = p;
-      lsum += p;
-    }
-    // O^T += V^T P^T, 16 keys per step: k-slot 8hh + e of step sub is key
-    // 32kc + 16sub + 8(e/4) + 4hh + e%4, i.e. accumulator entries 8sub .. 8sub+7.
+  };
+  // O^T += V^T P^T, 16 keys per step: k-slot 8hh + e of step sub is key
+  // 32kc + 16sub + 8(e/4) + 4hh + e%4, i.e. accumulator entries 8sub .. 8sub+7.
+  auto pv_step = [&](const unsigned char* vbuf, const vec (&bfrag)[2]) {
 #pragma unroll
     for (int sub = 0; sub < 2; ++sub) {
-      float pv[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) pv[e] = s[8 * sub + e];
-      const vec bfrag = M::pack(pv);
 #pragma unroll
       for (int i = 0; i < D / 32; ++i) {
-        const unsigned char* p0 = stage + voff[i][0] + sub * 16 * S::kRowBytes;
-        const unsigned char* p1 = stage + voff[i][1] + sub * 16 * S::kRowBytes;
+        const unsigned char* p0 = vbuf + voff[i][0] + sub * 16 * S::kRowBytes;
+        const unsigned char* p1 = vbuf + voff[i][1] + sub * 16 * S::kRowBytes;
         const s16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
             (__attribute__((address_space(3))) s16x4_t*)(p0));
         const s16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
             (__attribute__((address_space(3))) s16x4_t*)(p1));
         const s16x4_t both[2] = {lo, hi};
-        o[i] = M::run(__builtin_bit_cast(vec, both), bfrag, o[i]);
+        o[i] = M::run(__builtin_bit_cast(vec, both), bfrag[sub], o[i]);
       }
+      lacc = M::run(ones, bfrag[sub], lacc);
     }
   };
 
   // ---- pipeline ------------------------------------------------------------
+  // LDS slots: K(u) in K slot u&1, V(u) in V slot u&1 (slot p of K at
+  // p * kStageBytes, of V kTileBytes after it), key ids of tile u in ids slot
+  // u&1.  Iteration t computes S(t+1) = QK(t+1) next to the softmax of S(t),
+  // then PV(t) next to the masking and maximum of S(t+1).  Resident during
+  // iteration t: K(t+1), V(t); in flight: K(t+2), V(t+1), ids(t+3); one
+  // barrier per iteration.  The copies of an iteration are spread over its QK
+  // MFMAs (one DMA instruction after an MFMA), so that a copy that waits for
+  // room in the memory pipeline overlaps the matrix work already issued
+  // instead of stalling every wave right after the barrier.
+  constexpr int NQK = D / 16;  // QK MFMAs per tile
+  uint32_t vof_cur[H];         // V offsets of tile t+1 (its K copies went out earlier)
+  f32x16_t s_cur;              // masked scores of tile t
   if (ntiles > 0) {
     if (wave == 0) {
       stage_ids(0, 0);
       if (ntiles > 1) stage_ids(1, 1);
     }
     vm_lds_barrier();
-    issue_tile(0, 0, 0);
+    uint32_t kof[H], vof[H];
+    copy_offsets(0, 0, kof, vof);
+#pragma unroll
+    for (int x = 0; x < H; ++x) {
+      copy_k(smem_lds, x, kof[x]);
+      copy_v(smem_lds + uint32_t(S::kTileBytes), x, vof[x]);
+    }
+    copy_offsets(1, 1, kof, vof_cur);
+#pragma unroll
+    for (int x = 0; x < H; ++x) copy_k(smem_lds + uint32_t(S::kStageBytes), x, kof[x]);
+    vm_lds_barrier();  // K(0), V(0), K(1) landed; ids slots 0 and 1 read by every wave
+    if (wave == 0 && ntiles > 2) stage_ids(2, 0);
+    s_cur = qk(smem);
+    rescale(mask_max(0, s_cur));
   }
-  for (int t = 0; t < ntiles; ++t) {
-    vm_lds_barrier();  // tile t landed in stage t&1; stage (t+1)&1 and ids slot t&1 are free
-    if (t + 1 < ntiles) issue_tile(t + 1, (t + 1) & 1, (t + 1) & 1);
-    if (wave == 0 && t + 2 < ntiles) stage_ids(t + 2, t & 1);
-    compute_tile(t, smem + (t & 1) * S::kStageBytes);
+  // One iteration; the parity P = t & 1 is a compile-time constant so that
+  // the LDS slot addresses fold into the instructions' offsets and S(t),
+  // S(t+1) alternate between two register sets.
+  auto iteration = [&](int t, auto parity_tag, const f32x16_t& s_cur, f32x16_t& s_next) {
+    constexpr int P = decltype(parity_tag)::value;
+    constexpr uint32_t k_this = uint32_t(P * S::kStageBytes);          // K slot P
+    constexpr uint32_t k_next = uint32_t((P ^ 1) * S::kStageBytes);    // K slot P^1
+    constexpr uint32_t v_this = k_this + uint32_t(S::kTileBytes);      // V slot P
+    constexpr uint32_t v_next = k_next + uint32_t(S::kTileBytes);      // V slot P^1
+    vm_lds_barrier();  // V(t), K(t+1), ids(t+2) landed; K slot P, V slot P^1 free
+    if (wave == 0 && t + 3 < ntiles) stage_ids(t + 3, P ^ 1);
+    const unsigned char* kb = smem + k_next;
+    const float mneg = (mc == -__builtin_inff()) ? 0.f : -mc;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) s_next[e] = 0.f;
+    float pr[16];
+    uint32_t kof[H], vof_new[H];
+    // K operands are read kAhead MFMAs ahead of their use (LDS latency)
+    constexpr int kAhead = 3;
+    vec a[NQK];
+#pragma unroll
+    for (int st = 0; st < kAhead; ++st)
+      a[st] = __builtin_bit_cast(vec, *reinterpret_cast<const uint4*>(kb + koff[st]));
+#pragma unroll
+    for (int st = 0; st < NQK; ++st) {
+      __builtin_amdgcn_sched_barrier(0);
+      if (st + kAhead < NQK)
+        a[st + kAhead] =
+            __builtin_bit_cast(vec, *reinterpret_cast<const uint4*>(kb + koff[st + kAhead]));
+      s_next = M::run(a[st], qreg[st], s_next);  // past the last tile: masked away below
+      if (st == 0) copy_offsets(t + 2, P, kof, vof_new);
+      // copy c of the 2H of this iteration goes out after MFMA c*NQK/(2H):
+      // first V(t+1) into V slot P^1, then K(t+2) into K slot P
+#pragma unroll
+      for (int c = 0; c < 2 * H; ++c) {
+        if (c * NQK / (2 * H) != st) continue;
+        if (c < H)
+          copy_v(smem_lds + v_next, c, vof_cur[c]);
+        else
+          copy_k(smem_lds + k_this, c - H, kof[c - H]);
+      }
+      // this step's share of the softmax of S(t)
+#pragma unroll
+      for (int e = st * 16 / NQK; e < (st + 1) * 16 / NQK; ++e)
+        pr[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(s_cur[e], scale_log2, mneg));
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    const vec bfrag[2] = {M::pack(pr), M::pack(pr + 8)};
+    pv_step(smem + v_this, bfrag);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int x = 0; x < H; ++x) vof_cur[x] = vof_new[x];
+    rescale(mask_max(t + 1, s_next));
+  };
+  f32x16_t s_alt;  // scores of the odd tiles (s_cur holds the even ones)
+  for (int t = 0; t < ntiles; t += 2) {
+    iteration(t, std::integral_constant<int, 0>{}, s_cur, s_alt);
+    if (t + 1 < ntiles) iteration(t + 1, std::integral_constant<int, 1>{}, s_alt, s_cur);
   }
 
   // ---- merge the two key halves, normalise, store --------------------------
-  lds_barrier();  // every wave is done with the stages
+  vm_lds_barrier();  // every wave is done with the stages, the last copies have landed
   float* mo = reinterpret_cast<float*>(smem) + rh * 64 * (D / 2 + 2);
   if (kc == 1) {
 #pragma unroll
@@ -388,7 +519,7 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
         *reinterpret_cast<float4*>(mo + ((4 * i + g) * 64 + lane) * 4) =
             make_float4(o[i][4 * g], o[i][4 * g + 1], o[i][4 * g + 2], o[i][4 * g + 3]);
     mo[64 * (D / 2) + lane] = mc;
-    mo[64 * (D / 2) + 64 + lane] = lsum;
+    mo[64 * (D / 2) + 64 + lane] = lacc[0];
   }
   lds_barrier();
   if (kc == 0) {
@@ -396,7 +527,7 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
     const float m = __builtin_fmaxf(mc, m1);
     const float a0 = (mc == m) ? 1.f : __builtin_amdgcn_exp2f(mc - m);
     const float a1 = (m1 == m) ? 1.f : __builtin_amdgcn_exp2f(m1 - m);
-    const float l = sum_halves(lsum * a0 + l1 * a1);
+    const float l = lacc[0] * a0 + l1 * a1;  // both halves of the wave hold the full sums
     const float inv = l > 0.f ? 1.f / l : 0.f;
     const float c0 = a0 * inv, c1 = a1 * inv;
     if (qpos < Sq) {
