@@ -262,7 +262,11 @@ __global__ __launch_bounds__(256, 2) void select_wave_kernel(
   // ---- chunk loop -------------------------------------------------------------
   // Software pipeline: in iteration c the MFMA scores of chunk c+1 are computed
   // (stage (c+1)&1) while the decisions of chunk c run on the VALU, and the
-  // copy of chunk c+2 is in flight into stage c&1.
+  // copy of chunk c+2 is in flight into stage c&1.  The 2*NS MFMAs of chunk
+  // c+1 are issued one per slot, the slots spread through chunk c's VALU work
+  // (sched_barrier keeps the order): a wave's MFMA then executes while the
+  // same wave issues the VALU instructions that follow it, instead of the wave
+  // stalling on a burst of MFMA issues and then running its VALU work alone.
   const int kfirst = (smin > seg_lo ? smin : seg_lo) / kWChunk * kWChunk;
   const int nchunks = wg_end > kfirst ? (wg_end - kfirst + kWChunk - 1) / kWChunk : 0;
   f32x16_t acc[2], nxt[2];
@@ -277,8 +281,37 @@ __global__ __launch_bounds__(256, 2) void select_wave_kernel(
     const int st = c & 1;
     vm_lds_barrier();  // chunk c+1 landed; every wave has scored chunk c (stage st is free)
     if (c + 2 < nchunks) issue_chunk(kb0 + 2 * kWChunk, st);
-    if (c + 1 < nchunks && kb0 + kWChunk < wave_end) score(st ^ 1, nxt);
     if (kb0 < wave_end) {  // this wave's rows still need keys (uniform)
+      // MFMA slot i of chunk c+1: block i / NS, feature step i % NS; the A
+      // operand is read from LDS two slots ahead of its MFMA.  Past the
+      // wave's last chunk the slots score stale LDS contents, which the next
+      // iteration does not use (kb0 >= wave_end there).
+      const unsigned char* nstage = kst + (st ^ 1) * STAGE;
+      auto aload = [&](int i) {
+        return __builtin_bit_cast(vec, *reinterpret_cast<const uint4*>(
+                                           nstage + (i / NS) * 32 * ROWB + aoff[i % NS]));
+      };
+      vec aring[3];
+      aring[0] = aload(0);
+      aring[1] = aload(1);
+      auto slot = [&](int i) {
+        __builtin_amdgcn_sched_barrier(0);
+        if (i + 2 < 2 * NS) aring[(i + 2) % 3] = aload(i + 2);
+        const int bb = i / NS, s = i % NS;
+        if (s == 0) {
+#pragma unroll
+          for (int e = 0; e < 16; ++e) nxt[bb][e] = 0.f;
+        }
+        nxt[bb] = M::run(aring[i % 3], qreg[s], nxt[bb]);
+        __builtin_amdgcn_sched_barrier(0);
+      };
+      // Slots are placed after MFMA-free stretches of roughly equal VALU work.
+      constexpr int NSL = 2 * NS;
+      auto slots = [&](int from, int to) {
+#pragma unroll
+        for (int i = from; i < to; ++i) slot(i);
+      };
+
       if (kb0 < smin || kb0 + kWChunk > sk) {  // keys outside [smin, Sk) are not visited
 #pragma unroll
         for (int bb = 0; bb < 2; ++bb)
@@ -293,6 +326,7 @@ __global__ __launch_bounds__(256, 2) void select_wave_kernel(
         listcnt = 0;
         if (hh == 0) exr[wave][l32] = -__builtin_inff();
       }
+      slots(0, NSL / 8);
 
       // ---- running maximum per tile -------------------------------------------
       // A tile is worth listing only for a valid row, before the row's causal
@@ -351,6 +385,7 @@ __global__ __launch_bounds__(256, 2) void select_wave_kernel(
           nrec = g;
         }
       }
+      slots(NSL / 8, NSL / 4);
 #pragma unroll
       for (int bb = 0; bb < 2; ++bb)
         if (rec[bb]) {
@@ -358,6 +393,7 @@ __global__ __launch_bounds__(256, 2) void select_wave_kernel(
           nml[wave][l32][rpos[bb]] = tk / BK;
         }
       listcnt += nrec;
+      slots(NSL / 4, 3 * NSL / 8);
 
       // ---- decisions ------------------------------------------------------------
       // d = s^ - (m^ - gap): selected outright when d > band, ambiguous when
@@ -373,10 +409,15 @@ __global__ __launch_bounds__(256, 2) void select_wave_kernel(
         uint32_t bt = 0;
         float dmin = __builtin_inff();
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const float d = acc[bb][e] - mid[bb];
-          bt |= uint32_t(d > band) << e;
-          dmin = __builtin_fminf(dmin, __builtin_fabsf(d));
+        for (int half = 0; half < 2; ++half) {
+#pragma unroll
+          for (int e = 8 * half; e < 8 * half + 8; ++e) {
+            const float d = acc[bb][e] - mid[bb];
+            bt |= uint32_t(d > band) << e;
+            dmin = __builtin_fminf(dmin, __builtin_fabsf(d));
+          }
+          const int sl = 3 * NSL / 8 + (2 * bb + half) * NSL / 8;
+          slots(sl, sl + NSL / 8);
         }
         bits[bb] = bt;
         amb_lane = amb_lane || (dmin <= band);
@@ -457,6 +498,7 @@ __global__ __launch_bounds__(256, 2) void select_wave_kernel(
         bits[1] |= ovr[1];
       }
       append(kb0, 0, bits[0]);
+      slots(7 * NSL / 8, NSL);
       append(kb0, 1, bits[1]);
     }
 #pragma unroll
