@@ -106,19 +106,29 @@ int va_select(int dtype, const void* qs, int64_t sqb, int64_t sqh, int64_t sqn,
 
 /*
  * Split selection ("key segments"), the form va_prefill uses internally: the
- * keys are cut into segments of segment_keys keys (a multiple of 64 and of the
- * group span k_local_size*group_k_block, at most 64 segments) that are
- * selected independently.  Segment s of row J writes its keys in ascending
- * order from slot max(s*segment_keys, smin) - smin of the row's index layout
- * and its count to counts[((b*Hq + h)*nc + (J - J0))*nseg + s], nseg =
- * ceil(Sk / segment_keys); a row's list is the concatenation of its segments.
- * Needs the VA_SEL_WAVE kernel's conditions and `scratch`.  No counterpart
- * in the reference (its single launch writes dense rows); the selected sets
- * are the reference rule's, as for va_select.
+ * keys are cut into segments of segment_keys keys (a multiple of 64, at most
+ * 64 segments) that are selected in parallel.  When segment_keys is also a
+ * multiple of the group span k_local_size*group_k_block, every segment starts
+ * a group and one pass suffices.  When one group covers a whole row (group
+ * span >= Sk; the DiT configurations), a first pass records each segment's
+ * maxima and a second pass selects every segment from the maxima of the
+ * segments before it, in scratch (va_select_segments_scratch_floats).
+ * Segment s of row J writes its keys in ascending order from slot
+ * max(s*segment_keys, smin) - smin of the row's index layout and its count to
+ * counts[((b*Hq + h)*nc + (J - J0))*nseg + s], nseg = ceil(Sk / segment_keys);
+ * a row's list is the concatenation of its segments.  Needs the VA_SEL_WAVE
+ * kernel's conditions.  No counterpart in the reference (its single launch
+ * writes dense rows); the selected sets are the reference rule's, as for
+ * va_select.
  * va_select_segment_keys returns the segment length va_prefill uses, 0 when
- * the groups are too long to split, or -1 on invalid sizes.
+ * the keys are not split, or -1 on invalid sizes.
  */
 int64_t va_select_segment_keys(int64_t Sk, int64_t k_local_size, int64_t group_k_block);
+/* fp32 scratch floats va_select_segments needs: the key norms, plus two floats
+ * per (row, segment) in the two-pass form.  -1 on invalid sizes. */
+int64_t va_select_segments_scratch_floats(int64_t B, int64_t Hq, int64_t Hk, int64_t Sk,
+                                          int64_t nc, int64_t segment_keys,
+                                          int64_t k_local_size, int64_t group_k_block);
 int va_select_segments(int dtype, const void* qs, int64_t sqb, int64_t sqh, int64_t sqn,
                        const void* k, int64_t skb, int64_t skh, int64_t sks, int64_t B,
                        int64_t Hq, int64_t Hk, int64_t Sk, int64_t D, int64_t q_pooling_size,

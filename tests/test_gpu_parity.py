@@ -165,6 +165,15 @@ SEGMENT_CASES = [
     ("causal-G16-seg512-chunked", 4, 1, 3000, 128, torch.bfloat16, True, 16, 16, 0.10, 512, 12),
     ("noncausal-bk32-G4-seg128", 2, 2, 1500, 64, torch.float16, False, 32, 4, 0.15, 128, None),
     ("causal-gap0-seg256", 2, 1, 2048, 128, torch.bfloat16, True, 16, 16, None, 256, None),
+    # one group per row (DiT-style G): maxima pass, then the carry pass
+    ("noncausal-G8192-2pass-seg2048", 2, 2, 9000, 128, torch.bfloat16, False, 16, 8192, 0.15,
+     2048, None),
+    ("noncausal-G8192-2pass-seg512-chunked", 2, 1, 5000, 64, torch.float16, False, 16, 8192,
+     0.10, 512, 40),
+    ("causal-Glong-2pass-seg1024", 2, 1, 4096, 128, torch.bfloat16, True, 16, 1024, 0.10, 1024,
+     None),
+    ("noncausal-2pass-gap0-seg1024", 2, 2, 4100, 128, torch.bfloat16, False, 16, 8192, None,
+     1024, None),
 ]
 
 
@@ -351,6 +360,8 @@ E2E_CASES = [
     # name, B, Hq, Hk, S, D, dtype, causal, qps, bk, G, chunk, threshold
     ("vlm-like-causal", 1, 8, 2, 2048, 128, torch.bfloat16, True, 64, 16, 16, 1024, 0.5),
     ("dit-like-noncausal", 1, 4, 4, 2000, 128, torch.bfloat16, False, 64, 16, 8192, 1024, 0.3),
+    # long enough for the two-pass split selection (segments of 4096 keys)
+    ("dit-like-2pass", 1, 2, 2, 9000, 128, torch.bfloat16, False, 64, 16, 8192, 4608, 0.3),
     ("causal-qps128-bk16", 1, 4, 4, 1300, 64, torch.bfloat16, True, 128, 16, 4, 512, 0.6),
     ("A-fp32-noncausal", 1, 4, 4, 4096, 64, torch.float32, False, 64, 16, 16, 4096, 0.35),
 ]

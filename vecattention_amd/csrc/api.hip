@@ -39,9 +39,10 @@ hipError_t launch_select_wave(int dtype, const void* qs, int64_t sqb, int64_t sq
                               int64_t Hq, int64_t Hk, int64_t Sk, int64_t D, int64_t qps,
                               int64_t bk, int64_t group, int causal, int64_t bsq, float gap,
                               const float* gaps, const float* kmax, const RowLayout& lay,
-                              int32_t* counts, int32_t* indices, int64_t segk,
-                              hipStream_t stream);
+                              int32_t* counts, int32_t* indices, int64_t segk, float2* carry,
+                              int mode, hipStream_t stream);
 int64_t select_wave_segment_keys(int64_t Sk, int64_t bk, int64_t group);
+int64_t select_wave_carry_segment_keys(int64_t Sk, int64_t bk, int64_t group);
 int64_t key_norm_scratch_floats(int64_t B, int64_t Hk);
 hipError_t launch_key_norm(int dtype, const void* k, int64_t skb, int64_t skh, int64_t sks,
                            int64_t B, int64_t Hk, int64_t Sk, int64_t D, float* scratch,
@@ -191,14 +192,15 @@ static int select_impl(int dtype, const void* qs, int64_t sqb, int64_t sqh, int6
                        int64_t group, int causal, int wo_init, int64_t J0, int64_t nc,
                        int64_t bsq, float gap, const float* gaps, int64_t dense_stride,
                        int32_t* counts, int32_t* indices, SelKernel which, const float* kmax,
-                       int64_t segk, hipStream_t stream) {
+                       int64_t segk, hipStream_t stream, float2* carry = nullptr,
+                       int mode = 0) {
   const va::RowLayout lay = make_layout(J0, nc, qps, Sk, causal, wo_init, dense_stride);
   group = effective_group(group, Sk, bk);
   hipError_t e;
   if (which == kSelWave)
     e = va::launch_select_wave(dtype, qs, sqb, sqh, sqn, k, skb, skh, sks, B, Hq, Hk, Sk, D, qps,
                                bk, group, causal, bsq, gap, gaps, kmax, lay, counts, indices,
-                               segk, stream);
+                               segk, carry, mode, stream);
   else if (which == kSelMfma)
     e = va::launch_select_mfma(dtype, qs, sqb, sqh, sqn, k, skb, skh, sks, B, Hq, Hk, Sk, D, qps,
                                bk, group, causal, bsq, gap, gaps, kmax, lay, counts, indices,
@@ -281,11 +283,31 @@ int va_select(int dtype, const void* qs, int64_t sqb, int64_t sqh, int64_t sqn,
 }
 
 // Segments of the split selection.  The segment length must be a multiple of
-// the 64-key chunk and of the group span, with at most 64 segments.
+// the 64-key chunk and of the group span (one pass), or the groups must cover
+// every key of a row (two passes, carried maxima), with at most 64 segments.
 int64_t va_select_segment_keys(int64_t Sk, int64_t k_local_size, int64_t group_k_block) {
   if (Sk <= 0 || k_local_size <= 0 || group_k_block <= 0) return -1;
-  return va::select_wave_segment_keys(Sk, k_local_size,
-                                      effective_group(group_k_block, Sk, k_local_size));
+  const int64_t g = effective_group(group_k_block, Sk, k_local_size);
+  const int64_t segk = va::select_wave_segment_keys(Sk, k_local_size, g);
+  return segk > 0 ? segk : va::select_wave_carry_segment_keys(Sk, k_local_size, g);
+}
+
+// The two-pass form: the groups cover every key of a row and the segments do
+// not start groups.
+static bool segments_two_pass(int64_t Sk, int64_t bk, int64_t group, int64_t segment_keys) {
+  const int64_t gs = bk * effective_group(group, Sk, bk);
+  return segment_keys % gs != 0 && gs >= Sk;
+}
+
+int64_t va_select_segments_scratch_floats(int64_t B, int64_t Hq, int64_t Hk, int64_t Sk,
+                                          int64_t nc, int64_t segment_keys,
+                                          int64_t k_local_size, int64_t group_k_block) {
+  if (B <= 0 || Hq <= 0 || Hk <= 0 || Sk <= 0 || nc <= 0 || segment_keys <= 0 ||
+      k_local_size <= 0 || group_k_block <= 0)
+    return -1;
+  const int64_t kn = (va::key_norm_scratch_floats(B, Hk) + 3) / 4 * 4;
+  if (!segments_two_pass(Sk, k_local_size, group_k_block, segment_keys)) return kn;
+  return kn + 2 * B * Hq * nc * cdiv(Sk, segment_keys);  // (MFMA max, exact max) per segment
 }
 
 int va_select_segments(int dtype, const void* qs, int64_t sqb, int64_t sqh, int64_t sqn,
@@ -304,20 +326,30 @@ int va_select_segments(int dtype, const void* qs, int64_t sqb, int64_t sqh, int6
   if (!select_wave_ok(dtype, qs, sqb, sqh, sqn, k, skb, skh, sks, Sk, D, bk, group))
     return fail(VA_ERR_UNSUPPORTED, "segmented selection needs the wave selection kernel");
   const int64_t gs = bk * effective_group(group, Sk, bk);
-  if (segment_keys <= 0 || segment_keys % 64 || segment_keys % gs ||
-      cdiv(Sk, segment_keys) > 64)
+  if (segment_keys <= 0 || segment_keys % 64 || cdiv(Sk, segment_keys) > 64 ||
+      (segment_keys % gs != 0 && gs < Sk))
     return fail(VA_ERR_ARG, "segment_keys %lld: need a multiple of 64 and of the group span "
-                            "(%lld keys), at most 64 segments",
+                            "(%lld keys) unless one group covers the row, at most 64 segments",
                 (long long)segment_keys, (long long)gs);
-  if (!scratch || scratch_floats < va::key_norm_scratch_floats(B, Hk))
-    return fail(VA_ERR_ARG, "segmented selection needs scratch");
+  const bool two_pass = segments_two_pass(Sk, bk, group, segment_keys);
+  const int64_t need = va_select_segments_scratch_floats(B, Hq, Hk, Sk, nc, segment_keys, bk, group);
+  if (!scratch || scratch_floats < need)
+    return fail(VA_ERR_ARG, "segmented selection needs %lld scratch floats", (long long)need);
   hipStream_t st = static_cast<hipStream_t>(stream);
   rc = hip_check(va::launch_key_norm(dtype, k, skb, skh, sks, B, Hk, Sk, D, scratch, st),
                  "key norm launch");
   if (rc) return rc;
+  float2* carry = reinterpret_cast<float2*>(scratch + (va::key_norm_scratch_floats(B, Hk) + 3) / 4 * 4);
+  if (two_pass) {
+    rc = select_impl(dtype, qs, sqb, sqh, sqn, k, skb, skh, sks, B, Hq, Hk, Sk, D, qps, bk, group,
+                     causal, wo_init, J0, nc, bsq, gap, gaps, dense_stride, counts, indices,
+                     kSelWave, scratch, segment_keys, st, carry, va::kPassMax);
+    if (rc) return rc;
+  }
   rc = select_impl(dtype, qs, sqb, sqh, sqn, k, skb, skh, sks, B, Hq, Hk, Sk, D, qps, bk, group,
                    causal, wo_init, J0, nc, bsq, gap, gaps, dense_stride, counts, indices,
-                   kSelWave, scratch, segment_keys, st);
+                   kSelWave, scratch, segment_keys, st, carry,
+                   two_pass ? va::kPassCarry : va::kPassPlain);
   return rc ? rc : ok();
 }
 
@@ -445,15 +477,18 @@ int va_sparse_attn_segments(int dtype, const void* q, int64_t sqb, int64_t sqh, 
                           int(cdiv(Sk, segment_keys)), segment_keys, stream);
 }
 
-// Workspace of va_prefill: [scaled pooled q][counts][indices], 256-byte aligned.
+// Workspace of va_prefill: [scaled pooled q][counts][indices][key norms]
+// [segment maxima], 256-byte aligned.
 static void prefill_segments(int dtype, int64_t B, int64_t Hq, int64_t Sq, int64_t Sk, int64_t D,
                              int64_t qps, int causal, int64_t chunk, int64_t* qs_bytes,
-                             int64_t* cnt_bytes, int64_t* idx_bytes, int64_t* kn_bytes) {
+                             int64_t* cnt_bytes, int64_t* idx_bytes, int64_t* kn_bytes,
+                             int64_t* carry_bytes = nullptr) {
   *kn_bytes = align256(va::key_norm_scratch_floats(B, Hq) * 4);  // Hk <= Hq
   const int64_t nqb = cdiv(Sq, qps);
   *qs_bytes = align256(B * Hq * nqb * D * esize(dtype));
   const int64_t nc_max = cdiv(chunk < Sq ? chunk : Sq, qps);
   *cnt_bytes = align256(B * Hq * nc_max * 4 * kMaxSegments);  // per-segment counts
+  if (carry_bytes) *carry_bytes = align256(B * Hq * nc_max * 8 * kMaxSegments);  // (max, exact)
   int64_t idx_max = 0;
   for (int64_t i = 0; i < Sq; i += chunk) {
     const int64_t rows = (Sq - i < chunk) ? (Sq - i) : chunk;
@@ -470,9 +505,9 @@ int64_t va_prefill_workspace_size(int dtype, int64_t B, int64_t Hq, int64_t Sq, 
   if (!dtype_ok(dtype) || B <= 0 || Hq <= 0 || Sq <= 0 || Sk <= 0 || D <= 0 || qps <= 0 ||
       chunk_size <= 0 || chunk_size % qps)
     return -1;
-  int64_t a, b, c, d;
-  prefill_segments(dtype, B, Hq, Sq, Sk, D, qps, causal, chunk_size, &a, &b, &c, &d);
-  return a + b + c + d;
+  int64_t a, b, c, d, e;
+  prefill_segments(dtype, B, Hq, Sq, Sk, D, qps, causal, chunk_size, &a, &b, &c, &d, &e);
+  return a + b + c + d + e;
 }
 
 int va_prefill(int dtype, const void* q, int64_t sqb, int64_t sqh, int64_t sqs, const void* k,
@@ -493,14 +528,15 @@ int va_prefill(int dtype, const void* q, int64_t sqb, int64_t sqh, int64_t sqs, 
     return fail(VA_ERR_WORKSPACE, "workspace %lld bytes < required %lld",
                 (long long)workspace_bytes, (long long)need);
   const int64_t nqb = cdiv(Sq, qps);
-  int64_t qs_bytes, cnt_bytes, idx_bytes, kn_bytes;
+  int64_t qs_bytes, cnt_bytes, idx_bytes, kn_bytes, carry_bytes;
   prefill_segments(dtype, B, Hq, Sq, Sk, D, qps, causal, chunk_size, &qs_bytes, &cnt_bytes,
-                   &idx_bytes, &kn_bytes);
+                   &idx_bytes, &kn_bytes, &carry_bytes);
   char* ws = static_cast<char*>(workspace);
   void* qs = ws;
   int32_t* counts = reinterpret_cast<int32_t*>(ws + qs_bytes);
   int32_t* indices = reinterpret_cast<int32_t*>(ws + qs_bytes + cnt_bytes);
   float* knorm = reinterpret_cast<float*>(ws + qs_bytes + cnt_bytes + idx_bytes);
+  float2* carry = reinterpret_cast<float2*>(ws + qs_bytes + cnt_bytes + idx_bytes + kn_bytes);
   hipStream_t st = static_cast<hipStream_t>(stream);
 
   int rc = va_pool(dtype, q, B, Hq, Sq, D, sqb, sqh, sqs, qps, nullptr, qs, stream);
@@ -520,14 +556,23 @@ int va_prefill(int dtype, const void* q, int64_t sqb, int64_t sqh, int64_t sqs, 
     if (rc) return rc;
   }
   // Split the selection into key segments when the wave kernel and the MFMA
-  // attention (which reads the segmented lists) both run.
+  // attention (which reads the segmented lists) both run: segments that each
+  // start a group when the groups are short, otherwise (one group per row) a
+  // maxima pass followed by a carry pass.
   int64_t segk = 0;
+  bool two_pass = false;
   {
     const int64_t sq[3] = {sqb, sqh, sqs}, sk[3] = {skb, skh, sks}, sv[3] = {svb, svh, svs},
                   so[3] = {sob, soh, sos};
     if (which == kSelWave &&
-        attn_mfma_check(dtype, q, sq, k, sk, v, sv, out, so, Sk, D, qps).ok())
-      segk = va::select_wave_segment_keys(Sk, bk, effective_group(group, Sk, bk));
+        attn_mfma_check(dtype, q, sq, k, sk, v, sv, out, so, Sk, D, qps).ok()) {
+      const int64_t g = effective_group(group, Sk, bk);
+      segk = va::select_wave_segment_keys(Sk, bk, g);
+      if (segk == 0) {
+        segk = va::select_wave_carry_segment_keys(Sk, bk, g);
+        two_pass = segk > 0;
+      }
+    }
   }
   const int nseg = segk > 0 ? int(cdiv(Sk, segk)) : 1;
   const float scale = float(1.0 / std::sqrt(double(D)));
@@ -536,9 +581,15 @@ int va_prefill(int dtype, const void* q, int64_t sqb, int64_t sqh, int64_t sqs, 
     const int64_t J0 = i / qps, nc = cdiv(rows, qps);
     const int64_t es = esize(dtype);
     const void* qs_chunk = static_cast<const char*>(qs) + J0 * D * es;
+    if (two_pass) {
+      rc = select_impl(dtype, qs_chunk, Hq * nqb * D, nqb * D, D, k, skb, skh, sks, B, Hq, Hk,
+                       Sk, D, qps, bk, group, causal, causal, J0, nc, bsq, gap, gaps, 0, counts,
+                       indices, which, knorm, segk, st, carry, va::kPassMax);
+      if (rc) return rc;
+    }
     rc = select_impl(dtype, qs_chunk, Hq * nqb * D, nqb * D, D, k, skb, skh, sks, B, Hq, Hk, Sk,
                      D, qps, bk, group, causal, causal, J0, nc, bsq, gap, gaps, 0, counts, indices,
-                     which, knorm, segk, st);
+                     which, knorm, segk, st, carry, two_pass ? va::kPassCarry : va::kPassPlain);
     if (rc) return rc;
     rc = sparse_attn_impl(dtype, q, sqb, sqh, sqs, k, skb, skh, sks, v, svb, svh, svs, out, sob,
                           soh, sos, B, Hq, Hk, Sq, Sk, D, qps, causal, causal, J0, nc, 0, counts,

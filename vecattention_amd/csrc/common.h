@@ -8,6 +8,14 @@ namespace va {
 
 enum DType : int { kF32 = 0, kBF16 = 1, kF16 = 2 };
 
+// Passes of the wave selection kernel.  A selection whose groups are longer
+// than a key segment runs twice: the maxima pass scores every segment and
+// records, per row, the segment's MFMA maximum and its exact maximum; the
+// carry pass then selects each segment starting from the maxima of the
+// earlier segments of the same group, which are exactly the running maxima a
+// sequential walk would hold there.  Plain: one pass, no carried state.
+enum SelectPass : int { kPassPlain = 0, kPassMax = 1, kPassCarry = 2 };
+
 // Raw 16-bit storage types; arithmetic goes through explicit conversions so
 // that every rounding step is visible.
 struct bf16_t { uint16_t bits; };

@@ -49,6 +49,7 @@ constexpr int kWWaves = 4;         // waves per work-group
 constexpr int kWChunk = 64;        // keys per chunk
 constexpr int kWList = 16;         // near-max tiles per row
 
+
 // MFMA row m of the K operand -> key offset inside the 32-key block, such that
 // accumulator element e of lane l holds key 16*(l/32) + e.
 __device__ inline int wkperm(int m) { return 16 * ((m >> 2) & 1) + 4 * (m >> 3) + (m & 3); }
@@ -88,7 +89,7 @@ __global__ __launch_bounds__(256, 2) void select_wave_kernel(
     int64_t qps, uint32_t gspan, int causal, int64_t bsq, float gap_scalar,
     const float* __restrict__ gaps, const float* __restrict__ kmax, RowLayout lay,
     int32_t* __restrict__ counts, int32_t* __restrict__ indices, int64_t nrowsets, int segk,
-    int nseg) {
+    int nseg, float2* __restrict__ carry, int mode) {
   using M = Mfma<T>;
   using vec = typename M::vec;
   constexpr int NS = D / 16;                    // MFMA steps over the features
@@ -240,8 +241,23 @@ __global__ __launch_bounds__(256, 2) void select_wave_kernel(
     }
   };
 
-  // The first visited chunk need not start a group: start with no folded tiles.
-  if (hh == 0) exr[wave][l32] = -__builtin_inff();
+  // The first visited chunk need not start a group: start with no folded tiles
+  // (or, in the carry pass, with the maxima of the group's earlier segments).
+  const int64_t crow = (bh * nc + jr) * nseg;  // this row's carry records
+  if (mode == kPassCarry) {
+    const int64_t g0 = (int64_t(seg_lo) / int64_t(gspan)) * int64_t(gspan);  // group start
+    float cm = -__builtin_inff(), ce = -__builtin_inff();
+    if (valid)
+      for (int s2 = int(g0 / segk); s2 < seg; ++s2) {
+        const float2 cr = carry[crow + s2];
+        cm = __builtin_fmaxf(cm, cr.x);
+        ce = __builtin_fmaxf(ce, cr.y);
+      }
+    m = cm;
+    if (hh == 0) exr[wave][l32] = ce;
+  } else if (hh == 0) {
+    exr[wave][l32] = -__builtin_inff();
+  }
   ambk[wave][64 + lane] = 0;  // resolved flags start cleared
 
   // Append this lane's selected keys of block bb (bits over keys key0 + e).
@@ -257,6 +273,71 @@ __global__ __launch_bounds__(256, 2) void select_wave_kernel(
       ++pos;
     }
     rowcnt += cnt + ocnt;
+  };
+
+  // Exact resolution of the rows in `need` (bit r for row r), one row at a
+  // time: row r's jobs are every key of its listed tiles, then its ambiguous
+  // keys (ambm, as chunk offsets from kb0); the exact tile maxima give the
+  // exact running maximum at each ambiguous key's tile.  Resolved selections
+  // go to ovr, the listed tiles are folded into the row's exact maximum and
+  // the list is cleared.
+  auto resolve = [&](uint64_t need, int kb0, uint32_t (&ovr)[2]) {
+    while (need) {
+      const int r = __builtin_ctzll(need);
+      need &= need - 1;
+      const int n = __builtin_amdgcn_readlane(listcnt, r);
+      const T* qr = qs + b * sqb + h * sqh + (jr_wave + r) * sqn;
+      // Ambiguous keys of row r, as chunk offsets 32b + 16hh + e (64 bits).
+      const uint64_t a64 = uint64_t(ambm[wave][r][0]) | (uint64_t(ambm[wave][r][1]) << 16) |
+                           (uint64_t(ambm[wave][r][2]) << 32) |
+                           (uint64_t(ambm[wave][r][3]) << 48);
+      if ((a64 >> lane) & 1u)
+        ambk[wave][__builtin_amdgcn_mbcnt_hi(uint32_t(a64 >> 32),
+                                             __builtin_amdgcn_mbcnt_lo(uint32_t(a64), 0))] =
+            kb0 + lane;
+      const int ntile = n * BK, njobs = ntile + __builtin_popcountll(a64);
+      float E0 = exr[wave][r];
+      uint64_t take = 0;
+      for (int p = 0; p < njobs; p += 64) {
+        const int j = p + lane;
+        int key = -1;
+        if (j < ntile) key = nml[wave][r][j / BK] * BK + j % BK;
+        else if (j < njobs) key = ambk[wave][j - ntile];
+        float ex = -__builtin_inff();
+        if (key >= smin && key < sk) ex = exact_dot_global<T, D>(qr, kh + int64_t(key) * sks);
+        // exact maxima of the listed tiles (groups of BK lanes)
+        float tx = j < ntile ? ex : -__builtin_inff();
+#pragma unroll
+        for (int o = 1; o < BK; o <<= 1) tx = __builtin_fmaxf(tx, __shfl_xor(tx, o));
+        if (j < ntile && j % BK == 0) tmx[wave][j / BK] = tx;
+        // decisions of the ambiguous keys of this pass (all tile maxima
+        // come from this or earlier passes)
+        bool tk = false;
+        if (j >= ntile && j < njobs) {
+          const int t = key / BK;
+          float E = E0;
+          for (int i = 0; i < n; ++i)
+            if (nml[wave][r][i] <= t) E = __builtin_fmaxf(E, tmx[wave][i]);
+          tk = (ex + gap) >= E;
+        }
+        // Fold: bit (key - kb0) of the row's resolved selections.
+        if (tk) ambk[wave][64 + key - kb0] = 1;
+      }
+      // Gather the resolved bits: lane l reads the flag of chunk offset l.
+      const int fl = (a64 >> lane) & 1u ? ambk[wave][64 + lane] : 0;
+      take = __builtin_amdgcn_ballot_w64(fl == 1);
+      if ((a64 >> lane) & 1u) ambk[wave][64 + lane] = 0;
+      // This lane's quarter (2*bb + hh) of row r.
+      if (l32 == r) {
+        ovr[0] |= uint32_t(take >> (16 * hh)) & 0xffffu;
+        ovr[1] |= uint32_t(take >> (32 + 16 * hh)) & 0xffffu;
+      }
+      // Fold the listed tiles into the row's exact maximum.
+      float E = E0;
+      for (int i = 0; i < n; ++i) E = __builtin_fmaxf(E, tmx[wave][i]);
+      if (lane == 0) exr[wave][r] = E;
+      if (l32 == r) listcnt = 0;
+    }
   };
 
   // ---- chunk loop -------------------------------------------------------------
@@ -408,13 +489,16 @@ __global__ __launch_bounds__(256, 2) void select_wave_kernel(
         mid[bb] = ok ? mt[bb] - gap : __builtin_inff();
         uint32_t bt = 0;
         float dmin = __builtin_inff();
+        if (mode == kPassMax) mid[bb] = __builtin_inff();  // maxima only: select nothing
 #pragma unroll
         for (int half = 0; half < 2; ++half) {
+          if (mode != kPassMax) {
 #pragma unroll
-          for (int e = 8 * half; e < 8 * half + 8; ++e) {
-            const float d = acc[bb][e] - mid[bb];
-            bt |= uint32_t(d > band) << e;
-            dmin = __builtin_fminf(dmin, __builtin_fabsf(d));
+            for (int e = 8 * half; e < 8 * half + 8; ++e) {
+              const float d = acc[bb][e] - mid[bb];
+              bt |= uint32_t(d > band) << e;
+              dmin = __builtin_fminf(dmin, __builtin_fabsf(d));
+            }
           }
           const int sl = 3 * NSL / 8 + (2 * bb + half) * NSL / 8;
           slots(sl, sl + NSL / 8);
@@ -438,71 +522,26 @@ __global__ __launch_bounds__(256, 2) void select_wave_kernel(
         const bool row_amb = (uint32_t(amb_lane) | other_half(uint32_t(amb_lane))) != 0u;
         uint64_t need = __builtin_amdgcn_ballot_w64(hh == 0 && (row_amb || listcnt > kWList - 4));
         uint32_t ovr[2] = {0u, 0u};
-        while (need) {
-          const int r = __builtin_ctzll(need);
-          need &= need - 1;
-          const int n = __builtin_amdgcn_readlane(listcnt, r);
-          const T* qr = qs + b * sqb + h * sqh + (jr_wave + r) * sqn;
-          // Ambiguous keys of row r, as chunk offsets 32b + 16hh + e (64 bits).
-          const uint64_t a64 = uint64_t(ambm[wave][r][0]) | (uint64_t(ambm[wave][r][1]) << 16) |
-                               (uint64_t(ambm[wave][r][2]) << 32) |
-                               (uint64_t(ambm[wave][r][3]) << 48);
-          if ((a64 >> lane) & 1u)
-            ambk[wave][__builtin_amdgcn_mbcnt_hi(uint32_t(a64 >> 32),
-                                                 __builtin_amdgcn_mbcnt_lo(uint32_t(a64), 0))] =
-                kb0 + lane;
-          const int ntile = n * BK, njobs = ntile + __builtin_popcountll(a64);
-          float E0 = exr[wave][r];
-          uint64_t take = 0;
-          for (int p = 0; p < njobs; p += 64) {
-            const int j = p + lane;
-            int key = -1;
-            if (j < ntile) key = nml[wave][r][j / BK] * BK + j % BK;
-            else if (j < njobs) key = ambk[wave][j - ntile];
-            float ex = -__builtin_inff();
-            if (key >= smin && key < sk) ex = exact_dot_global<T, D>(qr, kh + int64_t(key) * sks);
-            // exact maxima of the listed tiles (groups of BK lanes)
-            float tx = j < ntile ? ex : -__builtin_inff();
-#pragma unroll
-            for (int o = 1; o < BK; o <<= 1) tx = __builtin_fmaxf(tx, __shfl_xor(tx, o));
-            if (j < ntile && j % BK == 0) tmx[wave][j / BK] = tx;
-            // decisions of the ambiguous keys of this pass (all tile maxima
-            // come from this or earlier passes)
-            bool tk = false;
-            if (j >= ntile && j < njobs) {
-              const int t = key / BK;
-              float E = E0;
-              for (int i = 0; i < n; ++i)
-                if (nml[wave][r][i] <= t) E = __builtin_fmaxf(E, tmx[wave][i]);
-              tk = (ex + gap) >= E;
-            }
-            // Fold: bit (key - kb0) of the row's resolved selections.
-            if (tk) ambk[wave][64 + key - kb0] = 1;
-          }
-          // Gather the resolved bits: lane l reads the flag of chunk offset l.
-          const int fl = (a64 >> lane) & 1u ? ambk[wave][64 + lane] : 0;
-          take = __builtin_amdgcn_ballot_w64(fl == 1);
-          if ((a64 >> lane) & 1u) ambk[wave][64 + lane] = 0;
-          // This lane's quarter (2*bb + hh) of row r.
-          if (l32 == r) {
-            ovr[0] |= uint32_t(take >> (16 * hh)) & 0xffffu;
-            ovr[1] |= uint32_t(take >> (32 + 16 * hh)) & 0xffffu;
-          }
-          // Fold the listed tiles into the row's exact maximum.
-          float E = E0;
-          for (int i = 0; i < n; ++i) E = __builtin_fmaxf(E, tmx[wave][i]);
-          if (lane == 0) exr[wave][r] = E;
-          if (l32 == r) listcnt = 0;
-        }
+        resolve(need, kb0, ovr);
         bits[0] |= ovr[0];
         bits[1] |= ovr[1];
       }
-      append(kb0, 0, bits[0]);
+      if (mode != kPassMax) append(kb0, 0, bits[0]);
       slots(7 * NSL / 8, NSL);
-      append(kb0, 1, bits[1]);
+      if (mode != kPassMax) append(kb0, 1, bits[1]);
     }
 #pragma unroll
     for (int bb = 0; bb < 2; ++bb) acc[bb] = nxt[bb];
+  }
+
+  if (mode == kPassMax) {
+    // Fold the tiles still listed, then record the segment's maxima.
+    ambm[wave][l32][hh] = 0u;
+    ambm[wave][l32][2 + hh] = 0u;
+    uint32_t ovr[2] = {0u, 0u};
+    resolve(__builtin_amdgcn_ballot_w64(hh == 0 && valid && listcnt > 0), 0, ovr);
+    if (valid && hh == 0) carry[crow + seg] = make_float2(m, exr[wave][l32]);
+    return;
   }
 
   if (valid && hh == 0) counts[(bh * nc + jr) * nseg + seg] = rowcnt < cap ? rowcnt : (cap > 0 ? cap : 0);
@@ -521,6 +560,18 @@ int64_t select_wave_segment_keys(int64_t Sk, int64_t bk, int64_t group) {
   return segk < Sk ? segk : 0;
 }
 
+// Key segments of the two-pass split (maxima pass, then carry pass), for rows
+// that are one group long (group span >= Sk): a multiple of the 64-key chunk,
+// about 4096 keys, at most 64 segments; 0 when there is nothing to split.
+int64_t select_wave_carry_segment_keys(int64_t Sk, int64_t bk, int64_t group) {
+  constexpr int64_t kTarget = 4096, kMaxSeg = 64;
+  if (bk * group < Sk) return 0;
+  int64_t want = (Sk + kMaxSeg - 1) / kMaxSeg;
+  if (want < kTarget) want = kTarget;
+  const int64_t segk = (want + kWChunk - 1) / kWChunk * kWChunk;
+  return segk < Sk ? segk : 0;
+}
+
 bool select_wave_supported(int dtype, int64_t D, int64_t bk, int64_t group) {
   return (dtype == kBF16 || dtype == kF16) && (D == 64 || D == 128) &&
          (bk == 16 || bk == 32 || bk == 64) && (bk * group) % kWChunk == 0;
@@ -533,7 +584,8 @@ static hipError_t launch_select_wave_tdb(const void* qs, int64_t sqb, int64_t sq
                                          int64_t qps, int64_t group, int causal, int64_t bsq,
                                          float gap, const float* gaps, const float* kmax,
                                          const RowLayout& lay, int32_t* counts, int32_t* indices,
-                                         int64_t segk, hipStream_t stream) {
+                                         int64_t segk, float2* carry, int mode,
+                                         hipStream_t stream) {
   const int64_t nrowsets = (lay.nc + kWWaves * kWRows - 1) / (kWWaves * kWRows);
   const int64_t nseg = segk > 0 ? (Sk + segk - 1) / segk : 1;
   // Group span in keys, capped at 2^31 (key offsets are below 2^24, so a span
@@ -543,7 +595,8 @@ static hipError_t launch_select_wave_tdb(const void* qs, int64_t sqb, int64_t sq
   hipLaunchKernelGGL((select_wave_kernel<T, D, BK>), dim3(unsigned(nblocks)), dim3(256), 0,
                      stream, static_cast<const T*>(qs), sqb, sqh, sqn, static_cast<const T*>(k),
                      skb, skh, sks, B, Hq, Hk, Sk, qps, uint32_t(gs), causal, bsq, gap, gaps, kmax,
-                     lay, counts, indices, nrowsets, int(segk > 0 ? segk : 0), int(nseg));
+                     lay, counts, indices, nrowsets, int(segk > 0 ? segk : 0), int(nseg), carry,
+                     mode);
   return hipGetLastError();
 }
 
@@ -554,12 +607,13 @@ static hipError_t launch_select_wave_td(int64_t bk, const void* qs, int64_t sqb,
                                         int64_t qps, int64_t group, int causal, int64_t bsq,
                                         float gap, const float* gaps, const float* kmax,
                                         const RowLayout& lay, int32_t* counts, int32_t* indices,
-                                        int64_t segk, hipStream_t stream) {
+                                        int64_t segk, float2* carry, int mode,
+                                        hipStream_t stream) {
 #define VA_SELW_BK(BB)                                                                          \
   if (bk == BB)                                                                                 \
     return launch_select_wave_tdb<T, D, BB>(qs, sqb, sqh, sqn, k, skb, skh, sks, B, Hq, Hk, Sk, \
                                             qps, group, causal, bsq, gap, gaps, kmax, lay,      \
-                                            counts, indices, segk, stream);
+                                            counts, indices, segk, carry, mode, stream);
   VA_SELW_BK(16)
   VA_SELW_BK(32)
   VA_SELW_BK(64)
@@ -572,12 +626,12 @@ hipError_t launch_select_wave(int dtype, const void* qs, int64_t sqb, int64_t sq
                               int64_t Hq, int64_t Hk, int64_t Sk, int64_t D, int64_t qps,
                               int64_t bk, int64_t group, int causal, int64_t bsq, float gap,
                               const float* gaps, const float* kmax, const RowLayout& lay,
-                              int32_t* counts, int32_t* indices, int64_t segk,
-                              hipStream_t stream) {
+                              int32_t* counts, int32_t* indices, int64_t segk, float2* carry,
+                              int mode, hipStream_t stream) {
 #define VA_SELW_CASE(TT, DD)                                                                 \
   return launch_select_wave_td<TT, DD>(bk, qs, sqb, sqh, sqn, k, skb, skh, sks, B, Hq, Hk, \
                                        Sk, qps, group, causal, bsq, gap, gaps, kmax, lay,    \
-                                       counts, indices, segk, stream);
+                                       counts, indices, segk, carry, mode, stream);
   if (dtype == kBF16 && D == 128) { VA_SELW_CASE(bf16_t, 128) }
   if (dtype == kBF16 && D == 64) { VA_SELW_CASE(bf16_t, 64) }
   if (dtype == kF16 && D == 128) { VA_SELW_CASE(f16_t, 128) }

@@ -126,7 +126,10 @@ def select_segments(qs_chunk, k, J0, gap, gaps, causal, q_pooling_size, k_local_
     cap = index_capacity(B, Hq, Sk, q_pooling_size, causal, wo_init, J0, nc, dense_stride)
     counts = torch.empty(B, Hq, nc, nseg, dtype=torch.int32, device=k.device)
     indices = torch.empty(max(cap, 1), dtype=torch.int32, device=k.device)
-    nscr = int(nat.lib().va_select_scratch_floats(B, Hk))
+    nscr = int(nat.lib().va_select_segments_scratch_floats(B, Hq, Hk, Sk, nc, segk, k_local_size,
+                                                            group_k_block))
+    if nscr < 0:
+        raise AssertionError("va_select_segments_scratch_floats: invalid sizes")
     scratch = torch.empty(max(nscr, 1), dtype=torch.float32, device=k.device)
     with torch.cuda.device(k.device):
         rc = nat.lib().va_select_segments(
