@@ -119,6 +119,17 @@ def run_stages(wl, q, k, v, gap, out, events=None):
         ev["p1"].record()
     res = []
     nqb = qs.shape[2]
+    idx_buf = scr_buf = None
+    if segk:  # buffers for the largest chunk, reused (as the prefill's workspace is)
+        B, Hq, Hk, Sk = q.shape[0], q.shape[1], k.shape[1], k.shape[2]
+        caps, scrs = [], []
+        for i in range(0, S, wl.chunk_size):
+            J0, nc = i // qps, math.ceil(min(wl.chunk_size, S - i) / qps)
+            caps.append(stages.index_capacity(B, Hq, Sk, qps, wl.causal, wl.causal, J0, nc))
+            scrs.append(int(stages.nat.lib().va_select_segments_scratch_floats(
+                B, Hq, Hk, Sk, nc, segk, wl.k_local_size, wl.group_k_block)))
+        idx_buf = torch.empty(max(max(caps), 1), dtype=torch.int32, device=q.device)
+        scr_buf = torch.empty(max(max(scrs), 1), dtype=torch.float32, device=q.device)
     for ci, i in enumerate(range(0, S, wl.chunk_size)):
         J0 = i // qps
         nc = math.ceil(min(wl.chunk_size, S - i) / qps)
@@ -127,7 +138,7 @@ def run_stages(wl, q, k, v, gap, out, events=None):
         if segk:
             cnt, idx = stages.select_segments(qs[:, :, J0:J0 + nc], k, J0, gap, None, wl.causal,
                                               qps, wl.k_local_size, wl.group_k_block, wl.causal,
-                                              segk)
+                                              segk, indices=idx_buf, scratch=scr_buf)
         else:
             cnt, idx = stages.select_rows(qs[:, :, J0:J0 + nc], k, J0, gap, None, wl.causal, qps,
                                           wl.k_local_size, wl.group_k_block, wl.causal)

@@ -39,8 +39,9 @@ hipError_t launch_select_wave(int dtype, const void* qs, int64_t sqb, int64_t sq
                               int64_t Hq, int64_t Hk, int64_t Sk, int64_t D, int64_t qps,
                               int64_t bk, int64_t group, int causal, int64_t bsq, float gap,
                               const float* gaps, const float* kmax, const RowLayout& lay,
-                              int32_t* counts, int32_t* indices, int64_t segk, float2* carry,
+                              int32_t* counts, int32_t* indices, int64_t segk, void* carry,
                               int mode, hipStream_t stream);
+constexpr int64_t kSegCarryBytes = 32;  // per (row, segment) record of the two-pass selection
 int64_t select_wave_segment_keys(int64_t Sk, int64_t bk, int64_t group);
 int64_t select_wave_carry_segment_keys(int64_t Sk, int64_t bk, int64_t group);
 int64_t key_norm_scratch_floats(int64_t B, int64_t Hk);
@@ -192,7 +193,7 @@ static int select_impl(int dtype, const void* qs, int64_t sqb, int64_t sqh, int6
                        int64_t group, int causal, int wo_init, int64_t J0, int64_t nc,
                        int64_t bsq, float gap, const float* gaps, int64_t dense_stride,
                        int32_t* counts, int32_t* indices, SelKernel which, const float* kmax,
-                       int64_t segk, hipStream_t stream, float2* carry = nullptr,
+                       int64_t segk, hipStream_t stream, void* carry = nullptr,
                        int mode = 0) {
   const va::RowLayout lay = make_layout(J0, nc, qps, Sk, causal, wo_init, dense_stride);
   group = effective_group(group, Sk, bk);
@@ -305,9 +306,9 @@ int64_t va_select_segments_scratch_floats(int64_t B, int64_t Hq, int64_t Hk, int
   if (B <= 0 || Hq <= 0 || Hk <= 0 || Sk <= 0 || nc <= 0 || segment_keys <= 0 ||
       k_local_size <= 0 || group_k_block <= 0)
     return -1;
-  const int64_t kn = (va::key_norm_scratch_floats(B, Hk) + 3) / 4 * 4;
+  const int64_t kn = (va::key_norm_scratch_floats(B, Hk) + 7) / 8 * 8;  // 32-byte aligned
   if (!segments_two_pass(Sk, k_local_size, group_k_block, segment_keys)) return kn;
-  return kn + 2 * B * Hq * nc * cdiv(Sk, segment_keys);  // (MFMA max, exact max) per segment
+  return kn + va::kSegCarryBytes / 4 * B * Hq * nc * cdiv(Sk, segment_keys);  // carry records
 }
 
 int va_select_segments(int dtype, const void* qs, int64_t sqb, int64_t sqh, int64_t sqn,
@@ -339,7 +340,7 @@ int va_select_segments(int dtype, const void* qs, int64_t sqb, int64_t sqh, int6
   rc = hip_check(va::launch_key_norm(dtype, k, skb, skh, sks, B, Hk, Sk, D, scratch, st),
                  "key norm launch");
   if (rc) return rc;
-  float2* carry = reinterpret_cast<float2*>(scratch + (va::key_norm_scratch_floats(B, Hk) + 3) / 4 * 4);
+  void* carry = scratch + (va::key_norm_scratch_floats(B, Hk) + 7) / 8 * 8;
   if (two_pass) {
     rc = select_impl(dtype, qs, sqb, sqh, sqn, k, skb, skh, sks, B, Hq, Hk, Sk, D, qps, bk, group,
                      causal, wo_init, J0, nc, bsq, gap, gaps, dense_stride, counts, indices,
@@ -488,7 +489,7 @@ static void prefill_segments(int dtype, int64_t B, int64_t Hq, int64_t Sq, int64
   *qs_bytes = align256(B * Hq * nqb * D * esize(dtype));
   const int64_t nc_max = cdiv(chunk < Sq ? chunk : Sq, qps);
   *cnt_bytes = align256(B * Hq * nc_max * 4 * kMaxSegments);  // per-segment counts
-  if (carry_bytes) *carry_bytes = align256(B * Hq * nc_max * 8 * kMaxSegments);  // (max, exact)
+  if (carry_bytes) *carry_bytes = align256(B * Hq * nc_max * va::kSegCarryBytes * kMaxSegments);
   int64_t idx_max = 0;
   for (int64_t i = 0; i < Sq; i += chunk) {
     const int64_t rows = (Sq - i < chunk) ? (Sq - i) : chunk;
@@ -536,7 +537,7 @@ int va_prefill(int dtype, const void* q, int64_t sqb, int64_t sqh, int64_t sqs, 
   int32_t* counts = reinterpret_cast<int32_t*>(ws + qs_bytes);
   int32_t* indices = reinterpret_cast<int32_t*>(ws + qs_bytes + cnt_bytes);
   float* knorm = reinterpret_cast<float*>(ws + qs_bytes + cnt_bytes + idx_bytes);
-  float2* carry = reinterpret_cast<float2*>(ws + qs_bytes + cnt_bytes + idx_bytes + kn_bytes);
+  void* carry = ws + qs_bytes + cnt_bytes + idx_bytes + kn_bytes;
   hipStream_t st = static_cast<hipStream_t>(stream);
 
   int rc = va_pool(dtype, q, B, Hq, Sq, D, sqb, sqh, sqs, qps, nullptr, qs, stream);

@@ -48,6 +48,19 @@ constexpr int kWRows = 32;         // pooled rows per wave
 constexpr int kWWaves = 4;         // waves per work-group
 constexpr int kWChunk = 64;        // keys per chunk
 constexpr int kWList = 16;         // near-max tiles per row
+constexpr int kCarryTiles = 4;     // near-max tiles a segment passes on
+
+// What the maxima pass records per (row, segment) of a two-pass selection:
+// the segment's MFMA maximum, the exact maximum of the tiles it folded (on
+// list overflow), and its remaining near-max tiles (tile maximum within `win`
+// of the segment maximum; the only tiles that can hold the exact maximum),
+// whose exact scores are left to the carry pass's rare path.
+struct SegCarry {
+  float m, ex;
+  int32_t n, pad;
+  int32_t tile[kCarryTiles];
+};
+static_assert(sizeof(SegCarry) == 32, "the host sizes carry buffers at 32 bytes per record");
 
 
 // MFMA row m of the K operand -> key offset inside the 32-key block, such that
@@ -89,7 +102,7 @@ __global__ __launch_bounds__(256, 2) void select_wave_kernel(
     int64_t qps, uint32_t gspan, int causal, int64_t bsq, float gap_scalar,
     const float* __restrict__ gaps, const float* __restrict__ kmax, RowLayout lay,
     int32_t* __restrict__ counts, int32_t* __restrict__ indices, int64_t nrowsets, int segk,
-    int nseg, float2* __restrict__ carry, int mode) {
+    int nseg, SegCarry* __restrict__ carry, int mode) {
   using M = Mfma<T>;
   using vec = typename M::vec;
   constexpr int NS = D / 16;                    // MFMA steps over the features
@@ -103,6 +116,7 @@ __global__ __launch_bounds__(256, 2) void select_wave_kernel(
 
   __shared__ __attribute__((aligned(1024))) unsigned char kst[2 * STAGE];
   __shared__ int32_t nml[kWWaves][kWRows][kWList];        // near-max tiles per row
+  __shared__ float nmx[kWWaves][kWRows][kWList];          // their MFMA tile maxima
   __shared__ float exr[kWWaves][kWRows];                  // exact max of folded tiles
   __shared__ float tmx[kWWaves][kWList];                  // rare path: exact tile maxima
   __shared__ uint32_t ambm[kWWaves][kWRows][4];           // rare path: ambiguous keys
@@ -244,16 +258,16 @@ __global__ __launch_bounds__(256, 2) void select_wave_kernel(
   // The first visited chunk need not start a group: start with no folded tiles
   // (or, in the carry pass, with the maxima of the group's earlier segments).
   const int64_t crow = (bh * nc + jr) * nseg;  // this row's carry records
+  const int s_first = int((int64_t(seg_lo) / int64_t(gspan)) * int64_t(gspan) / segk);  // group's first segment
+  float cm_in = -__builtin_inff();  // carry pass: MFMA maximum of the earlier segments
   if (mode == kPassCarry) {
-    const int64_t g0 = (int64_t(seg_lo) / int64_t(gspan)) * int64_t(gspan);  // group start
-    float cm = -__builtin_inff(), ce = -__builtin_inff();
+    float ce = -__builtin_inff();
     if (valid)
-      for (int s2 = int(g0 / segk); s2 < seg; ++s2) {
-        const float2 cr = carry[crow + s2];
-        cm = __builtin_fmaxf(cm, cr.x);
-        ce = __builtin_fmaxf(ce, cr.y);
+      for (int s2 = s_first; s2 < seg; ++s2) {
+        cm_in = __builtin_fmaxf(cm_in, carry[crow + s2].m);
+        ce = __builtin_fmaxf(ce, carry[crow + s2].ex);
       }
-    m = cm;
+    m = cm_in;
     if (hh == 0) exr[wave][l32] = ce;
   } else if (hh == 0) {
     exr[wave][l32] = -__builtin_inff();
@@ -340,6 +354,37 @@ __global__ __launch_bounds__(256, 2) void select_wave_kernel(
     }
   };
 
+  // Carry pass: the near-max tiles of the earlier segments whose maximum is
+  // within `win` of the carried maximum (only those can hold the exact
+  // maximum) start the row's list; rows with more candidates than the list
+  // holds fold a full list exactly and continue.
+  if (mode == kPassCarry) {
+    int ps = s_first, pi = 0;  // next candidate: segment ps, tile pi
+    ambm[wave][l32][hh] = 0u;
+    ambm[wave][l32][2 + hh] = 0u;
+    while (true) {
+      if (hh == 0 && valid) {
+        while (listcnt < kWList - 4 && ps < seg) {
+          const SegCarry& cr = carry[crow + ps];
+          if (cr.m >= cm_in - win && pi < cr.n) {
+            nml[wave][l32][listcnt] = cr.tile[pi++];
+            nmx[wave][l32][listcnt] = cr.m;
+            ++listcnt;
+          } else {
+            ++ps;
+            pi = 0;
+          }
+        }
+      }
+      const uint64_t more = __builtin_amdgcn_ballot_w64(hh == 0 && valid && ps < seg);
+      if (more == 0) break;
+      uint32_t ovr[2] = {0u, 0u};
+      resolve(more, 0, ovr);
+    }
+    const uint32_t lc = other_half(uint32_t(listcnt));  // the high half mirrors the count
+    if (hh) listcnt = int(lc);
+  }
+
   // ---- chunk loop -------------------------------------------------------------
   // Software pipeline: in iteration c the MFMA scores of chunk c+1 are computed
   // (stage (c+1)&1) while the decisions of chunk c run on the VALU, and the
@@ -424,6 +469,7 @@ __global__ __launch_bounds__(256, 2) void select_wave_kernel(
       int rec[2];   // this lane lists the tile as near-max
       int nrec;     // tiles the row lists in this chunk
       int rpos[2];  // list positions of this lane's tiles
+      float rmax[2];  // MFMA maxima of this lane's listed tiles
       {
         const float t00 = hh ? om0 : tm0, t01 = hh ? tm0 : om0;
         const float t10 = hh ? om1 : tm1, t11 = hh ? tm1 : om1;
@@ -441,6 +487,8 @@ __global__ __launch_bounds__(256, 2) void select_wave_kernel(
           rpos[0] = listcnt + (hh ? f00 : 0);
           rpos[1] = listcnt + f00 + f01 + (hh ? f10 : 0);
           nrec = f00 + f01 + f10 + f11;
+          rmax[0] = tm0;
+          rmax[1] = tm1;
         } else if (BK == 32) {
           const float bm0 = __builtin_fmaxf(t00, t01), bm1 = __builtin_fmaxf(t10, t11);
           const float r0 = __builtin_fmaxf(m, bm0), r1 = __builtin_fmaxf(r0, bm1);
@@ -454,6 +502,8 @@ __global__ __launch_bounds__(256, 2) void select_wave_kernel(
           rpos[0] = listcnt;
           rpos[1] = listcnt + g0;
           nrec = g0 + g1;
+          rmax[0] = bm0;
+          rmax[1] = bm1;
         } else {
           const float cm = __builtin_fmaxf(__builtin_fmaxf(t00, t01), __builtin_fmaxf(t10, t11));
           const float r = __builtin_fmaxf(m, cm);
@@ -464,6 +514,7 @@ __global__ __launch_bounds__(256, 2) void select_wave_kernel(
           rec[1] = 0;
           rpos[0] = rpos[1] = listcnt;
           nrec = g;
+          rmax[0] = rmax[1] = cm;
         }
       }
       slots(NSL / 8, NSL / 4);
@@ -472,6 +523,7 @@ __global__ __launch_bounds__(256, 2) void select_wave_kernel(
         if (rec[bb]) {
           const int tk = BK == 16 ? kb0 + 32 * bb + 16 * hh : (BK == 32 ? kb0 + 32 * bb : kb0);
           nml[wave][l32][rpos[bb]] = tk / BK;
+          nmx[wave][l32][rpos[bb]] = rmax[bb];
         }
       listcnt += nrec;
       slots(NSL / 4, 3 * NSL / 8);
@@ -535,12 +587,28 @@ __global__ __launch_bounds__(256, 2) void select_wave_kernel(
   }
 
   if (mode == kPassMax) {
-    // Fold the tiles still listed, then record the segment's maxima.
+    // Keep the listed tiles within `win` of the segment maximum; rows with
+    // more than kCarryTiles of them fold them exactly now (rare).
+    int keep = 0;
+    if (hh == 0 && valid) {
+      for (int i = 0; i < listcnt; ++i)
+        if (nmx[wave][l32][i] >= m - win) nml[wave][l32][keep++] = nml[wave][l32][i];
+      listcnt = keep;
+    }
     ambm[wave][l32][hh] = 0u;
     ambm[wave][l32][2 + hh] = 0u;
     uint32_t ovr[2] = {0u, 0u};
-    resolve(__builtin_amdgcn_ballot_w64(hh == 0 && valid && listcnt > 0), 0, ovr);
-    if (valid && hh == 0) carry[crow + seg] = make_float2(m, exr[wave][l32]);
+    resolve(__builtin_amdgcn_ballot_w64(hh == 0 && valid && listcnt > kCarryTiles), 0, ovr);
+    if (valid && hh == 0) {
+      SegCarry cr;
+      cr.m = m;
+      cr.ex = exr[wave][l32];
+      cr.n = listcnt;
+      cr.pad = 0;
+#pragma unroll
+      for (int i = 0; i < kCarryTiles; ++i) cr.tile[i] = i < listcnt ? nml[wave][l32][i] : -1;
+      carry[crow + seg] = cr;
+    }
     return;
   }
 
@@ -584,7 +652,7 @@ static hipError_t launch_select_wave_tdb(const void* qs, int64_t sqb, int64_t sq
                                          int64_t qps, int64_t group, int causal, int64_t bsq,
                                          float gap, const float* gaps, const float* kmax,
                                          const RowLayout& lay, int32_t* counts, int32_t* indices,
-                                         int64_t segk, float2* carry, int mode,
+                                         int64_t segk, SegCarry* carry, int mode,
                                          hipStream_t stream) {
   const int64_t nrowsets = (lay.nc + kWWaves * kWRows - 1) / (kWWaves * kWRows);
   const int64_t nseg = segk > 0 ? (Sk + segk - 1) / segk : 1;
@@ -607,7 +675,7 @@ static hipError_t launch_select_wave_td(int64_t bk, const void* qs, int64_t sqb,
                                         int64_t qps, int64_t group, int causal, int64_t bsq,
                                         float gap, const float* gaps, const float* kmax,
                                         const RowLayout& lay, int32_t* counts, int32_t* indices,
-                                        int64_t segk, float2* carry, int mode,
+                                        int64_t segk, SegCarry* carry, int mode,
                                         hipStream_t stream) {
 #define VA_SELW_BK(BB)                                                                          \
   if (bk == BB)                                                                                 \
@@ -626,12 +694,12 @@ hipError_t launch_select_wave(int dtype, const void* qs, int64_t sqb, int64_t sq
                               int64_t Hq, int64_t Hk, int64_t Sk, int64_t D, int64_t qps,
                               int64_t bk, int64_t group, int causal, int64_t bsq, float gap,
                               const float* gaps, const float* kmax, const RowLayout& lay,
-                              int32_t* counts, int32_t* indices, int64_t segk, float2* carry,
+                              int32_t* counts, int32_t* indices, int64_t segk, void* carry,
                               int mode, hipStream_t stream) {
 #define VA_SELW_CASE(TT, DD)                                                                 \
   return launch_select_wave_td<TT, DD>(bk, qs, sqb, sqh, sqn, k, skb, skh, sks, B, Hq, Hk, \
                                        Sk, qps, group, causal, bsq, gap, gaps, kmax, lay,    \
-                                       counts, indices, segk, carry, mode, stream);
+                                       counts, indices, segk, static_cast<SegCarry*>(carry), mode, stream);
   if (dtype == kBF16 && D == 128) { VA_SELW_CASE(bf16_t, 128) }
   if (dtype == kBF16 && D == 64) { VA_SELW_CASE(bf16_t, 64) }
   if (dtype == kF16 && D == 128) { VA_SELW_CASE(f16_t, 128) }

@@ -103,16 +103,19 @@ def select_rows(qs_chunk, k, J0, gap, gaps, causal, q_pooling_size, k_local_size
 
 
 def segment_keys(Sk, k_local_size, group_k_block):
-    """Segment length of the split selection (0: the groups are too long to split)."""
+    """Segment length of the split selection va_prefill uses (0: not split)."""
     return int(nat.lib().va_select_segment_keys(Sk, k_local_size, group_k_block))
 
 
 def select_segments(qs_chunk, k, J0, gap, gaps, causal, q_pooling_size, k_local_size,
-                    group_k_block, wo_init, segk, bsq=None, dense_stride=0):
+                    group_k_block, wo_init, segk, bsq=None, dense_stride=0, indices=None,
+                    scratch=None):
     """Split TilingSelect (the form VecAttention_prefill runs): keys cut into
-    segments of `segk` keys selected independently.  Returns (counts
+    segments of `segk` keys selected in parallel.  Returns (counts
     (B, Hq, nc, nseg) int32, indices int32): segment s of a row writes from slot
-    max(s*segk, smin) - smin of the row in the index layout.
+    max(s*segk, smin) - smin of the row in the index layout.  `indices` and
+    `scratch` may be passed in (int32 / fp32 device buffers at least as large as
+    the index layout and va_select_segments_scratch_floats) to reuse them.
     """
     if qs_chunk.stride(-1) != 1:
         qs_chunk = qs_chunk.contiguous()
@@ -125,12 +128,20 @@ def select_segments(qs_chunk, k, J0, gap, gaps, causal, q_pooling_size, k_local_
     nseg = -(-Sk // segk)
     cap = index_capacity(B, Hq, Sk, q_pooling_size, causal, wo_init, J0, nc, dense_stride)
     counts = torch.empty(B, Hq, nc, nseg, dtype=torch.int32, device=k.device)
-    indices = torch.empty(max(cap, 1), dtype=torch.int32, device=k.device)
+    if indices is None:
+        indices = torch.empty(max(cap, 1), dtype=torch.int32, device=k.device)
+    elif indices.dtype != torch.int32 or indices.numel() < cap:
+        raise AssertionError(f"indices: need {cap} int32 slots")
     nscr = int(nat.lib().va_select_segments_scratch_floats(B, Hq, Hk, Sk, nc, segk, k_local_size,
                                                             group_k_block))
     if nscr < 0:
         raise AssertionError("va_select_segments_scratch_floats: invalid sizes")
-    scratch = torch.empty(max(nscr, 1), dtype=torch.float32, device=k.device)
+    if scratch is None:
+        scratch = torch.empty(max(nscr, 1), dtype=torch.float32, device=k.device)
+    elif scratch.dtype != torch.float32 or scratch.numel() < nscr:
+        raise AssertionError(f"scratch: need {nscr} fp32 slots")
+    else:
+        nscr = scratch.numel()
     with torch.cuda.device(k.device):
         rc = nat.lib().va_select_segments(
             nat.dtype_code(k), nat.ptr(qs_chunk), qs_chunk.stride(0), qs_chunk.stride(1),
