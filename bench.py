@@ -103,6 +103,21 @@ def selectable(wl, S):
     return wl.B * wl.Hq * tot
 
 
+# ------------------------------------------------------------------ traffic --
+
+def profiled_traffic(workload, kernel):
+    """HBM bytes per launch of `kernel` on `workload` (FETCH_SIZE + WRITE_SIZE,
+    each scaled by the copy-kernel calibration) from the rocprofv3 --pmc runs
+    summarised in profiles/hbm_traffic.json; None when not profiled."""
+    path = os.path.join(ROOT, "profiles", "hbm_traffic.json")
+    try:
+        with open(path) as f:
+            rec = json.load(f)["workloads"][workload][kernel]
+    except (OSError, KeyError, ValueError):
+        return None
+    return int(round(rec["fetch_bytes"] + rec["write_bytes"]))
+
+
 # ------------------------------------------------------------------- stages --
 
 def run_stages(wl, q, k, v, gap, out, events=None):
@@ -359,7 +374,7 @@ def main():
         "roofline": {"bound": "mfma", "kernel": "attn_mfma_kernel",
                      "achieved": round(attn_tflops, 3), "peak": BF16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(attn_tflops / BF16_PEAK_TFLOPS, 4),
-                     "traffic": None},
+                     "traffic": profiled_traffic(wl.name, "attn_mfma_kernel")},
         "flops": {"attn_executed": F_attn, "dense": F_dense},
     }
     if not args.no_cpu:
