@@ -371,9 +371,12 @@ static AttnMfmaCheck attn_mfma_check(int dtype, const void* q, const int64_t* sq
     return reinterpret_cast<uintptr_t>(p) % 16 == 0 && s[0] % a == 0 && s[1] % a == 0 &&
            s[2] % a == 0;
   };
+  // The kernel reads a zero row at byte offset Sk * row stride (past the
+  // buffer's range, which needs rows that do not overlap, or one broadcast
+  // row) and computes offsets in 32 bits with 24-bit multiplies.
   auto span_ok = [&](const int64_t* s) {
-    return Sk < (int64_t(1) << 24) && s[2] >= 0 && s[2] * es < (int64_t(1) << 24) &&
-           ((Sk - 1) * s[2] + D) * es < (int64_t(1) << 31);
+    return Sk < (int64_t(1) << 24) && (s[2] == 0 || s[2] >= D) &&
+           s[2] * es < (int64_t(1) << 24) && (Sk * s[2] + D) * es < (int64_t(1) << 31);
   };
   AttnMfmaCheck c;
   c.shape = va::attn_mfma_supported(dtype, D, qps);
@@ -399,11 +402,13 @@ static int attn_dispatch(int dtype, const void* q, const int64_t* sq, const void
       return fail(VA_ERR_UNSUPPORTED, "MFMA attention needs bf16/fp16, D in {64,128}, qps in {64,128}");
     if (!mfma_align) return fail(VA_ERR_UNSUPPORTED, "MFMA attention needs 16-byte aligned rows");
     if (!mfma_span)
-      return fail(VA_ERR_UNSUPPORTED, "MFMA attention needs Sk < 2^24, row strides < 16 MiB and "
-                                      "< 2 GiB of rows per kv head");
+      return fail(VA_ERR_UNSUPPORTED, "MFMA attention needs Sk < 2^24, row strides < 16 MiB "
+                                      "that are 0 or at least D, and < 2 GiB of rows per kv head");
+    if (!(softmax_scale > 0.f))
+      return fail(VA_ERR_UNSUPPORTED, "MFMA attention needs a positive softmax scale");
     use_mfma = true;
   } else if (kernel == VA_ATTN_AUTO) {
-    use_mfma = mfma_shape && mfma_align && mfma_span;
+    use_mfma = mfma_shape && mfma_align && mfma_span && softmax_scale > 0.f;
   } else if (kernel != VA_ATTN_SIMPLE) {
     return fail(VA_ERR_ARG, "unknown kernel selector %d", kernel);
   }

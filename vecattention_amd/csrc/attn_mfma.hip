@@ -276,20 +276,29 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
 
   // Copy offsets of tile u: for each of this lane's H copies, the byte offset
   // of its 16-byte chunk in K (kof) and V (vof), from the key ids in ids slot
-  // idslot.  Rows past the tile's key count, keys outside [0, Sk) and every
-  // row of a tile past the end of the list get an out-of-range offset (their
-  // copies write zeros into a slot that is masked or never read).
+  // idslot.  Keys outside [0, Sk), rows past the tile's key count and every
+  // row of a tile past the end of the list are read as key Sk, whose offset
+  // Sk * row stride is past the buffer's range (the host checks that it does
+  // not wrap): their copies write zeros into a slot that is masked or never
+  // read.  Only partial tiles (a uniform branch) test the row count.
+  const uint32_t usk = uint32_t(Sk) & 0xffffffu;  // Sk < 2^24 (host check): 24-bit multiplies
   auto copy_offsets = [&](int u, int idslot, uint32_t (&kof)[H], uint32_t (&vof)[H]) {
     const int lim = tile_info(u).lim;
-    int32_t key[H];
-#pragma unroll
-    for (int x = 0; x < H; ++x) key[x] = ids[idslot * kTileKeys + id_pos + x];
+    uint32_t key[H];
 #pragma unroll
     for (int x = 0; x < H; ++x) {
-      // row (wave*H + x)*RPC + qr of the tile holds a key when it is below lim
-      const bool ok = (qr < lim - (wave * H + x) * RPC) & (uint32_t(key[x]) < uint32_t(Sk));
-      kof[x] = ok ? __umul24(uint32_t(key[x]), krb) + cchunk[x] : kOutOfRange;
-      vof[x] = ok ? __umul24(uint32_t(key[x]), vrb) + cchunk[x] : kOutOfRange;
+      const uint32_t id = uint32_t(ids[idslot * kTileKeys + id_pos + x]);
+      key[x] = id < usk ? id : usk;
+    }
+    if (lim < kTileKeys) {
+#pragma unroll
+      for (int x = 0; x < H; ++x)  // row (wave*H + x)*RPC + qr holds a key below lim
+        if (qr >= lim - (wave * H + x) * RPC) key[x] = usk;
+    }
+#pragma unroll
+    for (int x = 0; x < H; ++x) {
+      kof[x] = __umul24(key[x], krb) + cchunk[x];
+      vof[x] = __umul24(key[x], vrb) + cchunk[x];
     }
   };
   // Copy x of this wave into the K or V tile at LDS address base.
@@ -334,21 +343,16 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
   for (int i = 0; i < D / 32; ++i)
 #pragma unroll
     for (int e = 0; e < 16; ++e) o[i][e] = 0.f;
-  float mc = -__builtin_inff();  // running maximum, scaled (log2) units
-  // Row sums of the probabilities, accumulated on the matrix cores: an MFMA
-  // with an all-ones A operand and the PV step's B operand (P^T) adds, to
-  // every entry of lane l's accumulator, the sum over the step's 16 keys of
-  // row l % 32.  Entry 0 is the one kept (the rescale touches only it).  The
-  // sum is over the bf16/fp16-rounded probabilities that also weight V.
-  f32x16_t lacc;
-#pragma unroll
-  for (int e = 0; e < 16; ++e) lacc[e] = 0.f;
-  const vec ones = [] {
-    float one[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) one[e] = 1.f;
-    return M::pack(one);
-  }();
+  // Online-softmax state of this lane's row: running maximum mc (scaled, log2
+  // units), -mc as the exponent offset (0 while no key has been seen), and
+  // the raw-score level above which a tile moves the maximum.
+  float mc = -__builtin_inff(), mneg = 0.f, thr = -__builtin_inff();
+  const float inv_scale = 1.f / scale_log2;  // the host passes scale_log2 > 0
+  // Partial row sum of the probabilities of this lane's keys (lanes l and
+  // l ^ 32 hold the two halves of row l % 32): dot products of the packed
+  // bf16/fp16 probabilities with (1, 1), i.e. the rounded values that also
+  // weight V.
+  float lsum = 0.f;
 
   // S^T of one tile: 8 (D/16) MFMAs with K rows from the K slot at kbuf.
   auto qk = [&](const unsigned char* kbuf) {
@@ -364,7 +368,7 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
   };
   // Mask tile u's scores (empty slots, causal diagonal; every slot of a tile
   // past the end of the list) and return the tile maximum of this lane's row
-  // in scaled (log2) units.  Slot of s[e]: 32kc + 8(e/4) + 4hh + e%4.
+  // (raw scores).  Slot of s[e]: 32kc + 8(e/4) + 4hh + e%4.
   auto mask_max = [&](int u, f32x16_t& s) {
     const TileInfo ti = tile_info(u);
     if (ti.diag || ti.lim < kTileKeys) {  // rare: partial, diagonal or empty tiles
@@ -378,20 +382,25 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
     float tmax = -__builtin_inff();
 #pragma unroll
     for (int e = 0; e < 16; ++e) tmax = __builtin_fmaxf(tmax, s[e]);
-    return max_halves(tmax) * scale_log2;
+    return max_halves(tmax);
   };
   // Move the running maximum when some row's tile maximum exceeds it by more
-  // than the slack (rare): rescale O and the row sums.
-  auto rescale = [&](float tsc) {
-    if (__builtin_amdgcn_ballot_w64(tsc > mc + kRescaleSlack)) {
-      const float mnew = __builtin_fmaxf(mc, tsc);
+  // than the slack (rare): rescale O and the row sums.  The test compares raw
+  // scores with thr = (mc + slack) / scale; its rounding only moves the
+  // bound on the kept probabilities by a few ulps of 2^8.
+  auto rescale = [&](float tmax) {
+    if (__builtin_amdgcn_ballot_w64(tmax > thr)) {
+      const float mnew = __builtin_fmaxf(mc, tmax * scale_log2);
       const float alpha = (mnew == mc) ? 1.f : __builtin_amdgcn_exp2f(mc - mnew);
 #pragma unroll
       for (int i = 0; i < D / 32; ++i)
 #pragma unroll
         for (int e = 0; e < 16; ++e) o[i][e] *= alpha;
-      lacc[0] *= alpha;
+      lsum *= alpha;
       mc = mnew;
+      const bool none = mnew == -__builtin_inff();
+      mneg = none ? 0.f : -mnew;
+      thr = none ? -__builtin_inff() : (mnew + kRescaleSlack) * inv_scale;
     }
   };
   // O^T += V^T P^T, 16 keys per step: k-slot 8hh + e of step sub is key
@@ -410,7 +419,7 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
         const s16x4_t both[2] = {lo, hi};
         o[i] = M::run(__builtin_bit_cast(vec, both), bfrag[sub], o[i]);
       }
-      lacc = M::run(ones, bfrag[sub], lacc);
+      lsum = M::sum8(bfrag[sub], lsum);
     }
   };
 
@@ -460,7 +469,6 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
     vm_lds_barrier();  // V(t), K(t+1), ids(t+2) landed; K slot P, V slot P^1 free
     if (wave == 0 && t + 3 < ntiles) stage_ids(t + 3, P ^ 1);
     const unsigned char* kb = smem + k_next;
-    const float mneg = (mc == -__builtin_inff()) ? 0.f : -mc;
 #pragma unroll
     for (int e = 0; e < 16; ++e) s_next[e] = 0.f;
     float pr[16];
@@ -518,8 +526,11 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
       for (int g = 0; g < 4; ++g)
         *reinterpret_cast<float4*>(mo + ((4 * i + g) * 64 + lane) * 4) =
             make_float4(o[i][4 * g], o[i][4 * g + 1], o[i][4 * g + 2], o[i][4 * g + 3]);
+  }
+  const float lrow = sum_halves(lsum);  // row sum of this wave's key half, both halves
+  if (kc == 1) {
     mo[64 * (D / 2) + lane] = mc;
-    mo[64 * (D / 2) + 64 + lane] = lacc[0];
+    mo[64 * (D / 2) + 64 + lane] = lrow;
   }
   lds_barrier();
   if (kc == 0) {
@@ -527,7 +538,7 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
     const float m = __builtin_fmaxf(mc, m1);
     const float a0 = (mc == m) ? 1.f : __builtin_amdgcn_exp2f(mc - m);
     const float a1 = (m1 == m) ? 1.f : __builtin_amdgcn_exp2f(m1 - m);
-    const float l = lacc[0] * a0 + l1 * a1;  // both halves of the wave hold the full sums
+    const float l = lrow * a0 + l1 * a1;
     const float inv = l > 0.f ? 1.f / l : 0.f;
     const float c0 = a0 * inv, c1 = a1 * inv;
     if (qpos < Sq) {

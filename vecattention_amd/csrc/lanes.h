@@ -44,12 +44,15 @@ __device__ inline void copy4_to_lds(__amdgpu_buffer_rsrc_t r, uint32_t lds, uint
                : "memory");
 }
 
-// Max of x over lanes l and l ^ 32.
+// Max of x over lanes l and l ^ 32.  x must not be a signaling NaN (it is an
+// arithmetic result or an infinity here), so the plain v_max_f32 is used
+// without the quieting that fmaxf adds in front of it.
 __device__ inline float max_halves(float x) {
   const uint32_t u = __builtin_bit_cast(uint32_t, x);
   const auto p = __builtin_amdgcn_permlane32_swap(u, u, false, false);
-  return __builtin_fmaxf(__builtin_bit_cast(float, (uint32_t)p[0]),
-                         __builtin_bit_cast(float, (uint32_t)p[1]));
+  float r;
+  asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"((uint32_t)p[0]), "v"((uint32_t)p[1]));
+  return r;
 }
 __device__ inline float sum_halves(float x) {
   const uint32_t u = __builtin_bit_cast(uint32_t, x);

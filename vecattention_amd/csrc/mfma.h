@@ -20,6 +20,15 @@ template <> struct Mfma<bf16_t> {
     for (int e = 0; e < 8; ++e) r[e] = __bf16(x[e]);
     return r;
   }
+  // acc + the sum of the 8 elements of x (v_dot2c_f32_bf16 against (1, 1)).
+  __device__ static float sum8(vec x, float acc) {
+    typedef __bf16 pair __attribute__((ext_vector_type(2)));
+    const pair one = {__bf16(1.f), __bf16(1.f)};
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      acc = __builtin_amdgcn_fdot2_f32_bf16(pair{x[2 * i], x[2 * i + 1]}, one, acc, false);
+    return acc;
+  }
 };
 template <> struct Mfma<f16_t> {
   typedef f16x8_t vec;
@@ -31,6 +40,15 @@ template <> struct Mfma<f16_t> {
 #pragma unroll
     for (int e = 0; e < 8; ++e) r[e] = _Float16(x[e]);
     return r;
+  }
+  // acc + the sum of the 8 elements of x (v_dot2c_f32_f16 against (1, 1)).
+  __device__ static float sum8(vec x, float acc) {
+    typedef _Float16 pair __attribute__((ext_vector_type(2)));
+    const pair one = {_Float16(1.f), _Float16(1.f)};
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      acc = __builtin_amdgcn_fdot2(pair{x[2 * i], x[2 * i + 1]}, one, acc, false);
+    return acc;
   }
 };
 
