@@ -15,9 +15,10 @@
 // swizzle of their 16-byte chunks (chunk c of row R sits at c ^ swizzle(R))
 // so that the MFMA operand reads below are free of bank conflicts.  Two LDS
 // stages: the copies of tile t+1 are in flight while tile t is computed, and a
-// single barrier per tile separates them.  The key ids of tile t+2 are staged
-// in LDS one tile earlier (copied from the index list, or generated for the
-// local blocks).
+// single barrier per tile separates them.  Key ids are staged in LDS ahead of
+// their copies (copied from the index list, or generated for the local
+// blocks), all waves together once every kWaves tiles, one tile per wave, so
+// that no wave carries the staging work alone into every barrier.
 //
 // Compute.  Waves form a (row half, key half) grid: wave (rh, kc) owns query
 // rows [32rh, 32rh+32) and keys [32kc, 32kc+32) of every tile, with its own
@@ -62,7 +63,10 @@ struct AttnShape {
   static constexpr int kCopiesPerWave = kTileBytes / 1024 / kWaves;  // per operand
   static constexpr int kMergeBytes = kRowHalves * 64 * (D / 2 + 2) * 4;
   static constexpr int kDataBytes = 2 * kStageBytes > kMergeBytes ? 2 * kStageBytes : kMergeBytes;
-  static constexpr int kLdsBytes = kDataBytes + 2 * kTileKeys * 4;
+  // Key ids: a ring of 2 * kWaves tile slots; every kWaves tiles each wave
+  // stages the ids of one tile kWaves to 2 * kWaves - 1 tiles ahead.
+  static constexpr int kIdSlots = 2 * kWaves;
+  static constexpr int kLdsBytes = kDataBytes + kIdSlots * kTileKeys * 4;
   static_assert(kCopiesPerWave >= 1 && kRowsPerCopy * kCopiesPerWave * kWaves == kTileKeys,
                 "tile copies must split evenly over the waves");
 };
@@ -117,7 +121,7 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
   constexpr int H = S::kCopiesPerWave;
 
   __shared__ __attribute__((aligned(1024))) unsigned char smem[S::kLdsBytes];
-  int32_t* const ids = reinterpret_cast<int32_t*>(smem + S::kDataBytes);  // [2][64]
+  int32_t* const ids = reinterpret_cast<int32_t*>(smem + S::kDataBytes);  // [kIdSlots][64]
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid / 64), lane = tid % 64;
@@ -147,11 +151,10 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
 
   // Selected columns.  With nseg > 1 the row's list comes in key segments:
   // segment s holds counts[.., s] keys from slot max(s*segk, smin) - smin of
-  // the row (see select_wave.hip).  Lane s of wave 0 keeps sv = the exclusive
-  // prefix of the segment counts (the column where segment s starts), so
-  // column p of the concatenated list is slot seg_slot(s) + p - sv[s] for the
-  // last s with sv[s] <= p.
-  __shared__ int32_t segtot;
+  // the row (see select_wave.hip).  Lane s of every wave keeps sv = the
+  // exclusive prefix of the segment counts (the column where segment s
+  // starts), so column p of the concatenated list is slot seg_slot(s) + p -
+  // sv[s] for the last s with sv[s] <= p.
   int sv = 0x7fffffff;
   const int64_t cap = lay.capacity(J);
   const int smin = int(lay.smin());
@@ -159,25 +162,21 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
   int64_t cnt = 0;
   if (counts && nseg <= 1) {
     cnt = counts[bh * lay.nc + jr];
-  } else if (counts) {
-    if (wave == 0) {  // whole wave: the scan exchanges lanes
-      int c = 0;
-      if (lane < nseg) {
-        c = counts[(bh * lay.nc + jr) * nseg + lane];
-        const int room = int(cap) - seg_slot(lane);
-        c = c < 0 ? 0 : (c > room ? (room > 0 ? room : 0) : c);
-      }
-      int incl = c;
-#pragma unroll
-      for (int o = 1; o < 64; o <<= 1) {
-        const int y = __shfl_up(incl, o);
-        if (lane >= o) incl += y;
-      }
-      if (lane < nseg) sv = incl - c;
-      if (lane == nseg - 1) segtot = incl;
+  } else if (counts) {  // whole wave: the scan exchanges lanes
+    int c = 0;
+    if (lane < nseg) {
+      c = counts[(bh * lay.nc + jr) * nseg + lane];
+      const int room = int(cap) - seg_slot(lane);
+      c = c < 0 ? 0 : (c > room ? (room > 0 ? room : 0) : c);
     }
-    lds_barrier();
-    cnt = segtot;
+    int incl = c;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int y = __shfl_up(incl, o);
+      if (lane >= o) incl += y;
+    }
+    if (lane < nseg) sv = incl - c;
+    cnt = __builtin_amdgcn_readlane(incl, nseg - 1);
   }
   if (cnt > cap) cnt = cap;
   const int32_t* cols = indices ? indices + lay.row_offset(bh, jr) : nullptr;
@@ -234,15 +233,15 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
     return (w * H + x) * RPC + r;
   }();
 
-  // Stage the key ids of tile u into ids[slot] (wave 0 only; tiles are staged
-  // in increasing order).  Column positions of the selected list map to index
-  // slots through a scalar segment cursor: segment sc holds positions
+  // Stage the key ids of tile u into ids[slot] (one wave; each wave stages
+  // its tiles in increasing order).  Column positions of the selected list
+  // map to index slots through a scalar segment cursor: segment sc holds positions
   // [sv[sc], sc_next) at slots position + sc_base.  Positions only grow from
   // tile to tile, so the cursor moves forward once per segment (empty
   // segments are stepped over), and a tile with no segment boundary inside
   // it costs one add per lane.
   const int kNoBoundary = 0x7fffffff;
-  auto boundary = [&](int sg) {  // start of segment sg (wave 0), or none
+  auto boundary = [&](int sg) {  // start of segment sg, or none
     return sg < nseg ? __builtin_amdgcn_readlane(sv, sg) : kNoBoundary;
   };
   int sc = 0, sc_base = 0, sc_next = nseg > 1 ? boundary(1) : kNoBoundary;
@@ -403,44 +402,46 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
       thr = none ? -__builtin_inff() : (mnew + kRescaleSlack) * inv_scale;
     }
   };
-  // O^T += V^T P^T, 16 keys per step: k-slot 8hh + e of step sub is key
-  // 32kc + 16sub + 8(e/4) + 4hh + e%4, i.e. accumulator entries 8sub .. 8sub+7.
-  auto pv_step = [&](const unsigned char* vbuf, const vec (&bfrag)[2]) {
-#pragma unroll
-    for (int sub = 0; sub < 2; ++sub) {
-#pragma unroll
-      for (int i = 0; i < D / 32; ++i) {
-        const unsigned char* p0 = vbuf + voff[i][0] + sub * 16 * S::kRowBytes;
-        const unsigned char* p1 = vbuf + voff[i][1] + sub * 16 * S::kRowBytes;
-        const s16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (__attribute__((address_space(3))) s16x4_t*)(p0));
-        const s16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (__attribute__((address_space(3))) s16x4_t*)(p1));
-        const s16x4_t both[2] = {lo, hi};
-        o[i] = M::run(__builtin_bit_cast(vec, both), bfrag[sub], o[i]);
-      }
-      lsum = M::sum8(bfrag[sub], lsum);
-    }
+  // O^T += V^T P^T in NPV MFMAs, 16 keys each: MFMA f = sub * (D/32) + i
+  // adds keys 32kc + 16sub + .. into output block i; k-slot 8hh + e of step
+  // sub is key 32kc + 16sub + 8(e/4) + 4hh + e%4, i.e. accumulator entries
+  // 8sub .. 8sub+7.  read_v fetches MFMA f's V^T operand from the V tile at
+  // vbuf (issued ahead of its use), pv_mfma runs it.
+  constexpr int NPV = D / 16;
+  auto read_v = [&](const unsigned char* vbuf, int f) {
+    const int sub = f / (D / 32), i = f % (D / 32);
+    const unsigned char* p0 = vbuf + voff[i][0] + sub * 16 * S::kRowBytes;
+    const unsigned char* p1 = vbuf + voff[i][1] + sub * 16 * S::kRowBytes;
+    const s16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) s16x4_t*)(p0));
+    const s16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) s16x4_t*)(p1));
+    const s16x4_t both[2] = {lo, hi};
+    return __builtin_bit_cast(vec, both);
+  };
+  auto pv_mfma = [&](int f, const vec& vf, const vec (&bfrag)[2]) {
+    const int sub = f / (D / 32), i = f % (D / 32);
+    o[i] = M::run(vf, bfrag[sub], o[i]);
   };
 
   // ---- pipeline ------------------------------------------------------------
   // LDS slots: K(u) in K slot u&1, V(u) in V slot u&1 (slot p of K at
   // p * kStageBytes, of V kTileBytes after it), key ids of tile u in ids slot
-  // u&1.  Iteration t computes S(t+1) = QK(t+1) next to the softmax of S(t),
-  // then PV(t) next to the masking and maximum of S(t+1).  Resident during
-  // iteration t: K(t+1), V(t); in flight: K(t+2), V(t+1), ids(t+3); one
-  // barrier per iteration.  The copies of an iteration are spread over its QK
+  // u % kIdSlots.  Iteration t computes S(t+1) = QK(t+1) next to the softmax
+  // of S(t), then PV(t) next to the masking and maximum of S(t+1).  Resident
+  // during iteration t: K(t+1), V(t); in flight: K(t+2), V(t+1); one barrier
+  // per iteration.  Iterations t = 0 mod W stage the ids of tiles t+W ..
+  // t+2W-1, first read (for the copies of tile t+W) at iteration t+W-2 > t,
+  // and written over 2W tiles later, after their last read.  The copies of an iteration are spread over its QK
   // MFMAs (one DMA instruction after an MFMA), so that a copy that waits for
   // room in the memory pipeline overlaps the matrix work already issued
   // instead of stalling every wave right after the barrier.
   constexpr int NQK = D / 16;  // QK MFMAs per tile
   uint32_t vof_cur[H];         // V offsets of tile t+1 (its K copies went out earlier)
   f32x16_t s_cur;              // masked scores of tile t
+  constexpr int W = S::kWaves;
   if (ntiles > 0) {
-    if (wave == 0) {
-      stage_ids(0, 0);
-      if (ntiles > 1) stage_ids(1, 1);
-    }
+    if (wave < ntiles) stage_ids(wave, wave);  // tiles 0 .. W-1
     vm_lds_barrier();
     uint32_t kof[H], vof[H];
     copy_offsets(0, 0, kof, vof);
@@ -452,8 +453,7 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
     copy_offsets(1, 1, kof, vof_cur);
 #pragma unroll
     for (int x = 0; x < H; ++x) copy_k(smem_lds + uint32_t(S::kStageBytes), x, kof[x]);
-    vm_lds_barrier();  // K(0), V(0), K(1) landed; ids slots 0 and 1 read by every wave
-    if (wave == 0 && ntiles > 2) stage_ids(2, 0);
+    vm_lds_barrier();  // K(0), V(0), K(1) landed
     s_cur = qk(smem);
     rescale(mask_max(0, s_cur));
   }
@@ -466,16 +466,22 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
     constexpr uint32_t k_next = uint32_t((P ^ 1) * S::kStageBytes);    // K slot P^1
     constexpr uint32_t v_this = k_this + uint32_t(S::kTileBytes);      // V slot P
     constexpr uint32_t v_next = k_next + uint32_t(S::kTileBytes);      // V slot P^1
-    vm_lds_barrier();  // V(t), K(t+1), ids(t+2) landed; K slot P, V slot P^1 free
-    if (wave == 0 && t + 3 < ntiles) stage_ids(t + 3, P ^ 1);
+    vm_lds_barrier();  // V(t), K(t+1) landed; K slot P, V slot P^1 free
+    if (P == 0 && t % W == 0) {  // every wave stages one of tiles t+W .. t+2W-1
+      const int u = t + W + wave;
+      if (u < ntiles) stage_ids(u, u % S::kIdSlots);
+    }
     const unsigned char* kb = smem + k_next;
 #pragma unroll
     for (int e = 0; e < 16; ++e) s_next[e] = 0.f;
     float pr[16];
     uint32_t kof[H], vof_new[H];
-    // K operands are read kAhead MFMAs ahead of their use (LDS latency)
-    constexpr int kAhead = 3;
-    vec a[NQK];
+    // K operands are read kAhead MFMAs ahead of their use (LDS latency); the
+    // V^T operands of PV(t) kVAhead MFMAs ahead, the first ones during the
+    // last QK steps.
+    constexpr int kAhead = 3, kVAhead = 3;
+    const unsigned char* vb = smem + v_this;
+    vec a[NQK], vf[NPV];
 #pragma unroll
     for (int st = 0; st < kAhead; ++st)
       a[st] = __builtin_bit_cast(vec, *reinterpret_cast<const uint4*>(kb + koff[st]));
@@ -486,7 +492,7 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
         a[st + kAhead] =
             __builtin_bit_cast(vec, *reinterpret_cast<const uint4*>(kb + koff[st + kAhead]));
       s_next = M::run(a[st], qreg[st], s_next);  // past the last tile: masked away below
-      if (st == 0) copy_offsets(t + 2, P, kof, vof_new);
+      if (st == 0) copy_offsets(t + 2, (t + 2) % S::kIdSlots, kof, vof_new);
       // copy c of the 2H of this iteration goes out after MFMA c*NQK/(2H):
       // first V(t+1) into V slot P^1, then K(t+2) into K slot P
 #pragma unroll
@@ -497,6 +503,7 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
         else
           copy_k(smem_lds + k_this, c - H, kof[c - H]);
       }
+      if (st >= NQK - kVAhead) vf[st - (NQK - kVAhead)] = read_v(vb, st - (NQK - kVAhead));
       // this step's share of the softmax of S(t)
 #pragma unroll
       for (int e = st * 16 / NQK; e < (st + 1) * 16 / NQK; ++e)
@@ -504,8 +511,14 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
     }
     __builtin_amdgcn_sched_barrier(0);
     const vec bfrag[2] = {M::pack(pr), M::pack(pr + 8)};
-    pv_step(smem + v_this, bfrag);
+#pragma unroll
+    for (int f = 0; f < NPV; ++f) {
+      __builtin_amdgcn_sched_barrier(0);
+      if (f + kVAhead < NPV) vf[f + kVAhead] = read_v(vb, f + kVAhead);
+      pv_mfma(f, vf[f], bfrag);
+    }
     __builtin_amdgcn_sched_barrier(0);
+    lsum = M::sum8(bfrag[1], M::sum8(bfrag[0], lsum));
 #pragma unroll
     for (int x = 0; x < H; ++x) vof_cur[x] = vof_new[x];
     rescale(mask_max(t + 1, s_next));
