@@ -365,10 +365,9 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
     }
     return s;
   };
-  // Mask tile u's scores (empty slots, causal diagonal; every slot of a tile
-  // past the end of the list) and return the tile maximum of this lane's row
-  // (raw scores).  Slot of s[e]: 32kc + 8(e/4) + 4hh + e%4.
-  auto mask_max = [&](int u, f32x16_t& s) {
+  // Mask tile u's scores: empty slots, the causal diagonal, every slot of a
+  // tile past the end of the list.  Slot of s[e]: 32kc + 8(e/4) + 4hh + e%4.
+  auto mask = [&](int u, f32x16_t& s) {
     const TileInfo ti = tile_info(u);
     if (ti.diag || ti.lim < kTileKeys) {  // rare: partial, diagonal or empty tiles
 #pragma unroll
@@ -378,10 +377,6 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
         s[e] = ok ? s[e] : -__builtin_inff();
       }
     }
-    float tmax = -__builtin_inff();
-#pragma unroll
-    for (int e = 0; e < 16; ++e) tmax = __builtin_fmaxf(tmax, s[e]);
-    return max_halves(tmax);
   };
   // Move the running maximum when some row's tile maximum exceeds it by more
   // than the slack (rare): rescale O and the row sums.  The test compares raw
@@ -455,7 +450,11 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
     for (int x = 0; x < H; ++x) copy_k(smem_lds + uint32_t(S::kStageBytes), x, kof[x]);
     vm_lds_barrier();  // K(0), V(0), K(1) landed
     s_cur = qk(smem);
-    rescale(mask_max(0, s_cur));
+    mask(0, s_cur);
+    float tmax = -__builtin_inff();
+#pragma unroll
+    for (int e = 0; e < 16; e += 2) tmax = max3_plain(tmax, s_cur[e], s_cur[e + 1]);
+    rescale(max_halves(tmax));
   }
   // One iteration; the parity P = t & 1 is a compile-time constant so that
   // the LDS slot addresses fold into the instructions' offsets and S(t),
@@ -506,22 +505,34 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
       if (st >= NQK - kVAhead) vf[st - (NQK - kVAhead)] = read_v(vb, st - (NQK - kVAhead));
       // this step's share of the softmax of S(t)
 #pragma unroll
-      for (int e = st * 16 / NQK; e < (st + 1) * 16 / NQK; ++e)
+      for (int e = st * 16 / NQK; e < (st + 1) * 16 / NQK; ++e) {
         pr[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(s_cur[e], scale_log2, mneg));
+        asm volatile("" : "+v"(pr[e]));  // keeps the exp in this step (not sunk past mask)
+      }
     }
     __builtin_amdgcn_sched_barrier(0);
     const vec bfrag[2] = {M::pack(pr), M::pack(pr + 8)};
+    mask(t + 1, s_next);
+    // PV(t), with the row sums of P(t) and the maximum of S(t+1) spread over
+    // its MFMAs (in-order issue: VALU work placed between the MFMAs runs
+    // while they execute)
+    float tmax = -__builtin_inff();
 #pragma unroll
     for (int f = 0; f < NPV; ++f) {
       __builtin_amdgcn_sched_barrier(0);
       if (f + kVAhead < NPV) vf[f + kVAhead] = read_v(vb, f + kVAhead);
       pv_mfma(f, vf[f], bfrag);
+#pragma unroll
+      for (int j = f * 8 / NPV; j < (f + 1) * 8 / NPV; ++j)
+        lsum = M::add_pair(bfrag[j / 4], j % 4, lsum);
+#pragma unroll
+      for (int e = f * 16 / NPV; e < (f + 1) * 16 / NPV; e += 2)
+        tmax = max3_plain(tmax, s_next[e], s_next[e + 1]);
     }
     __builtin_amdgcn_sched_barrier(0);
-    lsum = M::sum8(bfrag[1], M::sum8(bfrag[0], lsum));
 #pragma unroll
     for (int x = 0; x < H; ++x) vof_cur[x] = vof_new[x];
-    rescale(mask_max(t + 1, s_next));
+    rescale(max_halves(tmax));
   };
   f32x16_t s_alt;  // scores of the odd tiles (s_cur holds the even ones)
   for (int t = 0; t < ntiles; t += 2) {

@@ -54,6 +54,12 @@ __device__ inline float max_halves(float x) {
   asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"((uint32_t)p[0]), "v"((uint32_t)p[1]));
   return r;
 }
+// max(a, b, c) for values that are not signaling NaNs (as max_halves).
+__device__ inline float max3_plain(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
 __device__ inline float sum_halves(float x) {
   const uint32_t u = __builtin_bit_cast(uint32_t, x);
   const auto p = __builtin_amdgcn_permlane32_swap(u, u, false, false);

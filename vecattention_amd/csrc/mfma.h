@@ -20,14 +20,11 @@ template <> struct Mfma<bf16_t> {
     for (int e = 0; e < 8; ++e) r[e] = __bf16(x[e]);
     return r;
   }
-  // acc + the sum of the 8 elements of x (v_dot2c_f32_bf16 against (1, 1)).
-  __device__ static float sum8(vec x, float acc) {
+  // acc + x[2i] + x[2i+1] (v_dot2c_f32_bf16 against (1, 1)).
+  __device__ static float add_pair(vec x, int i, float acc) {
     typedef __bf16 pair __attribute__((ext_vector_type(2)));
     const pair one = {__bf16(1.f), __bf16(1.f)};
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      acc = __builtin_amdgcn_fdot2_f32_bf16(pair{x[2 * i], x[2 * i + 1]}, one, acc, false);
-    return acc;
+    return __builtin_amdgcn_fdot2_f32_bf16(pair{x[2 * i], x[2 * i + 1]}, one, acc, false);
   }
 };
 template <> struct Mfma<f16_t> {
@@ -41,14 +38,11 @@ template <> struct Mfma<f16_t> {
     for (int e = 0; e < 8; ++e) r[e] = _Float16(x[e]);
     return r;
   }
-  // acc + the sum of the 8 elements of x (v_dot2c_f32_f16 against (1, 1)).
-  __device__ static float sum8(vec x, float acc) {
+  // acc + x[2i] + x[2i+1] (v_dot2c_f32_f16 against (1, 1)).
+  __device__ static float add_pair(vec x, int i, float acc) {
     typedef _Float16 pair __attribute__((ext_vector_type(2)));
     const pair one = {_Float16(1.f), _Float16(1.f)};
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      acc = __builtin_amdgcn_fdot2(pair{x[2 * i], x[2 * i + 1]}, one, acc, false);
-    return acc;
+    return __builtin_amdgcn_fdot2(pair{x[2 * i], x[2 * i + 1]}, one, acc, false);
   }
 };
 
