@@ -371,12 +371,11 @@ static AttnMfmaCheck attn_mfma_check(int dtype, const void* q, const int64_t* sq
     return reinterpret_cast<uintptr_t>(p) % 16 == 0 && s[0] % a == 0 && s[1] % a == 0 &&
            s[2] % a == 0;
   };
-  // The kernel reads a zero row at byte offset Sk * row stride (past the
-  // buffer's range, which needs rows that do not overlap, or one broadcast
-  // row) and computes offsets in 32 bits with 24-bit multiplies.
+  // The kernel addresses K and V rows through buffer resources whose record
+  // stride (the row stride in bytes) is a 14-bit field.
   auto span_ok = [&](const int64_t* s) {
-    return Sk < (int64_t(1) << 24) && (s[2] == 0 || s[2] >= D) &&
-           s[2] * es < (int64_t(1) << 24) && (Sk * s[2] + D) * es < (int64_t(1) << 31);
+    return Sk < (int64_t(1) << 24) && s[2] >= 0 && s[2] * es < (int64_t(1) << 14) &&
+           ((Sk - 1) * s[2] + D) * es < (int64_t(1) << 31);
   };
   AttnMfmaCheck c;
   c.shape = va::attn_mfma_supported(dtype, D, qps);
@@ -402,8 +401,8 @@ static int attn_dispatch(int dtype, const void* q, const int64_t* sq, const void
       return fail(VA_ERR_UNSUPPORTED, "MFMA attention needs bf16/fp16, D in {64,128}, qps in {64,128}");
     if (!mfma_align) return fail(VA_ERR_UNSUPPORTED, "MFMA attention needs 16-byte aligned rows");
     if (!mfma_span)
-      return fail(VA_ERR_UNSUPPORTED, "MFMA attention needs Sk < 2^24, row strides < 16 MiB "
-                                      "that are 0 or at least D, and < 2 GiB of rows per kv head");
+      return fail(VA_ERR_UNSUPPORTED, "MFMA attention needs Sk < 2^24, K/V row strides "
+                                      "< 16 KiB and < 2 GiB of rows per kv head");
     if (!(softmax_scale > 0.f))
       return fail(VA_ERR_UNSUPPORTED, "MFMA attention needs a positive softmax scale");
     use_mfma = true;

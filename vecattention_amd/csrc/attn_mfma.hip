@@ -210,9 +210,11 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
   // ---- buffers -------------------------------------------------------------
   const T* kh = k + b * skb + hk * skh;
   const T* vh = v + b * svb + hk * svh;
-  const uint32_t krb = uint32_t(sks * 2), vrb = uint32_t(svs * 2);  // row bytes
-  const __amdgpu_buffer_rsrc_t krs = make_rsrc(kh, uint32_t(((Sk - 1) * sks + D) * 2));
-  const __amdgpu_buffer_rsrc_t vrs = make_rsrc(vh, uint32_t(((Sk - 1) * svs + D) * 2));
+  // K and V as Sk records of their row stride: a copy addresses row `key`,
+  // and any key outside [0, Sk) reads zeros (the host checks that the
+  // strides fit the resource's 14-bit field).
+  const __amdgpu_buffer_rsrc_t krs = make_rsrc_rows(kh, uint32_t(sks * 2), uint32_t(Sk));
+  const __amdgpu_buffer_rsrc_t vrs = make_rsrc_rows(vh, uint32_t(svs * 2), uint32_t(Sk));
   const __amdgpu_buffer_rsrc_t irs =
       make_rsrc(cols, uint32_t(nseg > 1 ? (cap > 0 ? cap : 0) : n_col) * 4u);
   const uint32_t smem_lds = lds_addr(smem);
@@ -273,39 +275,32 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
     }
   };
 
-  // Copy offsets of tile u: for each of this lane's H copies, the byte offset
-  // of its 16-byte chunk in K (kof) and V (vof), from the key ids in ids slot
-  // idslot.  Keys outside [0, Sk), rows past the tile's key count and every
-  // row of a tile past the end of the list are read as key Sk, whose offset
-  // Sk * row stride is past the buffer's range (the host checks that it does
-  // not wrap): their copies write zeros into a slot that is masked or never
-  // read.  Only partial tiles (a uniform branch) test the row count.
-  const uint32_t usk = uint32_t(Sk) & 0xffffffu;  // Sk < 2^24 (host check): 24-bit multiplies
-  auto copy_offsets = [&](int u, int idslot, uint32_t (&kof)[H], uint32_t (&vof)[H]) {
+  // Copy addresses of tile u: for each of this lane's H copies, the (row,
+  // byte offset) pair of its 16-byte chunk, the row being the key id in ids
+  // slot idslot; K and V copies of a tile use the same pairs.  Keys outside
+  // [0, Sk) read zeros; rows past the tile's key count and every row of a
+  // tile past the end of the list are given row 2^32 - 1 (also zeros), so
+  // their copies fill slots that are masked or never read.  Only partial
+  // tiles (a uniform branch) test the row count: a full tile costs no VALU.
+  auto copy_pairs = [&](int u, int idslot, uint64_t (&pr)[H]) {
     const int lim = tile_info(u).lim;
     uint32_t key[H];
 #pragma unroll
-    for (int x = 0; x < H; ++x) {
-      const uint32_t id = uint32_t(ids[idslot * kTileKeys + id_pos + x]);
-      key[x] = id < usk ? id : usk;
-    }
+    for (int x = 0; x < H; ++x) key[x] = uint32_t(ids[idslot * kTileKeys + id_pos + x]);
     if (lim < kTileKeys) {
 #pragma unroll
       for (int x = 0; x < H; ++x)  // row (wave*H + x)*RPC + qr holds a key below lim
-        if (qr >= lim - (wave * H + x) * RPC) key[x] = usk;
+        if (qr >= lim - (wave * H + x) * RPC) key[x] = 0xffffffffu;
     }
 #pragma unroll
-    for (int x = 0; x < H; ++x) {
-      kof[x] = __umul24(key[x], krb) + cchunk[x];
-      vof[x] = __umul24(key[x], vrb) + cchunk[x];
-    }
+    for (int x = 0; x < H; ++x) pr[x] = uint64_t(key[x]) | (uint64_t(cchunk[x]) << 32);
   };
   // Copy x of this wave into the K or V tile at LDS address base.
-  auto copy_k = [&](uint32_t base, int x, uint32_t off) {
-    copy16_to_lds(krs, base + uint32_t((wave * H + x) * 1024), off);
+  auto copy_k = [&](uint32_t base, int x, uint64_t pr) {
+    copy16_row_to_lds(krs, base + uint32_t((wave * H + x) * 1024), pr);
   };
-  auto copy_v = [&](uint32_t base, int x, uint32_t off) {
-    copy16_to_lds(vrs, base + uint32_t((wave * H + x) * 1024), off);
+  auto copy_v = [&](uint32_t base, int x, uint64_t pr) {
+    copy16_row_to_lds(vrs, base + uint32_t((wave * H + x) * 1024), pr);
   };
 
   // Wait for Q here: otherwise the compiler places the wait at the first MFMA
@@ -432,22 +427,22 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
   // room in the memory pipeline overlaps the matrix work already issued
   // instead of stalling every wave right after the barrier.
   constexpr int NQK = D / 16;  // QK MFMAs per tile
-  uint32_t vof_cur[H];         // V offsets of tile t+1 (its K copies went out earlier)
+  uint64_t vpr_cur[H];         // copy pairs of tile t+1 (its K copies went out earlier)
   f32x16_t s_cur;              // masked scores of tile t
   constexpr int W = S::kWaves;
   if (ntiles > 0) {
     if (wave < ntiles) stage_ids(wave, wave);  // tiles 0 .. W-1
     vm_lds_barrier();
-    uint32_t kof[H], vof[H];
-    copy_offsets(0, 0, kof, vof);
+    uint64_t pr0[H];
+    copy_pairs(0, 0, pr0);
 #pragma unroll
     for (int x = 0; x < H; ++x) {
-      copy_k(smem_lds, x, kof[x]);
-      copy_v(smem_lds + uint32_t(S::kTileBytes), x, vof[x]);
+      copy_k(smem_lds, x, pr0[x]);
+      copy_v(smem_lds + uint32_t(S::kTileBytes), x, pr0[x]);
     }
-    copy_offsets(1, 1, kof, vof_cur);
+    copy_pairs(1, 1, vpr_cur);
 #pragma unroll
-    for (int x = 0; x < H; ++x) copy_k(smem_lds + uint32_t(S::kStageBytes), x, kof[x]);
+    for (int x = 0; x < H; ++x) copy_k(smem_lds + uint32_t(S::kStageBytes), x, vpr_cur[x]);
     vm_lds_barrier();  // K(0), V(0), K(1) landed
     s_cur = qk(smem);
     mask(0, s_cur);
@@ -474,7 +469,7 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
 #pragma unroll
     for (int e = 0; e < 16; ++e) s_next[e] = 0.f;
     float pr[16];
-    uint32_t kof[H], vof_new[H];
+    uint64_t kpr[H];
     // K operands are read kAhead MFMAs ahead of their use (LDS latency); the
     // V^T operands of PV(t) kVAhead MFMAs ahead, the first ones during the
     // last QK steps.
@@ -491,16 +486,16 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
         a[st + kAhead] =
             __builtin_bit_cast(vec, *reinterpret_cast<const uint4*>(kb + koff[st + kAhead]));
       s_next = M::run(a[st], qreg[st], s_next);  // past the last tile: masked away below
-      if (st == 0) copy_offsets(t + 2, (t + 2) % S::kIdSlots, kof, vof_new);
+      if (st == 0) copy_pairs(t + 2, (t + 2) % S::kIdSlots, kpr);
       // copy c of the 2H of this iteration goes out after MFMA c*NQK/(2H):
       // first V(t+1) into V slot P^1, then K(t+2) into K slot P
 #pragma unroll
       for (int c = 0; c < 2 * H; ++c) {
         if (c * NQK / (2 * H) != st) continue;
         if (c < H)
-          copy_v(smem_lds + v_next, c, vof_cur[c]);
+          copy_v(smem_lds + v_next, c, vpr_cur[c]);
         else
-          copy_k(smem_lds + k_this, c - H, kof[c - H]);
+          copy_k(smem_lds + k_this, c - H, kpr[c - H]);
       }
       if (st >= NQK - kVAhead) vf[st - (NQK - kVAhead)] = read_v(vb, st - (NQK - kVAhead));
       // this step's share of the softmax of S(t)
@@ -531,7 +526,7 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
     }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int x = 0; x < H; ++x) vof_cur[x] = vof_new[x];
+    for (int x = 0; x < H; ++x) vpr_cur[x] = kpr[x];
     rescale(max_halves(tmax));
   };
   f32x16_t s_alt;  // scores of the odd tiles (s_cur holds the even ones)

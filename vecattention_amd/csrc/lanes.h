@@ -20,6 +20,19 @@ __device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t by
                                            0x00020000);
 }
 
+// Buffer resource over `rows` records of `stride` bytes (stride < 2^14, the
+// field's width): an access with index >= rows reads zeros, so any key id
+// outside [0, rows) is safe to use as an index.
+__device__ inline __amdgpu_buffer_rsrc_t make_rsrc_rows(const void* base, uint32_t stride,
+                                                        uint32_t rows) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  const uint64_t lo = uint32_t(__builtin_amdgcn_readfirstlane(int(uint32_t(a))));
+  const uint64_t hi = uint32_t(__builtin_amdgcn_readfirstlane(int(uint32_t(a >> 32))));
+  return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(lo | (hi << 32)),
+                                           (short)__builtin_amdgcn_readfirstlane(int(stride)),
+                                           __builtin_amdgcn_readfirstlane(int(rows)), 0x00020000);
+}
+
 // LDS byte address of a pointer into __shared__ memory.
 __device__ inline uint32_t lds_addr(const void* p) {
   return uint32_t(reinterpret_cast<uintptr_t>((lds_void_ptr)(const_cast<void*>(p))));
@@ -35,6 +48,15 @@ __device__ inline void copy16_to_lds(__amdgpu_buffer_rsrc_t r, uint32_t lds, uin
   asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
                :
                : "s"(__builtin_amdgcn_readfirstlane(int(lds))), "v"(voffset), "s"(r)
+               : "memory");
+}
+// The same through a row resource (make_rsrc_rows): the lane's address is
+// row index * stride + byte offset, the pair packed as index | offset << 32.
+__device__ inline void copy16_row_to_lds(__amdgpu_buffer_rsrc_t r, uint32_t lds,
+                                         uint64_t index_offset) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 idxen offen lds"
+               :
+               : "s"(__builtin_amdgcn_readfirstlane(int(lds))), "v"(index_offset), "s"(r)
                : "memory");
 }
 __device__ inline void copy4_to_lds(__amdgpu_buffer_rsrc_t r, uint32_t lds, uint32_t voffset) {
