@@ -128,7 +128,7 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
   const int l32 = lane % 32, hh = lane / 32;
   const int rh = wave % S::kRowHalves, kc = wave / S::kRowHalves;
 
-  const WorkOrder wo{lay.nc, B, Hq, Hk};
+  const WorkOrder wo{lay.nc, B, Hq, Hk, causal == 0};
   int64_t jr, bh;
   if (!wo.map_item(blockIdx.x, jr, bh)) return;  // idle block (uniform)
   const int64_t b = bh / Hq, h = bh % Hq, hk = h / (Hq / Hk);
@@ -590,7 +590,7 @@ static hipError_t launch_attn_mfma_tdq(const void* q, const int64_t* sq, const v
                                        float scale_log2, const int32_t* counts,
                                        const int32_t* indices, const RowLayout& lay, int nseg,
                                        int segk, hipStream_t stream) {
-  const int64_t nblocks = WorkOrder{lay.nc, B, Hq, Hk}.grid_items();
+  const int64_t nblocks = WorkOrder{lay.nc, B, Hq, Hk, causal == 0}.grid_items();
   hipLaunchKernelGGL((attn_mfma_kernel<T, D, QPS>), dim3(unsigned(nblocks)),
                      dim3(AttnShape<D, QPS>::kThreads), 0,
                      stream, static_cast<const T*>(q), sq[0], sq[1], sq[2],

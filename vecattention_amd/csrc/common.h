@@ -82,13 +82,20 @@ __device__ inline void vm_lds_barrier() {
 // Work order.  Work-groups are dispatched round-robin over the 8 XCDs of the
 // chip (block i runs on XCD i % 8), each with its own L2.  A work item is
 // (row block jr in [0, nrows), q head bh in [0, B*Hq)); items of one kv head
-// (b, hk) read the same K/V rows, so they are kept on the same XCDs, and each
-// XCD walks its items longest-first (descending jr).  grid_items() is the
-// launch size; map_item() returns false for the few idle blocks of a launch
-// whose kv-group count does not split evenly over the XCDs.
+// (b, hk) read the same K/V rows, so they are kept on the same XCDs:
+//  - fewer kv groups than XCDs: each group gets 8/g XCDs, which walk its
+//    items longest-first (descending jr);
+//  - otherwise, each XCD walks a contiguous share of the items in group-major
+//    order, i.e. about one group at a time, so that the rows its L2 holds are
+//    those of one kv head (the share is whole groups when g % 8 == 0; for
+//    other g only when every row costs the same, `equal_rows`, else the items
+//    are dealt round-robin, longest-first, to keep the XCDs balanced).
+// grid_items() is the launch size; map_item() returns false for the few idle
+// blocks of a launch whose items do not split evenly over the XCDs.
 // ---------------------------------------------------------------------------
 struct WorkOrder {
   int64_t nrows, B, Hq, Hk;
+  bool equal_rows;  // every row block costs the same (non-causal)
   static constexpr int kXcd = 8;
 
   __host__ __device__ int64_t nkv() const { return B * Hk; }
@@ -100,6 +107,7 @@ struct WorkOrder {
       const int64_t per = (rep() * nrows + copies - 1) / copies;
       return kXcd * per;
     }
+    if (g % kXcd == 0 || equal_rows) return kXcd * ((g * rep() * nrows + kXcd - 1) / kXcd);
     return nrows * B * Hq;
   }
   __host__ __device__ bool map_item(int64_t i, int64_t& jr, int64_t& bh) const {
@@ -115,12 +123,12 @@ struct WorkOrder {
       bh = b * Hq + hk * r + j % r;
       return true;
     }
-    if (g % kXcd == 0) {  // several kv groups per XCD
-      const int64_t per = g / kXcd;
-      const int64_t x = i % kXcd, s = i / kXcd;
-      jr = nrows - 1 - s / (per * r);
-      const int64_t rem = s % (per * r);
-      const int64_t grp = x + kXcd * (rem / r);
+    if (g % kXcd == 0 || equal_rows) {  // contiguous shares, group-major
+      const int64_t n = g * r * nrows, per = (n + kXcd - 1) / kXcd;
+      const int64_t L = (i % kXcd) * per + i / kXcd;
+      if (L >= n) return false;
+      const int64_t grp = L / (r * nrows), rem = L % (r * nrows);
+      jr = nrows - 1 - rem / r;
       const int64_t b = grp / Hk, hk = grp % Hk;
       bh = b * Hq + hk * r + rem % r;
       return true;

@@ -117,7 +117,7 @@ __global__ __launch_bounds__(256) void select_mfma_kernel(
   const int wave = tid >> 6, lane = tid & 63;
   const int l32 = lane & 31, hh = lane >> 5;
 
-  const WorkOrder wo{nrowsets, B, Hq, Hk};
+  const WorkOrder wo{nrowsets, B, Hq, Hk, causal == 0};
   int64_t rs, bh;
   if (!wo.map_item(blockIdx.x, rs, bh)) return;  // idle block (uniform)
   const int64_t b = bh / Hq, h = bh % Hq, hk = h / (Hq / Hk);
@@ -560,7 +560,7 @@ static hipError_t launch_select_mfma_td(const void* qs, int64_t sqb, int64_t sqh
   // that large has its only boundary at 0 either way).
   const int64_t gs = (group > (int64_t(1) << 31) / bk) ? (int64_t(1) << 31) : bk * group;
   const uint32_t gspan32 = uint32_t(gs);
-  const int64_t nblocks = WorkOrder{nrowsets, B, Hq, Hk}.grid_items();
+  const int64_t nblocks = WorkOrder{nrowsets, B, Hq, Hk, causal == 0}.grid_items();
   hipLaunchKernelGGL((select_mfma_kernel<T, D>), dim3(unsigned(nblocks)), dim3(256), 0,
                      stream, static_cast<const T*>(qs), sqb, sqh, sqn, static_cast<const T*>(k),
                      skb, skh, sks, B, Hq, Hk, Sk, qps, int(bk), gspan32, causal, bsq, gap, gaps,

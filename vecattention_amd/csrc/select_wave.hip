@@ -126,7 +126,7 @@ __global__ __launch_bounds__(256, 2) void select_wave_kernel(
   const int wave = __builtin_amdgcn_readfirstlane(tid / 64), lane = tid % 64;
   const int l32 = lane % 32, hh = lane / 32;
 
-  const WorkOrder wo{nrowsets * nseg, B, Hq, Hk};
+  const WorkOrder wo{nrowsets * nseg, B, Hq, Hk, causal == 0};
   int64_t item, bh;
   if (!wo.map_item(blockIdx.x, item, bh)) return;  // idle block (uniform)
   const int64_t rs = item / nseg;    // row set
@@ -659,7 +659,7 @@ static hipError_t launch_select_wave_tdb(const void* qs, int64_t sqb, int64_t sq
   // Group span in keys, capped at 2^31 (key offsets are below 2^24, so a span
   // that large has its only boundary at 0 either way).
   const int64_t gs = (group > (int64_t(1) << 31) / BK) ? (int64_t(1) << 31) : BK * group;
-  const int64_t nblocks = WorkOrder{nrowsets * nseg, B, Hq, Hk}.grid_items();
+  const int64_t nblocks = WorkOrder{nrowsets * nseg, B, Hq, Hk, causal == 0}.grid_items();
   hipLaunchKernelGGL((select_wave_kernel<T, D, BK>), dim3(unsigned(nblocks)), dim3(256), 0,
                      stream, static_cast<const T*>(qs), sqb, sqh, sqn, static_cast<const T*>(k),
                      skb, skh, sks, B, Hq, Hk, Sk, qps, uint32_t(gs), causal, bsq, gap, gaps, kmax,
