@@ -427,40 +427,44 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
   // room in the memory pipeline overlaps the matrix work already issued
   // instead of stalling every wave right after the barrier.
   constexpr int NQK = D / 16;  // QK MFMAs per tile
-  uint64_t vpr_cur[H];         // copy pairs of tile t+1 (its K copies went out earlier)
   f32x16_t s_cur;              // masked scores of tile t
   constexpr int W = S::kWaves;
   if (ntiles > 0) {
     if (wave < ntiles) stage_ids(wave, wave);  // tiles 0 .. W-1
     vm_lds_barrier();
-    uint64_t pr0[H];
-    copy_pairs(0, 0, pr0);
+    // K(0), K(1), V(0); after QK(0), K(2) into K(0)'s slot.  The loop's
+    // barriers leave the 2H most recent copies of the wave in flight.
+    uint64_t pr[H], pr1[H];
+    copy_pairs(0, 0, pr);
+    copy_pairs(1, 1, pr1);
 #pragma unroll
-    for (int x = 0; x < H; ++x) {
-      copy_k(smem_lds, x, pr0[x]);
-      copy_v(smem_lds + uint32_t(S::kTileBytes), x, pr0[x]);
-    }
-    copy_pairs(1, 1, vpr_cur);
+    for (int x = 0; x < H; ++x) copy_k(smem_lds, x, pr[x]);
 #pragma unroll
-    for (int x = 0; x < H; ++x) copy_k(smem_lds + uint32_t(S::kStageBytes), x, vpr_cur[x]);
-    vm_lds_barrier();  // K(0), V(0), K(1) landed
+    for (int x = 0; x < H; ++x) copy_k(smem_lds + uint32_t(S::kStageBytes), x, pr1[x]);
+#pragma unroll
+    for (int x = 0; x < H; ++x) copy_v(smem_lds + uint32_t(S::kTileBytes), x, pr[x]);
+    vm_lds_barrier_keep<2 * H>();  // K(0) landed
     s_cur = qk(smem);
     mask(0, s_cur);
     float tmax = -__builtin_inff();
 #pragma unroll
     for (int e = 0; e < 16; e += 2) tmax = max3_plain(tmax, s_cur[e], s_cur[e + 1]);
     rescale(max_halves(tmax));
+    lds_barrier();  // every wave is done with K(0)
+    copy_pairs(2, 2, pr);
+#pragma unroll
+    for (int x = 0; x < H; ++x) copy_k(smem_lds, x, pr[x]);
   }
   // One iteration; the parity P = t & 1 is a compile-time constant so that
   // the LDS slot addresses fold into the instructions' offsets and S(t),
   // S(t+1) alternate between two register sets.
   auto iteration = [&](int t, auto parity_tag, const f32x16_t& s_cur, f32x16_t& s_next) {
     constexpr int P = decltype(parity_tag)::value;
-    constexpr uint32_t k_this = uint32_t(P * S::kStageBytes);          // K slot P
-    constexpr uint32_t k_next = uint32_t((P ^ 1) * S::kStageBytes);    // K slot P^1
-    constexpr uint32_t v_this = k_this + uint32_t(S::kTileBytes);      // V slot P
-    constexpr uint32_t v_next = k_next + uint32_t(S::kTileBytes);      // V slot P^1
-    vm_lds_barrier();  // V(t), K(t+1) landed; K slot P, V slot P^1 free
+    constexpr uint32_t k_next = uint32_t((P ^ 1) * S::kStageBytes);    // K slot of t+1 and t+3
+    constexpr uint32_t v_this = uint32_t(P * S::kStageBytes + S::kTileBytes);  // V slot of t
+    constexpr uint32_t v_next = k_next + uint32_t(S::kTileBytes);      // V slot of t+1
+    // ---- first half: QK(t+1) next to the softmax of S(t); copies of V(t+1)
+    vm_lds_barrier_keep<2 * H>();  // K(t+1) landed; every wave is done with PV(t-1)
     if (P == 0 && t % W == 0) {  // every wave stages one of tiles t+W .. t+2W-1
       const int u = t + W + wave;
       if (u < ntiles) stage_ids(u, u % S::kIdSlots);
@@ -469,10 +473,9 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
 #pragma unroll
     for (int e = 0; e < 16; ++e) s_next[e] = 0.f;
     float pr[16];
-    uint64_t kpr[H];
-    // K operands are read kAhead MFMAs ahead of their use (LDS latency); the
-    // V^T operands of PV(t) kVAhead MFMAs ahead, the first ones during the
-    // last QK steps.
+    uint64_t cpr[H];
+    // K operands are read kAhead MFMAs ahead of their use (LDS latency), the
+    // V^T operands of PV(t) kVAhead MFMAs ahead.
     constexpr int kAhead = 3, kVAhead = 3;
     const unsigned char* vb = smem + v_this;
     vec a[NQK], vf[NPV];
@@ -486,18 +489,10 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
         a[st + kAhead] =
             __builtin_bit_cast(vec, *reinterpret_cast<const uint4*>(kb + koff[st + kAhead]));
       s_next = M::run(a[st], qreg[st], s_next);  // past the last tile: masked away below
-      if (st == 0) copy_pairs(t + 2, (t + 2) % S::kIdSlots, kpr);
-      // copy c of the 2H of this iteration goes out after MFMA c*NQK/(2H):
-      // first V(t+1) into V slot P^1, then K(t+2) into K slot P
+      if (st == 0) copy_pairs(t + 1, (t + 1) % S::kIdSlots, cpr);
 #pragma unroll
-      for (int c = 0; c < 2 * H; ++c) {
-        if (c * NQK / (2 * H) != st) continue;
-        if (c < H)
-          copy_v(smem_lds + v_next, c, vpr_cur[c]);
-        else
-          copy_k(smem_lds + k_this, c - H, kpr[c - H]);
-      }
-      if (st >= NQK - kVAhead) vf[st - (NQK - kVAhead)] = read_v(vb, st - (NQK - kVAhead));
+      for (int c = 0; c < H; ++c)  // copy c goes out after MFMA c * NQK / H
+        if (c * NQK / H == st) copy_v(smem_lds + v_next, c, cpr[c]);
       // this step's share of the softmax of S(t)
 #pragma unroll
       for (int e = st * 16 / NQK; e < (st + 1) * 16 / NQK; ++e) {
@@ -508,15 +503,23 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
     __builtin_amdgcn_sched_barrier(0);
     const vec bfrag[2] = {M::pack(pr), M::pack(pr + 8)};
     mask(t + 1, s_next);
-    // PV(t), with the row sums of P(t) and the maximum of S(t+1) spread over
-    // its MFMAs (in-order issue: VALU work placed between the MFMAs runs
-    // while they execute)
+    // ---- second half: PV(t), with the row sums of P(t) and the maximum of
+    // S(t+1) spread over its MFMAs (in-order issue: VALU work placed between
+    // the MFMAs runs while they execute); copies of K(t+3) into the slot QK
+    // just read
+    vm_lds_barrier_keep<2 * H>();  // V(t) landed; every wave is done with K(t+1)
+#pragma unroll
+    for (int f = 0; f < kVAhead; ++f) vf[f] = read_v(vb, f);
+    copy_pairs(t + 3, (t + 3) % S::kIdSlots, cpr);
     float tmax = -__builtin_inff();
 #pragma unroll
     for (int f = 0; f < NPV; ++f) {
       __builtin_amdgcn_sched_barrier(0);
       if (f + kVAhead < NPV) vf[f + kVAhead] = read_v(vb, f + kVAhead);
       pv_mfma(f, vf[f], bfrag);
+#pragma unroll
+      for (int c = 0; c < H; ++c)  // copy c goes out after MFMA c * NPV / H
+        if (c * NPV / H == f) copy_k(smem_lds + k_next, c, cpr[c]);
 #pragma unroll
       for (int j = f * 8 / NPV; j < (f + 1) * 8 / NPV; ++j)
         lsum = M::add_pair(bfrag[j / 4], j % 4, lsum);
@@ -525,8 +528,6 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
         tmax = max3_plain(tmax, s_next[e], s_next[e + 1]);
     }
     __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int x = 0; x < H; ++x) vpr_cur[x] = kpr[x];
     rescale(max_halves(tmax));
   };
   f32x16_t s_alt;  // scores of the odd tiles (s_cur holds the even ones)

@@ -77,6 +77,13 @@ __device__ inline void lds_barrier() {
 __device__ inline void vm_lds_barrier() {
   asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
+// The same, leaving this wave's N most recent global loads in flight (loads
+// complete in issue order, so every older one has landed).
+template <int N>
+__device__ inline void vm_lds_barrier_keep() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
+}
 
 // ---------------------------------------------------------------------------
 // Work order.  Work-groups are dispatched round-robin over the 8 XCDs of the
