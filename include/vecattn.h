@@ -169,6 +169,21 @@ int va_sparse_attn(int dtype, const void* q, int64_t sqb, int64_t sqh, int64_t s
                    const int32_t* indices, float softmax_scale, int kernel, void* stream);
 
 /*
+ * Dense attention over all keys (every key visible; causal: query row i sees
+ * keys [0, i + Sk - Sq], the last query aligned with the last key, so
+ * Sq <= Sk), on the same MFMA kernel as va_sparse_attn.  Replaces
+ * spattn/src/Fullprefill.py:4-16 (Full_prefill, flashinfer
+ * single_prefill_with_kv_cache), which the dispatcher at
+ * spattn/src/models/utils.py:99-128 calls on the text tokens around a vision
+ * span.  bf16/fp16, D in {64, 128}; GQA as in va_sparse_attn.
+ */
+int va_dense_attn(int dtype, const void* q, int64_t sqb, int64_t sqh, int64_t sqs,
+                  const void* k, int64_t skb, int64_t skh, int64_t sks, const void* v,
+                  int64_t svb, int64_t svh, int64_t svs, void* out, int64_t sob, int64_t soh,
+                  int64_t sos, int64_t B, int64_t Hq, int64_t Hk, int64_t Sq, int64_t Sk,
+                  int64_t D, int causal, float softmax_scale, void* stream);
+
+/*
  * va_sparse_attn on the segmented lists of va_select_segments (counts of shape
  * (B, Hq, nc, ceil(Sk/segment_keys))); MFMA kernel only.  No counterpart in
  * the reference: it is the second half of va_prefill's chunk step.

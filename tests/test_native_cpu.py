@@ -112,3 +112,23 @@ def test_workspace_size_covers_largest_chunk(L):
     last = L.va_select_index_capacity(B, Hq, S, qps, 1, 1, (S - chunk) // qps, chunk // qps, 0)
     assert ws >= last * 4 + B * Hq * (S // qps) * D * 2
     assert ws < last * 4 + B * Hq * (S // qps) * D * 2 + 1 << 20
+
+
+def _dense(L, **over):
+    args = dict(dtype=nat.VA_BF16, q=256, sqb=0, sqh=0, sqs=128, k=256, skb=0, skh=0, sks=128,
+                v=256, svb=0, svh=0, svs=128, out=256, sob=0, soh=0, sos=128, B=1, Hq=4, Hk=2,
+                Sq=100, Sk=300, D=128, causal=1, scale=0.088, stream=None)
+    args.update(over)
+    return L.va_dense_attn(*args.values())
+
+
+def test_dense_attn_argument_errors_before_launch(L):
+    assert _dense(L, q=None) == nat.VA_ERR_ARG
+    assert _dense(L, Sq=400) == nat.VA_ERR_ARG                 # causal needs Sq <= Sk
+    assert _dense(L, Hk=3) == nat.VA_ERR_ARG
+    assert _dense(L, Sk=0) == nat.VA_ERR_ARG
+    assert _dense(L, dtype=nat.VA_F32) == nat.VA_ERR_UNSUPPORTED
+    assert _dense(L, D=256) == nat.VA_ERR_UNSUPPORTED
+    assert _dense(L, sks=1 << 14) == nat.VA_ERR_UNSUPPORTED   # row stride past the 14-bit field
+    assert _dense(L, scale=-1.0) == nat.VA_ERR_UNSUPPORTED
+    assert _dense(L, dtype=9) == nat.VA_ERR_ARG

@@ -5,10 +5,17 @@ selection-stage helpers its threshold tuner calls.
 """
 from .vecattention import VecAttention_prefill, threshold_to_gap
 from .stages import average_vector, fuse_qk_softmax_minp_wo_causal
+from .dispatch import (DiffusionStepContext, FastPrefillConfig, Full_prefill,
+                       customize_prefill_attention, select_cfg_threshold)
 
 __all__ = [
     "VecAttention_prefill",
     "average_vector",
     "fuse_qk_softmax_minp_wo_causal",
     "threshold_to_gap",
+    "Full_prefill",
+    "FastPrefillConfig",
+    "customize_prefill_attention",
+    "DiffusionStepContext",
+    "select_cfg_threshold",
 ]

@@ -48,6 +48,9 @@ SIGNATURES = {
     "va_sparse_attn": (_int, [_int, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _vp, _i64, _i64,
                               _i64, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                               _i64, _int, _int, _i64, _i64, _i64, _vp, _vp, _f32, _int, _vp]),
+    "va_dense_attn": (_int, [_int, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _vp, _i64, _i64,
+                             _i64, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+                             _int, _f32, _vp]),
     "va_sparse_attn_segments": (_int, [_int, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _vp,
                                        _i64, _i64, _i64, _vp, _i64, _i64, _i64, _i64, _i64, _i64,
                                        _i64, _i64, _i64, _i64, _int, _int, _i64, _i64, _i64, _i64,

@@ -53,7 +53,7 @@ hipError_t launch_attn_mfma(int dtype, int64_t D, int64_t qps, const void* q, co
                             void* out, const int64_t* so, int64_t B, int64_t Hq, int64_t Hk,
                             int64_t Sq, int64_t Sk, int causal, float scale_log2,
                             const int32_t* counts, const int32_t* indices, const RowLayout& lay,
-                            int nseg, int segk, hipStream_t stream);
+                            int nseg, int segk, int64_t dense_qoff, hipStream_t stream);
 }  // namespace va
 
 namespace {
@@ -417,7 +417,7 @@ static int attn_dispatch(int dtype, const void* q, const int64_t* sq, const void
   hipError_t e = use_mfma
                      ? va::launch_attn_mfma(dtype, D, qps, q, sq, k, sk, v, sv, out, so, B, Hq,
                                             Hk, Sq, Sk, causal, scale_log2, counts, indices, lay,
-                                            nseg, int(segk), stream)
+                                            nseg, int(segk), -1, stream)
                      : va::launch_attn_simple(dtype, q, sq, k, sk, v, sv, out, so, B, Hq, Hk, Sq,
                                               Sk, D, qps, causal, scale_log2, counts, indices,
                                               lay, stream);
@@ -462,6 +462,39 @@ int va_sparse_attn(int dtype, const void* q, int64_t sqb, int64_t sqh, int64_t s
   return sparse_attn_impl(dtype, q, sqb, sqh, sqs, k, skb, skh, sks, v, svb, svh, svs, out, sob,
                           soh, sos, B, Hq, Hk, Sq, Sk, D, qps, causal, wo_init, J0, nc,
                           dense_stride, counts, indices, softmax_scale, kernel, 1, 0, stream);
+}
+
+int va_dense_attn(int dtype, const void* q, int64_t sqb, int64_t sqh, int64_t sqs,
+                  const void* k, int64_t skb, int64_t skh, int64_t sks, const void* v,
+                  int64_t svb, int64_t svh, int64_t svs, void* out, int64_t sob, int64_t soh,
+                  int64_t sos, int64_t B, int64_t Hq, int64_t Hk, int64_t Sq, int64_t Sk,
+                  int64_t D, int causal, float softmax_scale, void* stream) {
+  if (!dtype_ok(dtype)) return fail(VA_ERR_ARG, "unknown dtype %d", dtype);
+  if (!q || !k || !v || !out) return fail(VA_ERR_ARG, "null tensor pointer");
+  if (B <= 0 || Hq <= 0 || Hk <= 0 || Sq <= 0 || Sk <= 0 || D <= 0)
+    return fail(VA_ERR_ARG, "non-positive size");
+  if (Hq % Hk) return fail(VA_ERR_ARG, "num q heads not a multiple of kv heads");
+  if (causal && Sq > Sk) return fail(VA_ERR_ARG, "causal attention needs Sq <= Sk");
+  constexpr int64_t qps = 64;
+  const int64_t nc = cdiv(Sq, qps);
+  if (nc * B * Hq > kMaxGrid) return fail(VA_ERR_UNSUPPORTED, "grid too large");
+  const int64_t sq[3] = {sqb, sqh, sqs}, sk[3] = {skb, skh, sks}, sv[3] = {svb, svh, svs},
+                so[3] = {sob, soh, sos};
+  const AttnMfmaCheck chk = attn_mfma_check(dtype, q, sq, k, sk, v, sv, out, so, Sk, D, qps);
+  if (!chk.shape)
+    return fail(VA_ERR_UNSUPPORTED, "dense attention needs bf16/fp16 and D in {64, 128}");
+  if (!chk.align) return fail(VA_ERR_UNSUPPORTED, "dense attention needs 16-byte aligned rows");
+  if (!chk.span)
+    return fail(VA_ERR_UNSUPPORTED, "dense attention needs Sk < 2^24, K/V row strides < 16 KiB "
+                                    "and < 2 GiB of rows per kv head");
+  if (!(softmax_scale > 0.f)) return fail(VA_ERR_UNSUPPORTED, "softmax scale must be positive");
+  const va::RowLayout lay = make_layout(0, nc, qps, Sk, causal, 0, 0);
+  const hipError_t e = va::launch_attn_mfma(
+      dtype, D, qps, q, sq, k, sk, v, sv, out, so, B, Hq, Hk, Sq, Sk, causal,
+      softmax_scale * 1.4426950408889634f, nullptr, nullptr, lay, 1, 0,
+      causal ? Sk - Sq : 0, static_cast<hipStream_t>(stream));
+  const int rc = hip_check(e, "dense attention launch");
+  return rc ? rc : ok();
 }
 
 int va_sparse_attn_segments(int dtype, const void* q, int64_t sqb, int64_t sqh, int64_t sqs,

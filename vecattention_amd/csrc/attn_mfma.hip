@@ -112,7 +112,7 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
     T* __restrict__ out, int64_t sob, int64_t soh, int64_t sos, int64_t B,
     int64_t Hq, int64_t Hk, int64_t Sq, int64_t Sk, int causal, float scale_log2,
     const int32_t* __restrict__ counts, const int32_t* __restrict__ indices,
-    RowLayout lay, int nseg, int segk) {
+    RowLayout lay, int nseg, int segk, int64_t dense_qoff) {
   using S = AttnShape<D, QPS>;
   using M = Mfma<T>;
   using vec = typename M::vec;
@@ -180,7 +180,8 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
   }
   if (cnt > cap) cnt = cap;
   const int32_t* cols = indices ? indices + lay.row_offset(bh, jr) : nullptr;
-  const KeyList kl = KeyList::make(J, QPS, Sk, causal, cnt, cols);
+  const KeyList kl = dense_qoff >= 0 ? KeyList::dense(J, QPS, Sk, causal, dense_qoff)
+                                     : KeyList::make(J, QPS, Sk, causal, cnt, cols);
   // Every count below fits in 32 bits (the host checks Sk < 2^24).
   const int n_init = int(kl.n_init), n_diag = int(kl.n_diag), n_col = int(kl.n_col);
   const int diag0 = int(kl.diag0);
@@ -590,14 +591,14 @@ static hipError_t launch_attn_mfma_tdq(const void* q, const int64_t* sq, const v
                                        int64_t Hk, int64_t Sq, int64_t Sk, int causal,
                                        float scale_log2, const int32_t* counts,
                                        const int32_t* indices, const RowLayout& lay, int nseg,
-                                       int segk, hipStream_t stream) {
+                                       int segk, int64_t dense_qoff, hipStream_t stream) {
   const int64_t nblocks = WorkOrder{lay.nc, B, Hq, Hk, causal == 0}.grid_items();
   hipLaunchKernelGGL((attn_mfma_kernel<T, D, QPS>), dim3(unsigned(nblocks)),
                      dim3(AttnShape<D, QPS>::kThreads), 0,
                      stream, static_cast<const T*>(q), sq[0], sq[1], sq[2],
                      static_cast<const T*>(k), sk[0], sk[1], sk[2], static_cast<const T*>(v),
                      sv[0], sv[1], sv[2], static_cast<T*>(out), so[0], so[1], so[2], B, Hq, Hk,
-                     Sq, Sk, causal, scale_log2, counts, indices, lay, nseg, segk);
+                     Sq, Sk, causal, scale_log2, counts, indices, lay, nseg, segk, dense_qoff);
   return hipGetLastError();
 }
 
@@ -608,12 +609,12 @@ static hipError_t launch_attn_mfma_t(int64_t D, int64_t qps, const void* q, cons
                                      int64_t Hq, int64_t Hk, int64_t Sq, int64_t Sk, int causal,
                                      float scale_log2, const int32_t* counts,
                                      const int32_t* indices, const RowLayout& lay, int nseg,
-                                     int segk, hipStream_t stream) {
+                                     int segk, int64_t dense_qoff, hipStream_t stream) {
 #define VA_ATTN_CASE(DD, QQ)                                                                   \
   if (D == DD && qps == QQ)                                                                    \
     return launch_attn_mfma_tdq<T, DD, QQ>(q, sq, k, sk, v, sv, out, so, B, Hq, Hk, Sq, Sk,   \
                                            causal, scale_log2, counts, indices, lay, nseg,    \
-                                           segk, stream);
+                                           segk, dense_qoff, stream);
   VA_ATTN_CASE(64, 64)
   VA_ATTN_CASE(128, 64)
   VA_ATTN_CASE(64, 128)
@@ -631,13 +632,15 @@ hipError_t launch_attn_mfma(int dtype, int64_t D, int64_t qps, const void* q, co
                             void* out, const int64_t* so, int64_t B, int64_t Hq, int64_t Hk,
                             int64_t Sq, int64_t Sk, int causal, float scale_log2,
                             const int32_t* counts, const int32_t* indices, const RowLayout& lay,
-                            int nseg, int segk, hipStream_t stream) {
+                            int nseg, int segk, int64_t dense_qoff, hipStream_t stream) {
   if (dtype == kBF16)
     return launch_attn_mfma_t<bf16_t>(D, qps, q, sq, k, sk, v, sv, out, so, B, Hq, Hk, Sq, Sk,
-                                      causal, scale_log2, counts, indices, lay, nseg, segk, stream);
+                                      causal, scale_log2, counts, indices, lay, nseg, segk,
+                                      dense_qoff, stream);
   if (dtype == kF16)
     return launch_attn_mfma_t<f16_t>(D, qps, q, sq, k, sk, v, sv, out, so, B, Hq, Hk, Sq, Sk,
-                                     causal, scale_log2, counts, indices, lay, nseg, segk, stream);
+                                     causal, scale_log2, counts, indices, lay, nseg, segk,
+                                     dense_qoff, stream);
   return hipErrorInvalidValue;
 }
 

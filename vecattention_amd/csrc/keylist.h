@@ -42,6 +42,28 @@ struct KeyList {
     }
     return kl;
   }
+  // Every key, for dense attention (the reference's Full_prefill).  A causal
+  // row at absolute position qoff + J*qps + r sees keys up to that position
+  // (qoff = Sk - Sq aligns the last query with the last key): the span
+  // [0, a0) whole and the diagonal span [a0, a0 + qps) under the causal mask,
+  // a0 = qoff + J*qps.  A non-causal row sees all Sk keys.
+  __device__ static KeyList dense(int64_t J, int64_t qps, int64_t Sk, int causal, int64_t qoff) {
+    KeyList kl;
+    kl.cols = nullptr;
+    kl.n_col = 0;
+    if (causal) {
+      const int64_t a0 = qoff + J * qps;
+      kl.n_init = a0 < Sk ? a0 : Sk;
+      kl.diag0 = a0;
+      const int64_t rem = Sk - a0;
+      kl.n_diag = rem < qps ? (rem > 0 ? rem : 0) : qps;
+    } else {
+      kl.n_init = Sk;
+      kl.diag0 = 0;
+      kl.n_diag = 0;
+    }
+    return kl;
+  }
   __device__ int64_t total() const { return n_init + n_diag + n_col; }
   __device__ int64_t key(int64_t p) const {
     if (p < n_init) return p;

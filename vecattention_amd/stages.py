@@ -187,6 +187,28 @@ def sparse_attention(q, k, v, out, J0, nc, counts, indices, causal, q_pooling_si
     return out
 
 
+def dense_attention(q, k, v, out=None, causal=True, softmax_scale=None):
+    """Attention over every key (va_dense_attn): (B, Hq, Sq, D) q, (B, Hk, Sk, D)
+    k/v; causal rows see keys up to i + Sk - Sq."""
+    q = q if q.stride(-1) == 1 else q.contiguous()
+    k = k if k.stride(-1) == 1 else k.contiguous()
+    v = v if v.stride(-1) == 1 else v.contiguous()
+    B, Hq, Sq, D = q.shape
+    Hk, Sk = k.shape[1], k.shape[2]
+    if out is None:
+        out = torch.empty_like(q)
+    if softmax_scale is None:
+        softmax_scale = 1.0 / math.sqrt(D)
+    with torch.cuda.device(q.device):
+        rc = nat.lib().va_dense_attn(
+            nat.dtype_code(q), nat.ptr(q), q.stride(0), q.stride(1), q.stride(2), nat.ptr(k),
+            k.stride(0), k.stride(1), k.stride(2), nat.ptr(v), v.stride(0), v.stride(1), v.stride(2),
+            nat.ptr(out), out.stride(0), out.stride(1), out.stride(2), B, Hq, Hk, Sq, Sk, D,
+            int(causal), float(softmax_scale), _stream(q))
+    nat.check("va_dense_attn", rc)
+    return out
+
+
 def fuse_qk_softmax_minp_wo_causal(
     avg_q_chunk,
     k,
