@@ -104,7 +104,11 @@ struct TileInfo {
   bool diag;
 };
 
-template <typename T, int D, int QPS>
+// kDense: every key of the block's rows (dense attention, causal offset
+// dense_qoff) instead of the local blocks and the selected columns; a
+// separate instantiation, so that the sparse kernel's code does not carry
+// the general key-span arithmetic.
+template <typename T, int D, int QPS, bool kDense>
 __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == kThreads
     const T* __restrict__ q, int64_t sqb, int64_t sqh, int64_t sqs,
     const T* __restrict__ k, int64_t skb, int64_t skh, int64_t sks,
@@ -180,8 +184,11 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
   }
   if (cnt > cap) cnt = cap;
   const int32_t* cols = indices ? indices + lay.row_offset(bh, jr) : nullptr;
-  const KeyList kl = dense_qoff >= 0 ? KeyList::dense(J, QPS, Sk, causal, dense_qoff)
-                                     : KeyList::make(J, QPS, Sk, causal, cnt, cols);
+  KeyList kl;
+  if constexpr (kDense)
+    kl = KeyList::dense(J, QPS, Sk, causal, dense_qoff);
+  else
+    kl = KeyList::make(J, QPS, Sk, causal, cnt, cols);
   // Every count below fits in 32 bits (the host checks Sk < 2^24).
   const int n_init = int(kl.n_init), n_diag = int(kl.n_diag), n_col = int(kl.n_col);
   const int diag0 = int(kl.diag0);
@@ -593,12 +600,24 @@ static hipError_t launch_attn_mfma_tdq(const void* q, const int64_t* sq, const v
                                        const int32_t* indices, const RowLayout& lay, int nseg,
                                        int segk, int64_t dense_qoff, hipStream_t stream) {
   const int64_t nblocks = WorkOrder{lay.nc, B, Hq, Hk, causal == 0}.grid_items();
-  hipLaunchKernelGGL((attn_mfma_kernel<T, D, QPS>), dim3(unsigned(nblocks)),
+  if (dense_qoff >= 0) {
+    if constexpr (QPS == 64) {  // dense attention runs on 64-row blocks
+      hipLaunchKernelGGL((attn_mfma_kernel<T, D, QPS, true>), dim3(unsigned(nblocks)),
+                         dim3(AttnShape<D, QPS>::kThreads), 0, stream, static_cast<const T*>(q),
+                         sq[0], sq[1], sq[2], static_cast<const T*>(k), sk[0], sk[1], sk[2],
+                         static_cast<const T*>(v), sv[0], sv[1], sv[2], static_cast<T*>(out),
+                         so[0], so[1], so[2], B, Hq, Hk, Sq, Sk, causal, scale_log2, counts,
+                         indices, lay, nseg, segk, dense_qoff);
+      return hipGetLastError();
+    }
+    return hipErrorInvalidValue;
+  }
+  hipLaunchKernelGGL((attn_mfma_kernel<T, D, QPS, false>), dim3(unsigned(nblocks)),
                      dim3(AttnShape<D, QPS>::kThreads), 0,
                      stream, static_cast<const T*>(q), sq[0], sq[1], sq[2],
                      static_cast<const T*>(k), sk[0], sk[1], sk[2], static_cast<const T*>(v),
                      sv[0], sv[1], sv[2], static_cast<T*>(out), so[0], so[1], so[2], B, Hq, Hk,
-                     Sq, Sk, causal, scale_log2, counts, indices, lay, nseg, segk, dense_qoff);
+                     Sq, Sk, causal, scale_log2, counts, indices, lay, nseg, segk, 0);
   return hipGetLastError();
 }
 
