@@ -46,6 +46,9 @@ def parse():
     ap.add_argument("--extra-json", default=None, help="append the result line to this file too")
     ap.add_argument("--threshold", type=float, default=None,
                     help="use this threshold instead of calibrating one to the keep ratio")
+    ap.add_argument("--tuner", action="store_true",
+                    help="time the threshold tuner's recall/sparsity evaluation "
+                         "(seg_pr_perHead) on the workload's shapes instead of the prefill")
     return ap.parse_args()
 
 
@@ -269,6 +272,110 @@ def cpu_baseline(wl, q_cpu, k_cpu, v_cpu, threshold, seconds):
             "host_threads_available": len(os.sched_getaffinity(0))}
 
 
+# -------------------------------------------------------------------- tuner --
+
+def bench_tuner(args, wl, dev):
+    """One seg_pr_perHead call (spattn/threshold/model_tuner.py:118-226) per
+    step on the workload's shapes: fp32 Q/K holding bf16 values (the tuner's
+    load_tensor copies of the dumped states), K expanded to the q heads (the
+    dumps follow repeat_kv), a per-head threshold vector around the first
+    bisection midpoint, chunk 8192 (the reference's default).  Beside it: the
+    dense-statistics kernel alone (its MFMA roofline) and the reference's
+    dense step (matmul + mask + fp32 softmax of model_tuner.py:193-199) timed
+    in torch on the same GPU for one (head, chunk) and scaled to the call, a
+    lower bound of the reference's evaluation (its mask loops excluded)."""
+    from vecattention_amd import stages, tuner
+    from vecattention_amd.synth import workload_inputs
+    q_cpu, k_cpu, _ = workload_inputs(wl, seed=0)
+    rep = wl.Hq // wl.Hk
+    q = q_cpu.float().to(dev)
+    k = k_cpu.repeat_interleave(rep, dim=1).float().to(dev)
+    B, H, S, D = q.shape
+    base = args.threshold if args.threshold is not None else 0.25
+    th = (base * torch.linspace(0.8, 1.2, H)).clamp(max=0.999).to(dev)
+    chunk = 8 * 1024
+
+    def call():
+        return tuner.seg_pr_perHead(q, k, wl.q_pooling_size, wl.k_local_size, wl.group_k_block,
+                                    threshold=th, chunk_size=chunk, causal=wl.causal)
+
+    def timed(fn, reps, warm):
+        for _ in range(warm):
+            fn()
+        torch.cuda.synchronize()
+        ts = []
+        for _ in range(reps):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            fn()
+            b.record()
+            torch.cuda.synchronize()
+            ts.append(a.elapsed_time(b))
+        return statistics.median(ts)
+
+    for _ in range(args.warmup):
+        r, sp = call()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        r, sp = call()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / max(args.steps, 1)
+    print(f"[bench] tuner: {ms:.3f} ms per seg_pr_perHead; recall {r.mean().item():.4f} "
+          f"sparsity {sp.mean().item():.4f}", file=sys.stderr, flush=True)
+
+    qb, kb = q.to(torch.bfloat16), k.to(torch.bfloat16)
+    stats = torch.empty(B, H, S, 2, dtype=torch.float32, device=dev)
+    t_dense = timed(lambda: stages.dense_row_stats(qb, kb, wl.causal, stats=stats), 5, 2)
+    visible = S * (S + 1) // 2 if wl.causal else S * S
+    F_dense = 2 * D * B * H * visible
+    dense_tflops = F_dense / (t_dense * 1e-3) / 1e12
+
+    rows = min(chunk, S)
+    mask = None
+    if wl.causal:
+        mask = torch.triu(torch.full((rows, S), float("-inf"), device=dev), diagonal=1)
+
+    def ref_dense():
+        a = torch.matmul(q[0, 0, :rows], k[0, 0].transpose(-2, -1)) / math.sqrt(D)
+        if mask is not None:
+            a = a + mask
+        return torch.softmax(a, dim=-1, dtype=torch.float32)
+    t_ref = timed(ref_dense, 3, 1) * B * H * math.ceil(S / chunk)
+    result = {
+        "metric": "tuner seg_pr_perHead latency (ms)",
+        "value": round(ms, 3),
+        "unit": "ms",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32 inputs (bf16 values), bf16 MFMA scores, fp32 sums",
+        "data": "synthetic (the workload's seeded inputs as fp32 copies)",
+        "config": {"workload": "tuner-" + wl.name, "B": B, "H": H, "S": S, "D": D,
+                   "causal": wl.causal, "block_size_q": wl.q_pooling_size,
+                   "block_size_k": wl.k_local_size, "group_size_k": wl.group_k_block,
+                   "chunk_size": chunk, "threshold_base": base},
+        "dense_stats_ms": round(t_dense, 4),
+        "reference_dense_step_ms_lower_bound": round(t_ref, 2),
+        "speedup_vs_reference_dense_step": round(t_ref / ms, 2),
+        "roofline": {"bound": "mfma", "kernel": "attn_mfma_kernel (dense statistics form)",
+                     "achieved": round(dense_tflops, 3), "peak": BF16_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(dense_tflops / BF16_PEAK_TFLOPS, 4),
+                     "traffic": None},
+        "recall_mean": round(r.mean().item(), 6),
+        "sparsity_mean": round(sp.mean().item(), 6),
+    }
+    line = json.dumps(result)
+    print(line, flush=True)
+    if args.extra_json:
+        with open(args.extra_json, "a") as f:
+            f.write(line + "\n")
+
+
 # --------------------------------------------------------------------- main --
 
 def main():
@@ -283,6 +390,9 @@ def main():
 
     wl = WORKLOADS[args.config]
     dev = torch.device("cuda:0")
+    if args.tuner:
+        bench_tuner(args, wl, dev)
+        return
     t_gen = time.perf_counter()
     q_cpu, k_cpu, v_cpu = workload_inputs(wl, seed=0)
     q, k, v = q_cpu.to(dev), k_cpu.to(dev), v_cpu.to(dev)

@@ -184,6 +184,34 @@ int va_dense_attn(int dtype, const void* q, int64_t sqb, int64_t sqh, int64_t sq
                   int64_t D, int causal, float softmax_scale, void* stream);
 
 /*
+ * Per-row softmax statistics for the threshold tuner's recall evaluation
+ * (seg_pr_perHead, spattn/threshold/model_tuner.py:118-226): for each query
+ * row i of head bh, stats[(bh*Sq + i)*2 + 0] = m and [+1] = l with
+ * l = sum over the row's keys j of 2^(s_ij - m), s_ij = q_i.k_j *
+ * softmax_scale * log2(e) (m = -inf, l = 0 for a row without keys).  m is a
+ * reference level within 8 of the row maximum, not necessarily the maximum.
+ *
+ * va_sparse_row_stats: the keys of va_sparse_attn (local blocks + selected
+ * columns, causal mask on the diagonal), rows of q-blocks [J0, J0+nc), same
+ * arguments minus V and the output.  va_dense_row_stats: every key (causal:
+ * j <= i + Sk - Sq), every row.  The row's attention mass on its selected
+ * keys, the tuner's per-row recall (model_tuner.py:202-219), is
+ * l_sparse * 2^(m_sparse - m_dense) / l_dense.  `kernel` as in
+ * va_sparse_attn: MFMA for bf16/fp16 (D in {64, 128}), the per-row kernel
+ * for fp32.
+ */
+int va_sparse_row_stats(int dtype, const void* q, int64_t sqb, int64_t sqh, int64_t sqs,
+                        const void* k, int64_t skb, int64_t skh, int64_t sks, int64_t B,
+                        int64_t Hq, int64_t Hk, int64_t Sq, int64_t Sk, int64_t D,
+                        int64_t q_pooling_size, int causal, int wo_init, int64_t J0, int64_t nc,
+                        int64_t dense_stride, const int32_t* counts, const int32_t* indices,
+                        float softmax_scale, int kernel, float* stats, void* stream);
+int va_dense_row_stats(int dtype, const void* q, int64_t sqb, int64_t sqh, int64_t sqs,
+                       const void* k, int64_t skb, int64_t skh, int64_t sks, int64_t B,
+                       int64_t Hq, int64_t Hk, int64_t Sq, int64_t Sk, int64_t D, int causal,
+                       float softmax_scale, int kernel, float* stats, void* stream);
+
+/*
  * va_sparse_attn on the segmented lists of va_select_segments (counts of shape
  * (B, Hq, nc, ceil(Sk/segment_keys))); MFMA kernel only.  No counterpart in
  * the reference: it is the second half of va_prefill's chunk step.

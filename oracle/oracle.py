@@ -15,6 +15,9 @@ Pieces and the reference lines they restate:
                       clipped to S_k, union selected columns, causal mask,
                       softmax scale 1/sqrt(D)); an empty key set gives 0
   prefill             spattn/src/VecAttention.py:43-123 (gap, chunk loop)
+  seg_pr_perhead      spattn/threshold/model_tuner.py:118-226 (the tuner's
+                      recall / sparsity evaluation: dense softmax per head,
+                      boolean mask of local blocks and selected columns)
 
 Pinning (tests/test_oracle.py): closed forms for pooling and gap; hand-derived
 known answers for the selection rule (prefix maximum updated before the
@@ -234,3 +237,57 @@ def prefill(q, k, v, threshold, q_pooling_size=128, k_local_size=128, group_k_bl
                       acc=acc)
         out[:, :, i:i + o.shape[2]] = o
     return out, chunks
+
+
+def seg_pr_perhead(q, k, block_size_q, block_size_k=16, group_size_k=16, threshold=None,
+                   chunk_size=8 * 1024, causal=False, dtype="float32", bsq=64):
+    """(recall (H,), sparsity (H,)) in float64, restating model_tuner.py:118-226.
+
+    q (B,H,S,D), k (B,Hk,Sk,D) float values of element type `dtype`;
+    threshold: per-head (H,) values.  gap = -log(th + 1e-50) in fp32
+    (model_tuner.py:150; 1e-50 is 0 in fp32).  Per chunk: pooled rows,
+    selection with wo_initial=causal (:183-187), then per (b, h) the dense
+    softmax with the top-left causal mask (:139-143,193-199), the boolean mask
+    of the blocks [off, min(off+64, Sk)) and the selected columns (:201-216),
+    recall = masked row sums (:216,220) and sparsity += (1 - mean(mask count /
+    visible count)) * chunk_len (:218-219), divided by B and S (:222-223).
+    """
+    q = as_f32(q).astype(np.float64)
+    k = as_f32(k).astype(np.float64)
+    B, H, S, D = q.shape
+    Hk, Sk = k.shape[1], k.shape[2]
+    rep = H // Hk
+    th = np.asarray(threshold, np.float32)
+    with np.errstate(divide="ignore"):
+        gap = (-np.log(th + np.float32(1e-50))).astype(np.float32)
+    gaps = np.ascontiguousarray(np.broadcast_to(gap, (B, H)).reshape(-1), np.float32)
+    _, qs = pool(q.astype(np.float32), block_size_q, dtype)
+    blk_count, blk_idx = local_blocks(B, H, S, block_size_q, causal)
+    recalls = np.zeros((B, H, S))
+    sparsity = np.zeros(H)
+    scale = 1.0 / math.sqrt(D)
+    for c0 in range(0, S, chunk_size):
+        rows = min(chunk_size, S - c0)
+        J0, nc = c0 // block_size_q, math.ceil(rows / block_size_q)
+        _, lists = select(qs, k.astype(np.float32), J0, nc, gaps, block_size_q, block_size_k,
+                          group_size_k, causal, causal, bsq)
+        pos = np.arange(c0, c0 + rows)
+        allowed = (np.arange(Sk)[None, :] <= pos[:, None]) if causal else np.ones((rows, Sk), bool)
+        for b in range(B):
+            for h in range(H):
+                s = (q[b, h, c0:c0 + rows] @ k[b, h // rep].T) * scale
+                s = np.where(allowed, s, -np.inf)
+                p = np.exp(s - s.max(axis=1, keepdims=True))
+                p /= p.sum(axis=1, keepdims=True)
+                mask = np.zeros((rows, Sk), bool)
+                for jr in range(nc):
+                    J = J0 + jr
+                    r0, r1 = jr * block_size_q, min((jr + 1) * block_size_q, rows)
+                    for off in blk_idx[b, h, J, :blk_count[b, h, J]]:
+                        mask[r0:r1, int(off):min(int(off) + SPATTN_BLOCK_SIZE_K, Sk)] = True
+                    mask[r0:r1, lists[b][h][jr]] = True
+                sparsity[h] += (1.0 - (mask.sum(axis=1) / allowed.sum(axis=1)).mean()) * rows
+                recalls[b, h, c0:c0 + rows] = (p * mask).sum(axis=1)
+    sparsity /= B
+    sparsity /= S
+    return recalls.sum(axis=(0, 2)) / (B * S), sparsity

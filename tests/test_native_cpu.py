@@ -132,3 +132,36 @@ def test_dense_attn_argument_errors_before_launch(L):
     assert _dense(L, sks=1 << 14) == nat.VA_ERR_UNSUPPORTED   # row stride past the 14-bit field
     assert _dense(L, scale=-1.0) == nat.VA_ERR_UNSUPPORTED
     assert _dense(L, dtype=9) == nat.VA_ERR_ARG
+
+
+def _dense_stats(L, **over):
+    args = dict(dtype=nat.VA_BF16, q=256, sqb=0, sqh=0, sqs=128, k=256, skb=0, skh=0, sks=128,
+                B=1, Hq=4, Hk=2, Sq=100, Sk=300, D=128, causal=1, scale=0.088,
+                kernel=nat.VA_ATTN_MFMA, stats=256, stream=None)
+    args.update(over)
+    return L.va_dense_row_stats(*args.values())
+
+
+def _sparse_stats(L, **over):
+    args = dict(dtype=nat.VA_BF16, q=256, sqb=0, sqh=0, sqs=128, k=256, skb=0, skh=0, sks=128,
+                B=1, Hq=4, Hk=2, Sq=256, Sk=256, D=128, qps=64, causal=1, wo_init=1, J0=0,
+                nc=4, dense_stride=0, counts=256, indices=256, scale=0.088,
+                kernel=nat.VA_ATTN_MFMA, stats=256, stream=None)
+    args.update(over)
+    return L.va_sparse_row_stats(*args.values())
+
+
+def test_row_stats_argument_errors_before_launch(L):
+    assert _dense_stats(L, stats=None) == nat.VA_ERR_ARG
+    assert _dense_stats(L, q=None) == nat.VA_ERR_ARG
+    assert _dense_stats(L, Sq=400) == nat.VA_ERR_ARG            # causal needs Sq <= Sk
+    assert _dense_stats(L, Hk=3) == nat.VA_ERR_ARG
+    assert _dense_stats(L, dtype=nat.VA_F32) == nat.VA_ERR_UNSUPPORTED  # MFMA asked for fp32
+    assert _dense_stats(L, D=96) == nat.VA_ERR_UNSUPPORTED
+    assert _dense_stats(L, scale=-1.0) == nat.VA_ERR_UNSUPPORTED
+    assert _dense_stats(L, kernel=7) == nat.VA_ERR_ARG
+    assert _sparse_stats(L, stats=None) == nat.VA_ERR_ARG
+    assert _sparse_stats(L, counts=None) == nat.VA_ERR_ARG      # counts without indices
+    assert _sparse_stats(L, Sq=300) == nat.VA_ERR_UNSUPPORTED   # causal needs Sq == Sk
+    assert _sparse_stats(L, nc=5) == nat.VA_ERR_ARG             # rows past the q-blocks
+    assert _sparse_stats(L, dtype=nat.VA_F32) == nat.VA_ERR_UNSUPPORTED

@@ -7,6 +7,7 @@ from .vecattention import VecAttention_prefill, threshold_to_gap
 from .stages import average_vector, fuse_qk_softmax_minp_wo_causal
 from .dispatch import (DiffusionStepContext, FastPrefillConfig, Full_prefill,
                        customize_prefill_attention, select_cfg_threshold)
+from .tuner import seg_pr_perHead
 
 __all__ = [
     "VecAttention_prefill",
@@ -18,4 +19,5 @@ __all__ = [
     "customize_prefill_attention",
     "DiffusionStepContext",
     "select_cfg_threshold",
+    "seg_pr_perHead",
 ]

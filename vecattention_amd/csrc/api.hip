@@ -24,7 +24,8 @@ hipError_t launch_attn_simple(int dtype, const void* q, const int64_t* sq, const
                               const int64_t* so, int64_t B, int64_t Hq, int64_t Hk, int64_t Sq,
                               int64_t Sk, int64_t D, int64_t qps, int causal, float scale_log2,
                               const int32_t* counts, const int32_t* indices,
-                              const RowLayout& lay, hipStream_t stream);
+                              const RowLayout& lay, int64_t dense_qoff, float* stats,
+                              hipStream_t stream);
 bool attn_mfma_supported(int dtype, int64_t D, int64_t qps);
 bool select_mfma_supported(int dtype, int64_t D, int64_t bk);
 hipError_t launch_select_mfma(int dtype, const void* qs, int64_t sqb, int64_t sqh, int64_t sqn,
@@ -53,7 +54,8 @@ hipError_t launch_attn_mfma(int dtype, int64_t D, int64_t qps, const void* q, co
                             void* out, const int64_t* so, int64_t B, int64_t Hq, int64_t Hk,
                             int64_t Sq, int64_t Sk, int causal, float scale_log2,
                             const int32_t* counts, const int32_t* indices, const RowLayout& lay,
-                            int nseg, int segk, int64_t dense_qoff, hipStream_t stream);
+                            int nseg, int segk, int64_t dense_qoff, float* stats,
+                            hipStream_t stream);
 }  // namespace va
 
 namespace {
@@ -391,9 +393,11 @@ static int attn_dispatch(int dtype, const void* q, const int64_t* sq, const void
                          int64_t Sk, int64_t D, int64_t qps, int causal,
                          const va::RowLayout& lay, const int32_t* counts,
                          const int32_t* indices, float softmax_scale, int kernel, int nseg,
-                         int64_t segk, hipStream_t stream) {
+                         int64_t segk, hipStream_t stream, float* stats = nullptr) {
   const float scale_log2 = softmax_scale * 1.4426950408889634f;
-  const AttnMfmaCheck chk = attn_mfma_check(dtype, q, sq, k, sk, v, sv, out, so, Sk, D, qps);
+  // Row statistics read no V and write no output: only q and k are checked.
+  const AttnMfmaCheck chk = stats ? attn_mfma_check(dtype, q, sq, k, sk, k, sk, q, sq, Sk, D, qps)
+                                  : attn_mfma_check(dtype, q, sq, k, sk, v, sv, out, so, Sk, D, qps);
   const bool mfma_shape = chk.shape, mfma_align = chk.align, mfma_span = chk.span;
   bool use_mfma = false;
   if (kernel == VA_ATTN_MFMA) {
@@ -417,10 +421,10 @@ static int attn_dispatch(int dtype, const void* q, const int64_t* sq, const void
   hipError_t e = use_mfma
                      ? va::launch_attn_mfma(dtype, D, qps, q, sq, k, sk, v, sv, out, so, B, Hq,
                                             Hk, Sq, Sk, causal, scale_log2, counts, indices, lay,
-                                            nseg, int(segk), -1, stream)
+                                            nseg, int(segk), -1, stats, stream)
                      : va::launch_attn_simple(dtype, q, sq, k, sk, v, sv, out, so, B, Hq, Hk, Sq,
                                               Sk, D, qps, causal, scale_log2, counts, indices,
-                                              lay, stream);
+                                              lay, -1, stats, stream);
   return hip_check(e, "attention launch");
 }
 
@@ -431,9 +435,10 @@ static int sparse_attn_impl(int dtype, const void* q, int64_t sqb, int64_t sqh, 
                             int64_t Sq, int64_t Sk, int64_t D, int64_t qps, int causal,
                             int wo_init, int64_t J0, int64_t nc, int64_t dense_stride,
                             const int32_t* counts, const int32_t* indices, float softmax_scale,
-                            int kernel, int nseg, int64_t segk, void* stream) {
+                            int kernel, int nseg, int64_t segk, void* stream,
+                            float* stats = nullptr) {
   if (!dtype_ok(dtype)) return fail(VA_ERR_ARG, "unknown dtype %d", dtype);
-  if (!q || !k || !v || !out) return fail(VA_ERR_ARG, "null tensor pointer");
+  if (!q || !k || (!stats && (!v || !out))) return fail(VA_ERR_ARG, "null tensor pointer");
   if ((counts == nullptr) != (indices == nullptr))
     return fail(VA_ERR_ARG, "counts and indices must both be given or both be NULL");
   if (B <= 0 || Hq <= 0 || Hk <= 0 || Sq <= 0 || Sk <= 0 || D <= 0 || qps <= 0 || nc <= 0 || J0 < 0)
@@ -448,7 +453,7 @@ static int sparse_attn_impl(int dtype, const void* q, int64_t sqb, int64_t sqh, 
   const va::RowLayout lay = make_layout(J0, nc, qps, Sk, causal, wo_init, dense_stride);
   int rc = attn_dispatch(dtype, q, sq, k, sk, v, sv, out, so, B, Hq, Hk, Sq, Sk, D, qps, causal,
                          lay, counts, indices, softmax_scale, kernel, nseg, segk,
-                         static_cast<hipStream_t>(stream));
+                         static_cast<hipStream_t>(stream), stats);
   return rc ? rc : ok();
 }
 
@@ -492,8 +497,66 @@ int va_dense_attn(int dtype, const void* q, int64_t sqb, int64_t sqh, int64_t sq
   const hipError_t e = va::launch_attn_mfma(
       dtype, D, qps, q, sq, k, sk, v, sv, out, so, B, Hq, Hk, Sq, Sk, causal,
       softmax_scale * 1.4426950408889634f, nullptr, nullptr, lay, 1, 0,
-      causal ? Sk - Sq : 0, static_cast<hipStream_t>(stream));
+      causal ? Sk - Sq : 0, nullptr, static_cast<hipStream_t>(stream));
   const int rc = hip_check(e, "dense attention launch");
+  return rc ? rc : ok();
+}
+
+int va_sparse_row_stats(int dtype, const void* q, int64_t sqb, int64_t sqh, int64_t sqs,
+                        const void* k, int64_t skb, int64_t skh, int64_t sks, int64_t B,
+                        int64_t Hq, int64_t Hk, int64_t Sq, int64_t Sk, int64_t D, int64_t qps,
+                        int causal, int wo_init, int64_t J0, int64_t nc, int64_t dense_stride,
+                        const int32_t* counts, const int32_t* indices, float softmax_scale,
+                        int kernel, float* stats, void* stream) {
+  if (!stats) return fail(VA_ERR_ARG, "null stats");
+  return sparse_attn_impl(dtype, q, sqb, sqh, sqs, k, skb, skh, sks, nullptr, 0, 0, 0, nullptr, 0,
+                          0, 0, B, Hq, Hk, Sq, Sk, D, qps, causal, wo_init, J0, nc, dense_stride,
+                          counts, indices, softmax_scale, kernel, 1, 0, stream, stats);
+}
+
+int va_dense_row_stats(int dtype, const void* q, int64_t sqb, int64_t sqh, int64_t sqs,
+                       const void* k, int64_t skb, int64_t skh, int64_t sks, int64_t B,
+                       int64_t Hq, int64_t Hk, int64_t Sq, int64_t Sk, int64_t D, int causal,
+                       float softmax_scale, int kernel, float* stats, void* stream) {
+  if (!dtype_ok(dtype)) return fail(VA_ERR_ARG, "unknown dtype %d", dtype);
+  if (!q || !k || !stats) return fail(VA_ERR_ARG, "null pointer");
+  if (B <= 0 || Hq <= 0 || Hk <= 0 || Sq <= 0 || Sk <= 0 || D <= 0)
+    return fail(VA_ERR_ARG, "non-positive size");
+  if (Hq % Hk) return fail(VA_ERR_ARG, "num q heads not a multiple of kv heads");
+  if (D > 256) return fail(VA_ERR_UNSUPPORTED, "head_dim %lld > 256", (long long)D);
+  if (causal && Sq > Sk) return fail(VA_ERR_ARG, "causal rows need Sq <= Sk");
+  constexpr int64_t qps = 64;
+  const int64_t nc = cdiv(Sq, qps);
+  if (nc * B * Hq > kMaxGrid) return fail(VA_ERR_UNSUPPORTED, "grid too large");
+  const int64_t sq[3] = {sqb, sqh, sqs}, sk[3] = {skb, skh, sks};
+  const AttnMfmaCheck chk = attn_mfma_check(dtype, q, sq, k, sk, k, sk, q, sq, Sk, D, qps);
+  const bool mfma_ok = chk.ok() && softmax_scale > 0.f;
+  bool use_mfma;
+  if (kernel == VA_ATTN_MFMA) {
+    if (!mfma_ok)
+      return fail(VA_ERR_UNSUPPORTED, "MFMA row statistics need bf16/fp16, D in {64, 128}, "
+                                      "16-byte aligned rows, Sk < 2^24, K row stride < 16 KiB "
+                                      "and a positive softmax scale");
+    use_mfma = true;
+  } else if (kernel == VA_ATTN_AUTO) {
+    use_mfma = mfma_ok;
+  } else if (kernel == VA_ATTN_SIMPLE) {
+    use_mfma = false;
+  } else {
+    return fail(VA_ERR_ARG, "unknown kernel selector %d", kernel);
+  }
+  const va::RowLayout lay = make_layout(0, nc, qps, Sk, causal, 0, 0);
+  const float scale_log2 = softmax_scale * 1.4426950408889634f;
+  const int64_t qoff = causal ? Sk - Sq : 0;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const hipError_t e =
+      use_mfma ? va::launch_attn_mfma(dtype, D, qps, q, sq, k, sk, nullptr, sk, nullptr, sq, B, Hq,
+                                      Hk, Sq, Sk, causal, scale_log2, nullptr, nullptr, lay, 1, 0,
+                                      qoff, stats, st)
+               : va::launch_attn_simple(dtype, q, sq, k, sk, nullptr, sk, nullptr, sq, B, Hq, Hk,
+                                        Sq, Sk, D, qps, causal, scale_log2, nullptr, nullptr, lay,
+                                        qoff, stats, st);
+  const int rc = hip_check(e, "row statistics launch");
   return rc ? rc : ok();
 }
 

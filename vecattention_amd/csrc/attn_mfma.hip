@@ -108,7 +108,12 @@ struct TileInfo {
 // dense_qoff) instead of the local blocks and the selected columns; a
 // separate instantiation, so that the sparse kernel's code does not carry
 // the general key-span arithmetic.
-template <typename T, int D, int QPS, bool kDense>
+// kStats: the row's softmax statistics instead of the attention output: no
+// V copies and no PV products; the row sums add the fp32 probabilities (not
+// their bf16/fp16 roundings), and row i of head bh gets
+// stats[(bh * Sq + i) * 2 + {0, 1}] = (m, l) with l = sum over its keys of
+// 2^(s * scale_log2 - m), s the raw score (m = -inf, l = 0 without keys).
+template <typename T, int D, int QPS, bool kDense, bool kStats>
 __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == kThreads
     const T* __restrict__ q, int64_t sqb, int64_t sqh, int64_t sqs,
     const T* __restrict__ k, int64_t skb, int64_t skh, int64_t sks,
@@ -116,7 +121,7 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
     T* __restrict__ out, int64_t sob, int64_t soh, int64_t sos, int64_t B,
     int64_t Hq, int64_t Hk, int64_t Sq, int64_t Sk, int causal, float scale_log2,
     const int32_t* __restrict__ counts, const int32_t* __restrict__ indices,
-    RowLayout lay, int nseg, int segk, int64_t dense_qoff) {
+    RowLayout lay, int nseg, int segk, int64_t dense_qoff, float* __restrict__ stats) {
   using S = AttnShape<D, QPS>;
   using M = Mfma<T>;
   using vec = typename M::vec;
@@ -392,7 +397,7 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
 #pragma unroll
       for (int i = 0; i < D / 32; ++i)
 #pragma unroll
-        for (int e = 0; e < 16; ++e) o[i][e] *= alpha;
+        for (int e = 0; e < 16; ++e) o[i][e] *= alpha;  // dead code under kStats
       lsum *= alpha;
       mc = mnew;
       const bool none = mnew == -__builtin_inff();
@@ -437,11 +442,15 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
   constexpr int NQK = D / 16;  // QK MFMAs per tile
   f32x16_t s_cur;              // masked scores of tile t
   constexpr int W = S::kWaves;
+  // Copies a wave may leave in flight at a barrier: the K and V copies of the
+  // tiles ahead (K only under kStats, where the copies of tile t+1 are
+  // K(t+1) and K(t+2)).
+  constexpr int kKeep = kStats ? H : 2 * H;
   if (ntiles > 0) {
     if (wave < ntiles) stage_ids(wave, wave);  // tiles 0 .. W-1
     vm_lds_barrier();
     // K(0), K(1), V(0); after QK(0), K(2) into K(0)'s slot.  The loop's
-    // barriers leave the 2H most recent copies of the wave in flight.
+    // barriers leave the kKeep most recent copies of the wave in flight.
     uint64_t pr[H], pr1[H];
     copy_pairs(0, 0, pr);
     copy_pairs(1, 1, pr1);
@@ -449,9 +458,11 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
     for (int x = 0; x < H; ++x) copy_k(smem_lds, x, pr[x]);
 #pragma unroll
     for (int x = 0; x < H; ++x) copy_k(smem_lds + uint32_t(S::kStageBytes), x, pr1[x]);
+    if constexpr (!kStats) {
 #pragma unroll
-    for (int x = 0; x < H; ++x) copy_v(smem_lds + uint32_t(S::kTileBytes), x, pr[x]);
-    vm_lds_barrier_keep<2 * H>();  // K(0) landed
+      for (int x = 0; x < H; ++x) copy_v(smem_lds + uint32_t(S::kTileBytes), x, pr[x]);
+    }
+    vm_lds_barrier_keep<kKeep>();  // K(0) landed
     s_cur = qk(smem);
     mask(0, s_cur);
     float tmax = -__builtin_inff();
@@ -472,7 +483,7 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
     constexpr uint32_t v_this = uint32_t(P * S::kStageBytes + S::kTileBytes);  // V slot of t
     constexpr uint32_t v_next = k_next + uint32_t(S::kTileBytes);      // V slot of t+1
     // ---- first half: QK(t+1) next to the softmax of S(t); copies of V(t+1)
-    vm_lds_barrier_keep<2 * H>();  // K(t+1) landed; every wave is done with PV(t-1)
+    vm_lds_barrier_keep<kKeep>();  // K(t+1) landed; every wave is done with PV(t-1)
     if (P == 0 && t % W == 0) {  // every wave stages one of tiles t+W .. t+2W-1
       const int u = t + W + wave;
       if (u < ntiles) stage_ids(u, u % S::kIdSlots);
@@ -500,7 +511,7 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
       if (st == 0) copy_pairs(t + 1, (t + 1) % S::kIdSlots, cpr);
 #pragma unroll
       for (int c = 0; c < H; ++c)  // copy c goes out after MFMA c * NQK / H
-        if (c * NQK / H == st) copy_v(smem_lds + v_next, c, cpr[c]);
+        if (!kStats && c * NQK / H == st) copy_v(smem_lds + v_next, c, cpr[c]);
       // this step's share of the softmax of S(t)
 #pragma unroll
       for (int e = st * 16 / NQK; e < (st + 1) * 16 / NQK; ++e) {
@@ -509,13 +520,30 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
       }
     }
     __builtin_amdgcn_sched_barrier(0);
-    const vec bfrag[2] = {M::pack(pr), M::pack(pr + 8)};
     mask(t + 1, s_next);
+    if constexpr (kStats) {  // row sums of P(t), maximum of S(t+1), copies of K(t+3)
+      vm_lds_barrier_keep<kKeep>();  // every wave is done with K(t+1)
+      copy_pairs(t + 3, (t + 3) % S::kIdSlots, cpr);
+#pragma unroll
+      for (int c = 0; c < H; ++c) copy_k(smem_lds + k_next, c, cpr[c]);
+      float ps[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ps[e] = pr[e] + pr[e + 8];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) ps[e] += ps[e + 4];
+      lsum += (ps[0] + ps[2]) + (ps[1] + ps[3]);
+      float tmax = -__builtin_inff();
+#pragma unroll
+      for (int e = 0; e < 16; e += 2) tmax = max3_plain(tmax, s_next[e], s_next[e + 1]);
+      rescale(max_halves(tmax));
+      return;
+    }
+    const vec bfrag[2] = {M::pack(pr), M::pack(pr + 8)};
     // ---- second half: PV(t), with the row sums of P(t) and the maximum of
     // S(t+1) spread over its MFMAs (in-order issue: VALU work placed between
     // the MFMAs runs while they execute); copies of K(t+3) into the slot QK
     // just read
-    vm_lds_barrier_keep<2 * H>();  // V(t) landed; every wave is done with K(t+1)
+    vm_lds_barrier_keep<kKeep>();  // V(t) landed; every wave is done with K(t+1)
 #pragma unroll
     for (int f = 0; f < kVAhead; ++f) vf[f] = read_v(vb, f);
     copy_pairs(t + 3, (t + 3) % S::kIdSlots, cpr);
@@ -547,6 +575,23 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
   // ---- merge the two key halves, normalise, store --------------------------
   vm_lds_barrier();  // every wave is done with the stages, the last copies have landed
   float* mo = reinterpret_cast<float*>(smem) + rh * 64 * (D / 2 + 2);
+  if constexpr (kStats) {
+    const float lrow = sum_halves(lsum);
+    if (kc == 1) {
+      mo[lane] = mc;
+      mo[64 + lane] = lrow;
+    }
+    lds_barrier();
+    if (kc == 0 && hh == 0 && qpos < Sq) {
+      const float m1 = mo[lane], l1 = mo[64 + lane];
+      const float m = __builtin_fmaxf(mc, m1);
+      const float a0 = (mc == m) ? 1.f : __builtin_amdgcn_exp2f(mc - m);
+      const float a1 = (m1 == m) ? 1.f : __builtin_amdgcn_exp2f(m1 - m);
+      *reinterpret_cast<float2*>(stats + (bh * Sq + qpos) * 2) =
+          make_float2(m, lrow * a0 + l1 * a1);
+    }
+    return;
+  }
   if (kc == 1) {
 #pragma unroll
     for (int i = 0; i < D / 32; ++i)
@@ -591,6 +636,29 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
   }
 }
 
+template <typename T, int D, int QPS, bool kDense, bool kStats>
+static hipError_t launch_attn_mfma_k(const void* q, const int64_t* sq, const void* k,
+                                     const int64_t* sk, const void* v, const int64_t* sv,
+                                     void* out, const int64_t* so, int64_t B, int64_t Hq,
+                                     int64_t Hk, int64_t Sq, int64_t Sk, int causal,
+                                     float scale_log2, const int32_t* counts,
+                                     const int32_t* indices, const RowLayout& lay, int nseg,
+                                     int segk, int64_t dense_qoff, float* stats,
+                                     hipStream_t stream) {
+  static const int64_t zero[3] = {0, 0, 0};
+  if (kStats) sv = so = zero;  // no V, no output
+  const int64_t nblocks = WorkOrder{lay.nc, B, Hq, Hk, causal == 0}.grid_items();
+  hipLaunchKernelGGL((attn_mfma_kernel<T, D, QPS, kDense, kStats>), dim3(unsigned(nblocks)),
+                     dim3(AttnShape<D, QPS>::kThreads), 0, stream, static_cast<const T*>(q),
+                     sq[0], sq[1], sq[2], static_cast<const T*>(k), sk[0], sk[1], sk[2],
+                     static_cast<const T*>(v), sv[0], sv[1], sv[2], static_cast<T*>(out), so[0],
+                     so[1], so[2], B, Hq, Hk, Sq, Sk, causal, scale_log2, counts, indices, lay,
+                     nseg, segk, kDense ? dense_qoff : 0, stats);
+  return hipGetLastError();
+}
+
+// dense_qoff >= 0: dense key lists (64-row blocks only); stats != nullptr: the
+// row statistics instead of the output.
 template <typename T, int D, int QPS>
 static hipError_t launch_attn_mfma_tdq(const void* q, const int64_t* sq, const void* k,
                                        const int64_t* sk, const void* v, const int64_t* sv,
@@ -598,27 +666,23 @@ static hipError_t launch_attn_mfma_tdq(const void* q, const int64_t* sq, const v
                                        int64_t Hk, int64_t Sq, int64_t Sk, int causal,
                                        float scale_log2, const int32_t* counts,
                                        const int32_t* indices, const RowLayout& lay, int nseg,
-                                       int segk, int64_t dense_qoff, hipStream_t stream) {
-  const int64_t nblocks = WorkOrder{lay.nc, B, Hq, Hk, causal == 0}.grid_items();
+                                       int segk, int64_t dense_qoff, float* stats,
+                                       hipStream_t stream) {
+#define VA_ATTN_LAUNCH(DENSE, STATS)                                                           \
+  return launch_attn_mfma_k<T, D, QPS, DENSE, STATS>(q, sq, k, sk, v, sv, out, so, B, Hq, Hk,  \
+                                                     Sq, Sk, causal, scale_log2, counts,      \
+                                                     indices, lay, nseg, segk, dense_qoff,    \
+                                                     stats, stream)
   if (dense_qoff >= 0) {
-    if constexpr (QPS == 64) {  // dense attention runs on 64-row blocks
-      hipLaunchKernelGGL((attn_mfma_kernel<T, D, QPS, true>), dim3(unsigned(nblocks)),
-                         dim3(AttnShape<D, QPS>::kThreads), 0, stream, static_cast<const T*>(q),
-                         sq[0], sq[1], sq[2], static_cast<const T*>(k), sk[0], sk[1], sk[2],
-                         static_cast<const T*>(v), sv[0], sv[1], sv[2], static_cast<T*>(out),
-                         so[0], so[1], so[2], B, Hq, Hk, Sq, Sk, causal, scale_log2, counts,
-                         indices, lay, nseg, segk, dense_qoff);
-      return hipGetLastError();
+    if constexpr (QPS == 64) {
+      if (stats) VA_ATTN_LAUNCH(true, true);
+      VA_ATTN_LAUNCH(true, false);
     }
     return hipErrorInvalidValue;
   }
-  hipLaunchKernelGGL((attn_mfma_kernel<T, D, QPS, false>), dim3(unsigned(nblocks)),
-                     dim3(AttnShape<D, QPS>::kThreads), 0,
-                     stream, static_cast<const T*>(q), sq[0], sq[1], sq[2],
-                     static_cast<const T*>(k), sk[0], sk[1], sk[2], static_cast<const T*>(v),
-                     sv[0], sv[1], sv[2], static_cast<T*>(out), so[0], so[1], so[2], B, Hq, Hk,
-                     Sq, Sk, causal, scale_log2, counts, indices, lay, nseg, segk, 0);
-  return hipGetLastError();
+  if (stats) VA_ATTN_LAUNCH(false, true);
+  VA_ATTN_LAUNCH(false, false);
+#undef VA_ATTN_LAUNCH
 }
 
 template <typename T>
@@ -628,12 +692,13 @@ static hipError_t launch_attn_mfma_t(int64_t D, int64_t qps, const void* q, cons
                                      int64_t Hq, int64_t Hk, int64_t Sq, int64_t Sk, int causal,
                                      float scale_log2, const int32_t* counts,
                                      const int32_t* indices, const RowLayout& lay, int nseg,
-                                     int segk, int64_t dense_qoff, hipStream_t stream) {
+                                     int segk, int64_t dense_qoff, float* stats,
+                                     hipStream_t stream) {
 #define VA_ATTN_CASE(DD, QQ)                                                                   \
   if (D == DD && qps == QQ)                                                                    \
     return launch_attn_mfma_tdq<T, DD, QQ>(q, sq, k, sk, v, sv, out, so, B, Hq, Hk, Sq, Sk,   \
                                            causal, scale_log2, counts, indices, lay, nseg,    \
-                                           segk, dense_qoff, stream);
+                                           segk, dense_qoff, stats, stream);
   VA_ATTN_CASE(64, 64)
   VA_ATTN_CASE(128, 64)
   VA_ATTN_CASE(64, 128)
@@ -651,15 +716,16 @@ hipError_t launch_attn_mfma(int dtype, int64_t D, int64_t qps, const void* q, co
                             void* out, const int64_t* so, int64_t B, int64_t Hq, int64_t Hk,
                             int64_t Sq, int64_t Sk, int causal, float scale_log2,
                             const int32_t* counts, const int32_t* indices, const RowLayout& lay,
-                            int nseg, int segk, int64_t dense_qoff, hipStream_t stream) {
+                            int nseg, int segk, int64_t dense_qoff, float* stats,
+                            hipStream_t stream) {
   if (dtype == kBF16)
     return launch_attn_mfma_t<bf16_t>(D, qps, q, sq, k, sk, v, sv, out, so, B, Hq, Hk, Sq, Sk,
                                       causal, scale_log2, counts, indices, lay, nseg, segk,
-                                      dense_qoff, stream);
+                                      dense_qoff, stats, stream);
   if (dtype == kF16)
     return launch_attn_mfma_t<f16_t>(D, qps, q, sq, k, sk, v, sv, out, so, B, Hq, Hk, Sq, Sk,
                                      causal, scale_log2, counts, indices, lay, nseg, segk,
-                                     dense_qoff, stream);
+                                     dense_qoff, stats, stream);
   return hipErrorInvalidValue;
 }
 

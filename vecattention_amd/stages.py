@@ -209,6 +209,60 @@ def dense_attention(q, k, v, out=None, causal=True, softmax_scale=None):
     return out
 
 
+def _stats_out(stats, B, Hq, Sq, device):
+    if stats is None:
+        return torch.empty(B, Hq, Sq, 2, dtype=torch.float32, device=device)
+    if stats.dtype != torch.float32 or tuple(stats.shape) != (B, Hq, Sq, 2) or not stats.is_contiguous():
+        raise AssertionError(f"stats must be a contiguous float32 ({B}, {Hq}, {Sq}, 2) tensor")
+    return stats
+
+
+def dense_row_stats(q, k, causal, softmax_scale=None, kernel=nat.VA_ATTN_AUTO, stats=None):
+    """Softmax statistics of every query row over every key (va_dense_row_stats).
+
+    Returns stats (B, Hq, Sq, 2) float32: (m, l) with l = sum_j 2^(s_ij - m),
+    s_ij = q_i.k_j * scale * log2(e); causal rows see keys <= i + Sk - Sq.
+    """
+    q = q if q.stride(-1) == 1 else q.contiguous()
+    k = k if k.stride(-1) == 1 else k.contiguous()
+    B, Hq, Sq, D = q.shape
+    Hk, Sk = k.shape[1], k.shape[2]
+    stats = _stats_out(stats, B, Hq, Sq, q.device)
+    if softmax_scale is None:
+        softmax_scale = 1.0 / math.sqrt(D)
+    with torch.cuda.device(q.device):
+        rc = nat.lib().va_dense_row_stats(
+            nat.dtype_code(q), nat.ptr(q), q.stride(0), q.stride(1), q.stride(2), nat.ptr(k),
+            k.stride(0), k.stride(1), k.stride(2), B, Hq, Hk, Sq, Sk, D, int(causal),
+            float(softmax_scale), int(kernel), nat.ptr(stats), _stream(q))
+    nat.check("va_dense_row_stats", rc)
+    return stats
+
+
+def sparse_row_stats(q, k, J0, nc, counts, indices, causal, q_pooling_size, wo_init=None,
+                     dense_stride=0, softmax_scale=None, kernel=nat.VA_ATTN_AUTO, stats=None):
+    """Softmax statistics of the rows of q-blocks [J0, J0+nc) over their
+    vector-sparse key sets (va_sparse_row_stats); other rows of `stats` are
+    left as they are.  Same (m, l) convention as dense_row_stats."""
+    q = q if q.stride(-1) == 1 else q.contiguous()
+    k = k if k.stride(-1) == 1 else k.contiguous()
+    B, Hq, Sq, D = q.shape
+    Hk, Sk = k.shape[1], k.shape[2]
+    stats = _stats_out(stats, B, Hq, Sq, q.device)
+    if wo_init is None:
+        wo_init = causal
+    if softmax_scale is None:
+        softmax_scale = 1.0 / math.sqrt(D)
+    with torch.cuda.device(q.device):
+        rc = nat.lib().va_sparse_row_stats(
+            nat.dtype_code(q), nat.ptr(q), q.stride(0), q.stride(1), q.stride(2), nat.ptr(k),
+            k.stride(0), k.stride(1), k.stride(2), B, Hq, Hk, Sq, Sk, D, q_pooling_size,
+            int(causal), int(wo_init), J0, nc, dense_stride, nat.ptr(counts), nat.ptr(indices),
+            float(softmax_scale), int(kernel), nat.ptr(stats), _stream(q))
+    nat.check("va_sparse_row_stats", rc)
+    return stats
+
+
 def fuse_qk_softmax_minp_wo_causal(
     avg_q_chunk,
     k,
@@ -254,5 +308,5 @@ def fuse_qk_softmax_minp_wo_causal(
 __all__ = [
     "average_vector", "fuse_qk_softmax_minp_wo_causal", "pool_scaled", "select_rows",
     "sparse_attention", "index_capacity", "row_offset", "threshold_to_gap", "segment_keys",
-    "select_segments",
+    "select_segments", "dense_row_stats", "sparse_row_stats",
 ]
