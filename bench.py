@@ -46,6 +46,9 @@ def parse():
     ap.add_argument("--extra-json", default=None, help="append the result line to this file too")
     ap.add_argument("--threshold", type=float, default=None,
                     help="use this threshold instead of calibrating one to the keep ratio")
+    ap.add_argument("--decode", type=int, default=None, metavar="L",
+                    help="time decode attention (single_decode_with_kv_cache) over a KV cache "
+                         "of L tokens with the workload's heads instead of the prefill")
     ap.add_argument("--tuner", action="store_true",
                     help="time the threshold tuner's recall/sparsity evaluation "
                          "(seg_pr_perHead) on the workload's shapes instead of the prefill")
@@ -376,6 +379,78 @@ def bench_tuner(args, wl, dev):
             f.write(line + "\n")
 
 
+# ------------------------------------------------------------------- decode --
+
+def bench_decode(args, wl, dev):
+    """Decode attention of one token over an L-token KV cache with the
+    workload's heads (q (Hq, D), K/V NHD (L, Hk, D), bf16), as the reference's
+    decode branch calls flashinfer (load_qwen2p5_vl.py:61-66), but on the
+    unexpanded kv heads.  HBM roofline: K and V are read once (2 * L * Hk * D
+    elements); q and the output are negligible.  Baseline: torch SDPA
+    (enable_gqa) on the same GPU and tensors."""
+    from vecattention_amd.decode import single_decode_with_kv_cache
+    L, Hq, Hk, D = args.decode, wl.Hq, wl.Hk, wl.D
+    g = torch.Generator().manual_seed(0)
+    q = torch.randn(Hq, D, generator=g).to(wl.dtype).to(dev)
+    k = torch.randn(L, Hk, D, generator=g).to(wl.dtype).to(dev)
+    v = torch.randn(L, Hk, D, generator=g).to(wl.dtype).to(dev)
+    esz = torch.tensor([], dtype=wl.dtype).element_size()
+    kv_bytes = 2 * L * Hk * D * esz
+
+    def timed(fn, reps, warm):
+        for _ in range(warm):
+            fn()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(reps):
+            fn()
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / reps
+
+    call = lambda: single_decode_with_kv_cache(q, k, v, kv_layout="NHD")  # noqa: E731
+    steps = max(args.steps, 1) * 20
+    ms = timed(call, steps, max(args.warmup, 1) * 5)
+    gbs = kv_bytes / (ms * 1e-3) / 1e9
+    print(f"[bench] decode L={L}: {ms * 1e3:.1f} us per call, {gbs:.0f} GB/s", file=sys.stderr,
+          flush=True)
+    qs, ks, vs = q[None, :, None, :], k.permute(1, 0, 2)[None], v.permute(1, 0, 2)[None]
+    sdpa_ms = None
+    try:
+        sdpa = lambda: torch.nn.functional.scaled_dot_product_attention(  # noqa: E731
+            qs, ks, vs, enable_gqa=True)
+        sdpa_ms = timed(sdpa, steps, 5)
+    except RuntimeError as e:
+        print(f"[bench] SDPA unavailable: {str(e)[:80]}", file=sys.stderr, flush=True)
+    result = {
+        "metric": "decode attention latency (us)",
+        "value": round(ms * 1e3, 2),
+        "unit": "us",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": max(args.warmup, 1) * 5,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": {torch.bfloat16: "bf16", torch.float16: "fp16"}.get(wl.dtype, "fp32"),
+        "data": "synthetic (seeded N(0,1) q, K and V)",
+        "config": {"workload": f"decode-{wl.name}-L{L}", "Hq": Hq, "Hk": Hk, "D": D, "L": L,
+                   "kv_layout": "NHD"},
+        "sdpa_us": None if sdpa_ms is None else round(sdpa_ms * 1e3, 2),
+        "speedup_vs_sdpa": None if sdpa_ms is None else round(sdpa_ms / ms, 2),
+        "roofline": {"bound": "hbm", "kernel": "attn_mfma_kernel (split form) + decode_merge_kernel",
+                     "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+    }
+    line = json.dumps(result)
+    print(line, flush=True)
+    if args.extra_json:
+        with open(args.extra_json, "a") as f:
+            f.write(line + "\n")
+
+
 # --------------------------------------------------------------------- main --
 
 def main():
@@ -392,6 +467,9 @@ def main():
     dev = torch.device("cuda:0")
     if args.tuner:
         bench_tuner(args, wl, dev)
+        return
+    if args.decode:
+        bench_decode(args, wl, dev)
         return
     t_gen = time.perf_counter()
     q_cpu, k_cpu, v_cpu = workload_inputs(wl, seed=0)

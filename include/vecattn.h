@@ -39,7 +39,7 @@ enum {
   VA_ERR_ARG = -1,          /* invalid argument (mirrors the reference's asserts) */
   VA_ERR_UNSUPPORTED = -2,  /* valid for the reference, not handled by this build */
   VA_ERR_HIP = -3,          /* a HIP runtime call failed (no device, launch error) */
-  VA_ERR_WORKSPACE = -4     /* workspace smaller than va_prefill_workspace_size() */
+  VA_ERR_WORKSPACE = -4     /* workspace smaller than its *_workspace_size() query */
 };
 
 enum { VA_ATTN_AUTO = 0, VA_ATTN_MFMA = 1, VA_ATTN_SIMPLE = 2 };
@@ -210,6 +210,25 @@ int va_dense_row_stats(int dtype, const void* q, int64_t sqb, int64_t sqh, int64
                        const void* k, int64_t skb, int64_t skh, int64_t sks, int64_t B,
                        int64_t Hq, int64_t Hk, int64_t Sq, int64_t Sk, int64_t D, int causal,
                        float softmax_scale, int kernel, float* stats, void* stream);
+
+/*
+ * Decode attention: one query row per q head over the whole KV cache of its kv
+ * head, no mask.  Replaces flashinfer.single_decode_with_kv_cache as called at
+ * spattn/src/models/load_qwen2p5_vl.py:61-66 (kv_layout "NHD") and
+ * spattn/src/models/load_llama.py:183-188 (kv_layout "HND"): out[h] =
+ * softmax(q[h] . K[:, h / (Hq/Hk)]^T * softmax_scale) V[:, h / (Hq/Hk)].
+ * q: (Hq, D) with head stride sqh; K/V element (n, h, d) at base + h*skh +
+ * n*sks + d (NHD: skh = D, sks = Hk*D; HND: skh = L*D, sks = D); out: (Hq, D)
+ * with head stride soh, q's dtype.  The MFMA path (bf16/fp16, D in {64, 128},
+ * Hq/Hk <= 64) splits each kv head's L keys over work-groups and merges their
+ * partial softmax states; it needs `workspace` of va_decode_workspace_size()
+ * bytes (16-byte aligned).  VA_ATTN_SIMPLE (any dtype) needs none.
+ */
+int64_t va_decode_workspace_size(int64_t Hq, int64_t Hk, int64_t L, int64_t D);
+int va_decode_attn(int dtype, const void* q, int64_t sqh, const void* k, int64_t skh,
+                   int64_t sks, const void* v, int64_t svh, int64_t svs, void* out, int64_t soh,
+                   int64_t Hq, int64_t Hk, int64_t L, int64_t D, float softmax_scale, int kernel,
+                   void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
  * va_sparse_attn on the segmented lists of va_select_segments (counts of shape

@@ -15,6 +15,10 @@ Pieces and the reference lines they restate:
                       clipped to S_k, union selected columns, causal mask,
                       softmax scale 1/sqrt(D)); an empty key set gives 0
   prefill             spattn/src/VecAttention.py:43-123 (gap, chunk loop)
+  decode              flashinfer.single_decode_with_kv_cache as called at
+                      spattn/src/models/load_qwen2p5_vl.py:61-66 (NHD) and
+                      spattn/src/models/load_llama.py:183-188 (HND): one
+                      query row per head, softmax over every cached key
   seg_pr_perhead      spattn/threshold/model_tuner.py:118-226 (the tuner's
                       recall / sparsity evaluation: dense softmax per head,
                       boolean mask of local blocks and selected columns)
@@ -291,3 +295,25 @@ def seg_pr_perhead(q, k, block_size_q, block_size_k=16, group_size_k=16, thresho
     sparsity /= B
     sparsity /= S
     return recalls.sum(axis=(0, 2)) / (B * S), sparsity
+
+
+def decode(q, k, v, kv_layout="NHD", sm_scale=None):
+    """(Hq, D) float64: out[h] = softmax(q[h] . K_g^T * sm_scale) V_g with
+    g = h // (Hq / Hk), every key visible (flashinfer-python 0.5.2
+    single_decode_with_kv_cache semantics: default sm_scale 1/sqrt(D), GQA
+    by integer division of the head index)."""
+    q = as_f32(q).astype(np.float64)
+    k = as_f32(k).astype(np.float64)
+    v = as_f32(v).astype(np.float64)
+    if kv_layout == "NHD":
+        k, v = k.transpose(1, 0, 2), v.transpose(1, 0, 2)
+    Hq, D = q.shape
+    Hk = k.shape[0]
+    scale = 1.0 / math.sqrt(D) if sm_scale is None else float(sm_scale)
+    out = np.zeros((Hq, D))
+    for h in range(Hq):
+        g = h // (Hq // Hk)
+        s = (k[g] @ q[h]) * scale
+        p = np.exp(s - s.max())
+        out[h] = (p @ v[g]) / p.sum()
+    return out

@@ -165,3 +165,27 @@ def test_row_stats_argument_errors_before_launch(L):
     assert _sparse_stats(L, Sq=300) == nat.VA_ERR_UNSUPPORTED   # causal needs Sq == Sk
     assert _sparse_stats(L, nc=5) == nat.VA_ERR_ARG             # rows past the q-blocks
     assert _sparse_stats(L, dtype=nat.VA_F32) == nat.VA_ERR_UNSUPPORTED
+
+
+def _decode(lib, **over):
+    args = dict(dtype=nat.VA_BF16, q=256, sqh=128, k=256, skh=128, sks=512, v=256, svh=128,
+                svs=512, out=256, soh=128, Hq=28, Hk=4, L=1000, D=128, scale=0.088,
+                kernel=nat.VA_ATTN_MFMA, ws=256, ws_bytes=1 << 30, stream=None)
+    args.update(over)
+    return lib.va_decode_attn(*args.values())
+
+
+def test_decode_argument_errors_before_launch(L):
+    assert L.va_decode_workspace_size(28, 3, 1000, 128) == -1
+    need = L.va_decode_workspace_size(28, 4, 1000, 128)
+    assert need > 0 and need % 256 == 0
+    assert _decode(L, q=None) == nat.VA_ERR_ARG
+    assert _decode(L, Hk=3) == nat.VA_ERR_ARG
+    assert _decode(L, L=0) == nat.VA_ERR_ARG
+    assert _decode(L, dtype=nat.VA_F32) == nat.VA_ERR_UNSUPPORTED   # MFMA asked for fp32
+    assert _decode(L, D=96, sqh=96, skh=96, svh=96, soh=96) == nat.VA_ERR_UNSUPPORTED
+    assert _decode(L, Hq=4 * 65, Hk=4) == nat.VA_ERR_UNSUPPORTED    # > 64 q heads per kv head
+    assert _decode(L, sks=1 << 14) == nat.VA_ERR_UNSUPPORTED        # row stride past 14 bits
+    assert _decode(L, ws=None) == nat.VA_ERR_WORKSPACE
+    assert _decode(L, ws_bytes=need - 256) == nat.VA_ERR_WORKSPACE
+    assert _decode(L, kernel=9) == nat.VA_ERR_ARG

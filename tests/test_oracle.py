@@ -320,3 +320,41 @@ def test_attention_empty_key_set_is_zero():
     cnt, idx = orc.local_blocks(B, H, S, 64, False)
     out = orc.attention(q, q, q, 64, False, cnt, idx, [[[np.zeros(0, np.int64)]]])
     assert np.all(out == 0)
+
+
+# ---- decode (flashinfer single_decode_with_kv_cache semantics) ----
+
+@pytest.mark.parametrize("layout", ["NHD", "HND"])
+def test_decode_matches_sdpa_float64(layout):
+    """Against torch's SDPA in float64 with the kv heads expanded
+    (repeat_interleave, the repeat_kv convention) and one query row per head."""
+    import torch
+    g = torch.Generator().manual_seed(5)
+    Hq, Hk, L, D = 8, 2, 77, 32
+    q = torch.randn(Hq, D, generator=g).double()  # fp32 values: the oracle reads fp32
+    k = torch.randn(Hk, L, D, generator=g).double()
+    v = torch.randn(Hk, L, D, generator=g).double()
+    kk = k.repeat_interleave(Hq // Hk, dim=0)
+    vv = v.repeat_interleave(Hq // Hk, dim=0)
+    want = torch.nn.functional.scaled_dot_product_attention(
+        q[:, None, :], kk, vv, scale=0.3)[:, 0, :].numpy()
+    kl, vl = (k.transpose(0, 1), v.transpose(0, 1)) if layout == "NHD" else (k, v)
+    got = orc.decode(q.numpy(), kl.numpy(), vl.numpy(), layout, sm_scale=0.3)
+    np.testing.assert_allclose(got, want, rtol=1e-12, atol=1e-12)
+
+
+def test_decode_closed_forms():
+    """One key: the output is that key's value row.  Equal keys: the mean of
+    the value rows."""
+    rng = np.random.default_rng(6)
+    f32 = lambda *shape: rng.standard_normal(shape).astype(np.float32)  # noqa: E731
+    q = f32(4, 16)
+    v1 = f32(1, 2, 16)
+    k1 = f32(1, 2, 16)
+    out = orc.decode(q, k1, v1, "NHD")
+    np.testing.assert_allclose(out, np.repeat(v1[0], 2, axis=0), rtol=1e-12)
+    kq = np.repeat(f32(1, 1, 16), 9, axis=0)
+    vq = f32(9, 1, 16)
+    out = orc.decode(q, kq, vq, "NHD")
+    np.testing.assert_allclose(out, np.repeat(vq[:, 0].astype(np.float64).mean(0, keepdims=True),
+                                              4, axis=0), rtol=1e-12)

@@ -8,6 +8,7 @@ from .stages import average_vector, fuse_qk_softmax_minp_wo_causal
 from .dispatch import (DiffusionStepContext, FastPrefillConfig, Full_prefill,
                        customize_prefill_attention, select_cfg_threshold)
 from .tuner import seg_pr_perHead
+from .decode import single_decode_with_kv_cache
 
 __all__ = [
     "VecAttention_prefill",
@@ -20,4 +21,5 @@ __all__ = [
     "DiffusionStepContext",
     "select_cfg_threshold",
     "seg_pr_perHead",
+    "single_decode_with_kv_cache",
 ]

@@ -56,6 +56,13 @@ hipError_t launch_attn_mfma(int dtype, int64_t D, int64_t qps, const void* q, co
                             const int32_t* counts, const int32_t* indices, const RowLayout& lay,
                             int nseg, int segk, int64_t dense_qoff, float* stats,
                             hipStream_t stream);
+hipError_t launch_attn_split(int dtype, int64_t D, const void* q, const int64_t* sq,
+                             const void* k, const int64_t* sk, const void* v, const int64_t* sv,
+                             int64_t B, int64_t H, int64_t Sq, int64_t Sk, float scale_log2,
+                             int64_t nsplit, int64_t span, float* part, hipStream_t stream);
+hipError_t launch_decode_merge(int dtype, int64_t D, const float* part, int64_t G, int64_t Sq,
+                               int64_t nsplit, void* out, int64_t sog, int64_t sor,
+                               hipStream_t stream);
 }  // namespace va
 
 namespace {
@@ -576,6 +583,83 @@ int va_sparse_attn_segments(int dtype, const void* q, int64_t sqb, int64_t sqh, 
                           soh, sos, B, Hq, Hk, Sq, Sk, D, qps, causal, wo_init, J0, nc,
                           dense_stride, counts, indices, softmax_scale, VA_ATTN_MFMA,
                           int(cdiv(Sk, segment_keys)), segment_keys, stream);
+}
+
+// Decode: the kv cache of each kv head is cut into nsplit ranges of `span`
+// keys (a multiple of the 64-key tile, at least 4 tiles), enough ranges for
+// about two work-groups per CU over all kv heads.
+static void decode_split(int64_t L, int64_t Hk, int64_t* nsplit, int64_t* span) {
+  constexpr int64_t kTargetGroups = 512;
+  const int64_t n = cdiv(kTargetGroups, Hk);
+  int64_t sp = cdiv(cdiv(L, n), 64) * 64;
+  if (sp < 256) sp = 256;
+  *span = sp;
+  *nsplit = cdiv(L, sp);
+}
+
+int64_t va_decode_workspace_size(int64_t Hq, int64_t Hk, int64_t L, int64_t D) {
+  if (Hq <= 0 || Hk <= 0 || L <= 0 || D <= 0 || Hq % Hk) return -1;
+  int64_t nsplit, span;
+  decode_split(L, Hk, &nsplit, &span);
+  return align256(((2 * Hq * nsplit + 3) / 4 * 4 + Hq * nsplit * D) * 4);
+}
+
+int va_decode_attn(int dtype, const void* q, int64_t sqh, const void* k, int64_t skh,
+                   int64_t sks, const void* v, int64_t svh, int64_t svs, void* out, int64_t soh,
+                   int64_t Hq, int64_t Hk, int64_t L, int64_t D, float softmax_scale, int kernel,
+                   void* workspace, int64_t workspace_bytes, void* stream) {
+  if (!dtype_ok(dtype)) return fail(VA_ERR_ARG, "unknown dtype %d", dtype);
+  if (!q || !k || !v || !out) return fail(VA_ERR_ARG, "null tensor pointer");
+  if (Hq <= 0 || Hk <= 0 || L <= 0 || D <= 0) return fail(VA_ERR_ARG, "non-positive size");
+  if (Hq % Hk) return fail(VA_ERR_ARG, "num q heads not a multiple of kv heads");
+  if (D > 256) return fail(VA_ERR_UNSUPPORTED, "head_dim %lld > 256", (long long)D);
+  const int64_t rep = Hq / Hk;
+  // The query heads of kv head h are the rows of one group: q row r of group h
+  // is q head h*rep + r.
+  const int64_t sq[3] = {0, rep * sqh, sqh}, sk[3] = {0, skh, sks}, sv[3] = {0, svh, svs},
+                so[3] = {0, rep * soh, soh};
+  const AttnMfmaCheck chk = attn_mfma_check(dtype, q, sq, k, sk, v, sv, out, so, L, D, 64);
+  const bool mfma_ok = chk.ok() && rep <= 64 && softmax_scale > 0.f;
+  bool use_mfma;
+  if (kernel == VA_ATTN_MFMA) {
+    if (!mfma_ok)
+      return fail(VA_ERR_UNSUPPORTED, "MFMA decode needs bf16/fp16, D in {64, 128}, at most 64 "
+                                      "q heads per kv head, 16-byte aligned rows, L < 2^24, "
+                                      "K/V row strides < 16 KiB and a positive softmax scale");
+    use_mfma = true;
+  } else if (kernel == VA_ATTN_AUTO) {
+    use_mfma = mfma_ok;
+  } else if (kernel == VA_ATTN_SIMPLE) {
+    use_mfma = false;
+  } else {
+    return fail(VA_ERR_ARG, "unknown kernel selector %d", kernel);
+  }
+  const float scale_log2 = softmax_scale * 1.4426950408889634f;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (!use_mfma) {
+    if (rep > 1024) return fail(VA_ERR_UNSUPPORTED, "more than 1024 q heads per kv head");
+    const va::RowLayout lay = make_layout(0, 1, rep, L, 0, 0, 0);
+    const int rc = hip_check(va::launch_attn_simple(dtype, q, sq, k, sk, v, sv, out, so, 1, Hk, Hk,
+                                                    rep, L, D, rep, 0, scale_log2, nullptr,
+                                                    nullptr, lay, 0, nullptr, st),
+                             "decode launch");
+    return rc ? rc : ok();
+  }
+  int64_t nsplit, span;
+  decode_split(L, Hk, &nsplit, &span);
+  const int64_t need = va_decode_workspace_size(Hq, Hk, L, D);
+  if (!workspace || workspace_bytes < need)
+    return fail(VA_ERR_WORKSPACE, "decode needs %lld workspace bytes", (long long)need);
+  if (reinterpret_cast<uintptr_t>(workspace) % 16)
+    return fail(VA_ERR_ARG, "workspace must be 16-byte aligned");
+  float* part = static_cast<float*>(workspace);
+  int rc = hip_check(va::launch_attn_split(dtype, D, q, sq, k, sk, v, sv, 1, Hk, rep, L,
+                                           scale_log2, nsplit, span, part, st),
+                     "decode split launch");
+  if (rc) return rc;
+  rc = hip_check(va::launch_decode_merge(dtype, D, part, Hk, rep, nsplit, out, rep * soh, soh, st),
+                 "decode merge launch");
+  return rc ? rc : ok();
 }
 
 // Workspace of va_prefill: [scaled pooled q][counts][indices][key norms]

@@ -113,7 +113,15 @@ struct TileInfo {
 // their bf16/fp16 roundings), and row i of head bh gets
 // stats[(bh * Sq + i) * 2 + {0, 1}] = (m, l) with l = sum over its keys of
 // 2^(s * scale_log2 - m), s the raw score (m = -inf, l = 0 without keys).
-template <typename T, int D, int QPS, bool kDense, bool kStats>
+// kSplit: split key ranges (decode): block row J holds keys [J*span,
+// (J+1)*span) of the K/V rows, span passed in dense_qoff, for the same query
+// rows [0, Sq) in every J (no causal mask); each (bh, J) writes its rows'
+// normalised partial output and (m, l) in fp32 to stats, row-major over
+// (bh, i, J) so that the partials of one row are contiguous: (m, l) of row i
+// at stats[((bh * Sq + i) * nc + J) * 2], the output after all of them (from
+// the next multiple of 4 floats, P = ceil(2 * B * Hq * nc * Sq / 4) * 4), at
+// stats + P + ((bh * Sq + i) * nc + J) * D.
+template <typename T, int D, int QPS, bool kDense, bool kStats, bool kSplit>
 __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == kThreads
     const T* __restrict__ q, int64_t sqb, int64_t sqh, int64_t sqs,
     const T* __restrict__ k, int64_t skb, int64_t skh, int64_t sks,
@@ -146,7 +154,7 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
   // ---- Q^T operand: lane holds row 32rh + l32, features [16s + 8hh, +8) ----
   // (loads issued first; their latency overlaps the list bookkeeping below)
   const int qrow_local = 32 * rh + l32;
-  const int64_t qpos = J * QPS + qrow_local;
+  const int64_t qpos = (kSplit ? 0 : J * QPS) + qrow_local;
   vec qreg[D / 16];
   {
     const T* qr_ptr = q + b * sqb + h * sqh + qpos * sqs;
@@ -190,7 +198,9 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
   if (cnt > cap) cnt = cap;
   const int32_t* cols = indices ? indices + lay.row_offset(bh, jr) : nullptr;
   KeyList kl;
-  if constexpr (kDense)
+  if constexpr (kSplit)
+    kl = KeyList::split(J, dense_qoff, Sk);
+  else if constexpr (kDense)
     kl = KeyList::dense(J, QPS, Sk, causal, dense_qoff);
   else
     kl = KeyList::make(J, QPS, Sk, causal, cnt, cols);
@@ -614,6 +624,25 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
     const float l = lrow * a0 + l1 * a1;
     const float inv = l > 0.f ? 1.f / l : 0.f;
     const float c0 = a0 * inv, c1 = a1 * inv;
+    if constexpr (kSplit) {  // fp32 partial output and (m, l) of this key range
+      if (qpos < Sq) {
+        const int64_t item = (bh * Sq + qpos) * lay.nc + jr;
+        float* po = stats + (2 * B * Hq * lay.nc * Sq + 3) / 4 * 4 + item * D;
+#pragma unroll
+        for (int i = 0; i < D / 32; ++i) {
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const float4 x1 = *reinterpret_cast<const float4*>(mo + ((4 * i + g) * 64 + lane) * 4);
+            const int d0 = i * 32 + 8 * g + 4 * hh;
+            *reinterpret_cast<float4*>(po + d0) = make_float4(
+                o[i][4 * g + 0] * c0 + x1.x * c1, o[i][4 * g + 1] * c0 + x1.y * c1,
+                o[i][4 * g + 2] * c0 + x1.z * c1, o[i][4 * g + 3] * c0 + x1.w * c1);
+          }
+        }
+        if (hh == 0) *reinterpret_cast<float2*>(stats + item * 2) = make_float2(m, l);
+      }
+      return;
+    }
     if (qpos < Sq) {
       T* orow = out + b * sob + h * soh + qpos * sos;
 #pragma unroll
@@ -636,7 +665,7 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
   }
 }
 
-template <typename T, int D, int QPS, bool kDense, bool kStats>
+template <typename T, int D, int QPS, bool kDense, bool kStats, bool kSplit = false>
 static hipError_t launch_attn_mfma_k(const void* q, const int64_t* sq, const void* k,
                                      const int64_t* sk, const void* v, const int64_t* sv,
                                      void* out, const int64_t* so, int64_t B, int64_t Hq,
@@ -648,12 +677,12 @@ static hipError_t launch_attn_mfma_k(const void* q, const int64_t* sq, const voi
   static const int64_t zero[3] = {0, 0, 0};
   if (kStats) sv = so = zero;  // no V, no output
   const int64_t nblocks = WorkOrder{lay.nc, B, Hq, Hk, causal == 0}.grid_items();
-  hipLaunchKernelGGL((attn_mfma_kernel<T, D, QPS, kDense, kStats>), dim3(unsigned(nblocks)),
+  hipLaunchKernelGGL((attn_mfma_kernel<T, D, QPS, kDense, kStats, kSplit>), dim3(unsigned(nblocks)),
                      dim3(AttnShape<D, QPS>::kThreads), 0, stream, static_cast<const T*>(q),
                      sq[0], sq[1], sq[2], static_cast<const T*>(k), sk[0], sk[1], sk[2],
                      static_cast<const T*>(v), sv[0], sv[1], sv[2], static_cast<T*>(out), so[0],
                      so[1], so[2], B, Hq, Hk, Sq, Sk, causal, scale_log2, counts, indices, lay,
-                     nseg, segk, kDense ? dense_qoff : 0, stats);
+                     nseg, segk, (kDense || kSplit) ? dense_qoff : 0, stats);
   return hipGetLastError();
 }
 
@@ -704,6 +733,49 @@ static hipError_t launch_attn_mfma_t(int64_t D, int64_t qps, const void* q, cons
   VA_ATTN_CASE(64, 128)
   VA_ATTN_CASE(128, 128)
 #undef VA_ATTN_CASE
+  return hipErrorInvalidValue;
+}
+
+// Split-key partials for decode: q rows [0, Sq) of each of the B*H row groups
+// (the query heads sharing kv head h of batch b) against keys
+// [J*span, (J+1)*span), J < nsplit; results in `part` as described at the
+// kernel.
+template <typename T>
+static hipError_t launch_attn_split_t(int64_t D, const void* q, const int64_t* sq, const void* k,
+                                      const int64_t* sk, const void* v, const int64_t* sv,
+                                      int64_t B, int64_t H, int64_t Sq, int64_t Sk,
+                                      float scale_log2, int64_t nsplit, int64_t span,
+                                      float* part, hipStream_t stream) {
+  RowLayout lay;
+  lay.J0 = 0;
+  lay.nc = nsplit;
+  lay.qps = 64;
+  lay.Sk = Sk;
+  lay.dense_stride = 0;
+  lay.causal = 0;
+  lay.wo_init = 0;
+  static const int64_t zero[3] = {0, 0, 0};
+  if (D == 64)
+    return launch_attn_mfma_k<T, 64, 64, true, false, true>(
+        q, sq, k, sk, v, sv, nullptr, zero, B, H, H, Sq, Sk, 0, scale_log2, nullptr, nullptr, lay,
+        1, 0, span, part, stream);
+  if (D == 128)
+    return launch_attn_mfma_k<T, 128, 64, true, false, true>(
+        q, sq, k, sk, v, sv, nullptr, zero, B, H, H, Sq, Sk, 0, scale_log2, nullptr, nullptr, lay,
+        1, 0, span, part, stream);
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_attn_split(int dtype, int64_t D, const void* q, const int64_t* sq,
+                             const void* k, const int64_t* sk, const void* v, const int64_t* sv,
+                             int64_t B, int64_t H, int64_t Sq, int64_t Sk, float scale_log2,
+                             int64_t nsplit, int64_t span, float* part, hipStream_t stream) {
+  if (dtype == kBF16)
+    return launch_attn_split_t<bf16_t>(D, q, sq, k, sk, v, sv, B, H, Sq, Sk, scale_log2, nsplit,
+                                       span, part, stream);
+  if (dtype == kF16)
+    return launch_attn_split_t<f16_t>(D, q, sq, k, sk, v, sv, B, H, Sq, Sk, scale_log2, nsplit,
+                                      span, part, stream);
   return hipErrorInvalidValue;
 }
 

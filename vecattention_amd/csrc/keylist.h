@@ -64,6 +64,19 @@ struct KeyList {
     }
     return kl;
   }
+  // Keys [J*span, min((J+1)*span, Sk)) of a split key range (decode: the
+  // work-group's share of the KV cache), held as the "diagonal" span of the
+  // list; the kernel applies no causal mask to it (causal = 0).
+  __device__ static KeyList split(int64_t J, int64_t span, int64_t Sk) {
+    KeyList kl;
+    kl.cols = nullptr;
+    kl.n_col = 0;
+    kl.n_init = 0;
+    kl.diag0 = J * span;
+    const int64_t rem = Sk - kl.diag0;
+    kl.n_diag = rem < span ? (rem > 0 ? rem : 0) : span;
+    return kl;
+  }
   __device__ int64_t total() const { return n_init + n_diag + n_col; }
   __device__ int64_t key(int64_t p) const {
     if (p < n_init) return p;
