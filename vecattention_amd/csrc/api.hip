@@ -587,9 +587,11 @@ int va_sparse_attn_segments(int dtype, const void* q, int64_t sqb, int64_t sqh, 
 
 // Decode: the kv cache of each kv head is cut into nsplit ranges of `span`
 // keys (a multiple of the 64-key tile, at least 4 tiles), enough ranges for
-// about two work-groups per CU over all kv heads.
+// about one work-group per CU over all kv heads (measured on MI355X against
+// 128 - 1024 work-groups: fewer, longer ranges amortise each work-group's
+// first copies and halve the partials the merge reads).
 static void decode_split(int64_t L, int64_t Hk, int64_t* nsplit, int64_t* span) {
-  constexpr int64_t kTargetGroups = 512;
+  constexpr int64_t kTargetGroups = 256;
   const int64_t n = cdiv(kTargetGroups, Hk);
   int64_t sp = cdiv(cdiv(L, n), 64) * 64;
   if (sp < 256) sp = 256;
