@@ -13,7 +13,7 @@
 //
 // HBM-bound: each Q element is read once.  A thread owns VEC consecutive
 // features of one pooled row, so 16-byte loads of a full Q row are coalesced
-// across D/VEC neighbouring threads.
+// across D/VEC neighbouring threads, and keeps 8 rows' loads in flight.
 #include "common.h"
 
 namespace va {
@@ -39,14 +39,30 @@ __global__ __launch_bounds__(256) void pool_scale_kernel(
 #pragma unroll
   for (int e = 0; e < VEC; ++e) acc[e] = 0.0;
 
-  for (int64_t r = 0; r < rows; ++r) {
-    T v[VEC];
+  auto load = [&](T (&v)[VEC], int64_t r) {
     if constexpr (VEC * sizeof(T) == 16) {
       *reinterpret_cast<uint4*>(v) = *reinterpret_cast<const uint4*>(src + r * sqs);
     } else {
 #pragma unroll
       for (int e = 0; e < VEC; ++e) v[e] = src[r * sqs + e];
     }
+  };
+  // Rows are loaded U at a time (U loads in flight per thread) and added in
+  // row order, so the sums are those of the sequential loop.
+  constexpr int U = 8;
+  int64_t r = 0;
+  for (; r + U <= rows; r += U) {
+    T v[U][VEC];
+#pragma unroll
+    for (int u = 0; u < U; ++u) load(v[u], r + u);
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) acc[e] += double(to_f32(v[u][e]));
+  }
+  for (; r < rows; ++r) {
+    T v[VEC];
+    load(v, r);
 #pragma unroll
     for (int e = 0; e < VEC; ++e) acc[e] += double(to_f32(v[e]));
   }
