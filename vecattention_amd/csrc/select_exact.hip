@@ -24,11 +24,13 @@
 
 namespace va {
 
-constexpr int kSelRows = 16;     // pooled rows per work-group
 constexpr int kSelChunk = 256;   // keys per inner chunk (== blockDim.x)
 constexpr int kSelMaxD = 256;
 
-template <typename T>
+// kSelRows: pooled rows per work-group (16, 8 or 4: the host takes the most
+// rows that still give at least 256 work-groups, since each work-group walks
+// every key of its rows).
+template <typename T, int kSelRows>
 __global__ __launch_bounds__(256) void select_exact_kernel(
     const T* __restrict__ qs, int64_t sqb, int64_t sqh, int64_t sqn, const T* __restrict__ k,
     int64_t skb, int64_t skh, int64_t sks, int64_t B, int64_t Hq, int64_t Hk,
@@ -199,13 +201,20 @@ static hipError_t launch_select_exact_t(
     int64_t qps, int64_t bk, int64_t group, int causal, int64_t bsq,
     float gap_scalar, const float* gaps, const RowLayout& lay, int32_t* counts,
     int32_t* indices, hipStream_t stream) {
-  const int64_t nrowsets = (lay.nc + kSelRows - 1) / kSelRows;
-  const int64_t nblocks = nrowsets * B * Hq;
-  hipLaunchKernelGGL((select_exact_kernel<T>), dim3(unsigned(nblocks)), dim3(kSelChunk), 0,
-                     stream, static_cast<const T*>(qs), sqb, sqh, sqn, static_cast<const T*>(k),
-                     skb, skh, sks, B, Hq, Hk, Sk, D, qps, bk, group, causal, bsq,
-                     gap_scalar, gaps, lay, counts, indices, nrowsets);
-  return hipGetLastError();
+  auto launch = [&](auto rows_tag) {
+    constexpr int R = decltype(rows_tag)::value;
+    const int64_t nrowsets = (lay.nc + R - 1) / R;
+    const int64_t nblocks = nrowsets * B * Hq;
+    hipLaunchKernelGGL((select_exact_kernel<T, R>), dim3(unsigned(nblocks)), dim3(kSelChunk), 0,
+                       stream, static_cast<const T*>(qs), sqb, sqh, sqn,
+                       static_cast<const T*>(k), skb, skh, sks, B, Hq, Hk, Sk, D, qps, bk, group,
+                       causal, bsq, gap_scalar, gaps, lay, counts, indices, nrowsets);
+    return hipGetLastError();
+  };
+  constexpr int64_t kMinGroups = 256;
+  if ((lay.nc + 15) / 16 * B * Hq >= kMinGroups) return launch(std::integral_constant<int, 16>{});
+  if ((lay.nc + 7) / 8 * B * Hq >= kMinGroups) return launch(std::integral_constant<int, 8>{});
+  return launch(std::integral_constant<int, 4>{});
 }
 
 hipError_t launch_select_exact(int dtype, const void* qs, int64_t sqb, int64_t sqh,
