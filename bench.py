@@ -10,9 +10,13 @@ F_attn / t_step in TFLOP/s, where t_step is the timed VecAttention_prefill
 step (ms_per_step) and F_attn counts the attention FLOPs actually executed
 (4*D per query row per gathered key, local diagonal blocks counted whole).
 Extra fields: per-stage latencies (the same kernels, timed stage by stage with
-events on the launch stream), selection GB/s, dense bf16 SDPA latency on the
-same GPU and the speedup of the step over it, the roofline of the dominant
-kernel, and the CPU oracle timed on a bounded sample.
+events on the launch stream), selection GB/s, the dense latencies on the
+same GPU (PyTorch SDPA and this library's va_dense_attn) and the speedups of
+the step over both, the roofline of the dominant kernel, and the CPU oracle
+timed on a bounded sample.
+
+Other modes (one JSON line each): --decode L (decode attention over an
+L-token KV cache), --tuner (the threshold tuner's recall/sparsity evaluation).
 """
 import argparse
 import json
@@ -230,6 +234,28 @@ def time_dense(wl, q, k, v, reps=10, warmup=3):
             last = str(e)
             continue
     return None, f"unavailable: {last[:80]}"
+
+
+def time_dense_va(wl, q, k, v, reps=5, warmup=2):
+    """This library's dense attention (va_dense_attn, the Full_prefill path) on
+    the same tensors: every key, causal rows bottom-right aligned, GQA read in
+    place."""
+    from vecattention_amd import stages
+    out = torch.empty_like(q)
+    f = lambda: stages.dense_attention(q, k, v, out, causal=wl.causal)  # noqa: E731
+    for _ in range(warmup):
+        f()
+    torch.cuda.synchronize()
+    ts = []
+    for _ in range(reps):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        f()
+        b.record()
+        torch.cuda.synchronize()
+        ts.append(a.elapsed_time(b))
+    del out
+    return statistics.median(ts)
 
 
 # --------------------------------------------------------------- CPU oracle --
@@ -522,10 +548,13 @@ def main():
     ms_per_step = (time.perf_counter() - t0) * 1e3 / max(args.steps, 1)
     print(f"[bench] {args.steps} steps: {ms_per_step:.3f} ms/step", file=sys.stderr, flush=True)
 
-    dense_ms, dense_backend = (None, "skipped")
+    dense_ms, dense_backend, dense_va_ms = (None, "skipped", None)
     if not args.no_dense:
         dense_ms, dense_backend = time_dense(wl, q, k, v)
         print(f"[bench] dense SDPA ({dense_backend}): {dense_ms} ms", file=sys.stderr, flush=True)
+        if wl.dtype != torch.float32:
+            dense_va_ms = time_dense_va(wl, q, k, v)
+            print(f"[bench] dense va_dense_attn: {dense_va_ms:.3f} ms", file=sys.stderr, flush=True)
 
     t_sel_total = t_pool + t_sel
     # value: the whole VecAttention_prefill step, as timed above
@@ -558,6 +587,9 @@ def main():
         "dense_ms": None if dense_ms is None else round(dense_ms, 4),
         "dense_backend": dense_backend,
         "speedup_vs_dense": None if dense_ms is None else round(dense_ms / ms_per_step, 3),
+        "dense_va_ms": None if dense_va_ms is None else round(dense_va_ms, 4),
+        "dense_va_tflops": None if dense_va_ms is None else round(F_dense / (dense_va_ms * 1e-3) / 1e12, 1),
+        "speedup_vs_dense_va": None if dense_va_ms is None else round(dense_va_ms / ms_per_step, 3),
         "dense_equiv_tflops": round(F_dense / (ms_per_step * 1e-3) / 1e12, 3),
         "roofline": {"bound": "mfma", "kernel": "attn_mfma_kernel",
                      "achieved": round(attn_tflops, 3), "peak": BF16_PEAK_TFLOPS,
