@@ -146,9 +146,12 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
   const int rh = wave % S::kRowHalves, kc = wave / S::kRowHalves;
 
   const WorkOrder wo{lay.nc, B, Hq, Hk, causal == 0};
-  int64_t jr, bh;
-  if (!wo.map_item(blockIdx.x, jr, bh)) return;  // idle block (uniform)
-  const int64_t b = bh / Hq, h = bh % Hq, hk = h / (Hq / Hk);
+  int jr32, bh32;
+  if (!wo.map_item32(blockIdx.x, jr32, bh32)) return;  // idle block (uniform)
+  const int64_t jr = jr32, bh = bh32;
+  const uint32_t hq32 = uint32_t(Hq);  // 32-bit: every index is below 2^31
+  const int64_t b = uint32_t(bh32) / hq32, h = uint32_t(bh32) % hq32;
+  const int64_t hk = uint32_t(h) / (hq32 / uint32_t(Hk));
   const int64_t J = lay.J0 + jr;
 
   // ---- Q^T operand: lane holds row 32rh + l32, features [16s + 8hh, +8) ----

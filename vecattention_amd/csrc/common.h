@@ -145,6 +145,36 @@ struct WorkOrder {
     bh = i % BH;
     return true;
   }
+  // map_item in 32-bit arithmetic, for kernels: every quantity is below 2^31
+  // (the host bounds nrows * B * Hq by the grid limit), and a 64-bit division
+  // costs a few hundred dependent scalar instructions at every work-group start.
+  __device__ bool map_item32(uint32_t i, int& jr, int& bh) const {
+    const uint32_t n_rows = uint32_t(nrows), hq = uint32_t(Hq), hkv = uint32_t(Hk);
+    const uint32_t g = uint32_t(B) * hkv, r = hq / hkv;
+    if (kXcd % g == 0) {
+      const uint32_t copies = kXcd / g;
+      const uint32_t x = i % kXcd, s = i / kXcd;
+      const uint32_t grp = x % g, c = x / g;
+      const uint32_t j = s * copies + c;
+      if (j >= r * n_rows) return false;
+      jr = int(n_rows - 1 - j / r);
+      bh = int((grp / hkv) * hq + (grp % hkv) * r + j % r);
+      return true;
+    }
+    if (g % kXcd == 0 || equal_rows) {
+      const uint32_t rn = r * n_rows, n = g * rn, per = (n + kXcd - 1) / kXcd;
+      const uint32_t L = (i % kXcd) * per + i / kXcd;
+      if (L >= n) return false;
+      const uint32_t grp = L / rn, rem = L % rn;
+      jr = int(n_rows - 1 - rem / r);
+      bh = int((grp / hkv) * hq + (grp % hkv) * r + rem % r);
+      return true;
+    }
+    const uint32_t BH = uint32_t(B) * hq;
+    jr = int(n_rows - 1 - i / BH);
+    bh = int(i % BH);
+    return true;
+  }
 };
 
 // ---------------------------------------------------------------------------
@@ -173,7 +203,7 @@ struct RowLayout {
   __host__ __device__ static int64_t tri(int64_t n) { return n >= 1 ? n * (n - 1) / 2 : 0; }
   // Sum over j in [0, J) of max(0, j - a).
   __host__ __device__ int64_t prefix_causal(int64_t J) const {
-    const int64_t a = smin() / qps;  // 0 or 1
+    const int64_t a = wo_init ? 1 : 0;  // smin / qps for causal rows
     return tri(J - a);
   }
   __host__ __device__ int64_t capacity(int64_t J) const {
