@@ -61,7 +61,7 @@ struct AttnShape {
   static constexpr int kStageBytes = 2 * kTileBytes;         // K tile, then V tile
   static constexpr int kRowsPerCopy = 1024 / kRowBytes;      // rows per 1 KB copy
   static constexpr int kCopiesPerWave = kTileBytes / 1024 / kWaves;  // per operand
-  static constexpr int kMergeBytes = kRowHalves * 64 * (D / 2 + 2) * 4;
+  static constexpr int kMergeBytes = kRowHalves * 64 * (D / 2 + 4) * 4;
   static constexpr int kDataBytes = 2 * kStageBytes > kMergeBytes ? 2 * kStageBytes : kMergeBytes;
   // Key ids: a ring of 2 * kWaves tile slots; every kWaves tiles each wave
   // stages the ids of one tile kWaves to 2 * kWaves - 1 tiles ahead.
@@ -587,7 +587,7 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
 
   // ---- merge the two key halves, normalise, store --------------------------
   vm_lds_barrier();  // every wave is done with the stages, the last copies have landed
-  float* mo = reinterpret_cast<float*>(smem) + rh * 64 * (D / 2 + 2);
+  float* mo = reinterpret_cast<float*>(smem) + rh * 64 * (D / 2 + 4);
   if constexpr (kStats) {
     const float lrow = sum_halves(lsum);
     if (kc == 1) {
@@ -605,54 +605,61 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
     }
     return;
   }
-  if (kc == 1) {
+  // Each wave of a row half finishes half of the features (kc 0: blocks
+  // [0, HB), kc 1: [HB, NB) of 32 features): it leaves the other half of its
+  // partial output and its (m, l) in LDS and combines its own half with the
+  // other wave's.  Per row half: two 64 x D/4 float regions (written by kc 0,
+  // kc 1), then (m, l) of both waves.
+  constexpr int NB = D / 32, HB = NB / 2;
+  float* xw = mo + kc * 64 * (D / 4);
+  const float* xr = mo + (kc ^ 1) * 64 * (D / 4);
+  float* mlx = mo + 64 * (D / 2);
+  const float lrow = sum_halves(lsum);  // row sum of this wave's key half, both halves
+  auto finish = [&](auto keep_tag) {
+    constexpr int K0 = decltype(keep_tag)::value * HB;  // first block kept here
+    constexpr int O0 = HB - K0;                          // first block the other wave keeps
 #pragma unroll
-    for (int i = 0; i < D / 32; ++i)
+    for (int ii = 0; ii < HB; ++ii)
 #pragma unroll
       for (int g = 0; g < 4; ++g)
-        *reinterpret_cast<float4*>(mo + ((4 * i + g) * 64 + lane) * 4) =
-            make_float4(o[i][4 * g], o[i][4 * g + 1], o[i][4 * g + 2], o[i][4 * g + 3]);
-  }
-  const float lrow = sum_halves(lsum);  // row sum of this wave's key half, both halves
-  if (kc == 1) {
-    mo[64 * (D / 2) + lane] = mc;
-    mo[64 * (D / 2) + 64 + lane] = lrow;
-  }
-  lds_barrier();
-  if (kc == 0) {
-    const float m1 = mo[64 * (D / 2) + lane], l1 = mo[64 * (D / 2) + 64 + lane];
+        *reinterpret_cast<float4*>(xw + ((4 * ii + g) * 64 + lane) * 4) =
+            make_float4(o[O0 + ii][4 * g], o[O0 + ii][4 * g + 1], o[O0 + ii][4 * g + 2],
+                        o[O0 + ii][4 * g + 3]);
+    mlx[kc * 128 + lane] = mc;
+    mlx[kc * 128 + 64 + lane] = lrow;
+    lds_barrier();
+    const float m1 = mlx[(kc ^ 1) * 128 + lane], l1 = mlx[(kc ^ 1) * 128 + 64 + lane];
     const float m = __builtin_fmaxf(mc, m1);
     const float a0 = (mc == m) ? 1.f : __builtin_amdgcn_exp2f(mc - m);
     const float a1 = (m1 == m) ? 1.f : __builtin_amdgcn_exp2f(m1 - m);
     const float l = lrow * a0 + l1 * a1;
     const float inv = l > 0.f ? 1.f / l : 0.f;
     const float c0 = a0 * inv, c1 = a1 * inv;
+    if (qpos >= Sq) return;
     if constexpr (kSplit) {  // fp32 partial output and (m, l) of this key range
-      if (qpos < Sq) {
-        const int64_t item = (bh * Sq + qpos) * lay.nc + jr;
-        float* po = stats + (2 * B * Hq * lay.nc * Sq + 3) / 4 * 4 + item * D;
+      const int64_t item = (bh * Sq + qpos) * lay.nc + jr;
+      float* po = stats + (2 * B * Hq * lay.nc * Sq + 3) / 4 * 4 + item * D;
 #pragma unroll
-        for (int i = 0; i < D / 32; ++i) {
-#pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            const float4 x1 = *reinterpret_cast<const float4*>(mo + ((4 * i + g) * 64 + lane) * 4);
-            const int d0 = i * 32 + 8 * g + 4 * hh;
-            *reinterpret_cast<float4*>(po + d0) = make_float4(
-                o[i][4 * g + 0] * c0 + x1.x * c1, o[i][4 * g + 1] * c0 + x1.y * c1,
-                o[i][4 * g + 2] * c0 + x1.z * c1, o[i][4 * g + 3] * c0 + x1.w * c1);
-          }
-        }
-        if (hh == 0) *reinterpret_cast<float2*>(stats + item * 2) = make_float2(m, l);
-      }
-      return;
-    }
-    if (qpos < Sq) {
-      T* orow = out + b * sob + h * soh + qpos * sos;
-#pragma unroll
-      for (int i = 0; i < D / 32; ++i) {
+      for (int ii = 0; ii < HB; ++ii) {
+        const int i = K0 + ii;
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-          const float4 x1 = *reinterpret_cast<const float4*>(mo + ((4 * i + g) * 64 + lane) * 4);
+          const float4 x1 = *reinterpret_cast<const float4*>(xr + ((4 * ii + g) * 64 + lane) * 4);
+          const int d0 = i * 32 + 8 * g + 4 * hh;
+          *reinterpret_cast<float4*>(po + d0) = make_float4(
+              o[i][4 * g + 0] * c0 + x1.x * c1, o[i][4 * g + 1] * c0 + x1.y * c1,
+              o[i][4 * g + 2] * c0 + x1.z * c1, o[i][4 * g + 3] * c0 + x1.w * c1);
+        }
+      }
+      if (kc == 0 && hh == 0) *reinterpret_cast<float2*>(stats + item * 2) = make_float2(m, l);
+    } else {
+      T* orow = out + b * sob + h * soh + qpos * sos;
+#pragma unroll
+      for (int ii = 0; ii < HB; ++ii) {
+        const int i = K0 + ii;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const float4 x1 = *reinterpret_cast<const float4*>(xr + ((4 * ii + g) * 64 + lane) * 4);
           const int d0 = i * 32 + 8 * g + 4 * hh;
           const T e0 = Round<T>::store(o[i][4 * g + 0] * c0 + x1.x * c1);
           const T e1 = Round<T>::store(o[i][4 * g + 1] * c0 + x1.y * c1);
@@ -665,7 +672,11 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
         }
       }
     }
-  }
+  };
+  if (kc == 0)
+    finish(std::integral_constant<int, 0>{});
+  else
+    finish(std::integral_constant<int, 1>{});
 }
 
 template <typename T, int D, int QPS, bool kDense, bool kStats, bool kSplit = false>
