@@ -71,9 +71,6 @@ struct AttnShape {
                 "tile copies must split evenly over the waves");
 };
 
-// Per-tile facts shared by the copy and the compute of a tile: number of
-// valid slots, and for diagonal tiles the offset of slot 0 from the first
-// diagonal key.
 // XOR swizzle of the 16-byte chunks of tile row R.  The LDS serves 256 bytes
 // per clock from 64 four-byte banks: a ds_read_b128 is served 16 lanes at a
 // time, a ds_read_b64_tr_b16 32 lanes at a time.  Rows R and R + 256 / (2D)
@@ -98,6 +95,9 @@ __device__ inline int chunk_swizzle(int R) {
   }
 }
 
+// Per-tile facts shared by the copy and the compute of a tile: number of
+// valid slots, and for diagonal tiles the offset of slot 0 from the first
+// diagonal key.
 struct TileInfo {
   int lim;
   int dshift;
@@ -443,15 +443,19 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
   // ---- pipeline ------------------------------------------------------------
   // LDS slots: K(u) in K slot u&1, V(u) in V slot u&1 (slot p of K at
   // p * kStageBytes, of V kTileBytes after it), key ids of tile u in ids slot
-  // u % kIdSlots.  Iteration t computes S(t+1) = QK(t+1) next to the softmax
-  // of S(t), then PV(t) next to the masking and maximum of S(t+1).  Resident
-  // during iteration t: K(t+1), V(t); in flight: K(t+2), V(t+1); one barrier
-  // per iteration.  Iterations t = 0 mod W stage the ids of tiles t+W ..
-  // t+2W-1, first read (for the copies of tile t+W) at iteration t+W-2 > t,
-  // and written over 2W tiles later, after their last read.  The copies of an iteration are spread over its QK
-  // MFMAs (one DMA instruction after an MFMA), so that a copy that waits for
-  // room in the memory pipeline overlaps the matrix work already issued
-  // instead of stalling every wave right after the barrier.
+  // u % kIdSlots.  Iteration t has two halves, each opened by a barrier:
+  //  - first half (K(t+1) landed): S(t+1) = QK(t+1) next to the softmax of
+  //    S(t); the copies of V(t+1) go out between the QK MFMAs;
+  //  - second half (V(t) landed; every wave is done with K(t+1)): PV(t) next
+  //    to the masking and maximum of S(t+1); the copies of K(t+3) go into the
+  //    K slot QK(t+1) just read.
+  // Each copy thus has one and a half tiles to land, and a barrier leaves
+  // the 2H most recent copies of the wave in flight.  Iterations t = 0 mod W
+  // stage the ids of tiles t+W .. t+2W-1, first read (for the copies of
+  // K(t+W)) at iteration t+W-3 > t, and written over 2W tiles later, after
+  // their last read.  Copies are spread over the MFMAs (one DMA instruction
+  // after an MFMA), so that a copy that waits for room in the memory pipeline
+  // overlaps the matrix work already issued.
   constexpr int NQK = D / 16;  // QK MFMAs per tile
   f32x16_t s_cur;              // masked scores of tile t
   constexpr int W = S::kWaves;
