@@ -189,12 +189,7 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
       const int room = int(cap) - seg_slot(lane);
       c = c < 0 ? 0 : (c > room ? (room > 0 ? room : 0) : c);
     }
-    int incl = c;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const int y = __shfl_up(incl, o);
-      if (lane >= o) incl += y;
-    }
+    const int incl = wave_inclusive_sum(c);
     if (lane < nseg) sv = incl - c;
     cnt = __builtin_amdgcn_readlane(incl, nseg - 1);
   }

@@ -107,4 +107,20 @@ __device__ inline float other_half(float x) {
   return __builtin_bit_cast(float, other_half(__builtin_bit_cast(uint32_t, x)));
 }
 
+// Inclusive prefix sum over the 64 lanes, in registers (DPP): shifts by 1,
+// 2, 4, 8 inside each row of 16 lanes, then the total of row 0 (lane 15)
+// added to row 1 and that of row 2 to row 3 (row_bcast:15), then the total
+// of rows 0-1 (lane 31) added to rows 2-3 (row_bcast:31).  A lane whose DPP
+// source is outside its row, or whose row is masked off, adds the `old`
+// operand, 0.
+__device__ inline int wave_inclusive_sum(int x) {
+  x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, false);  // row_shr:1
+  x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, false);  // row_shr:2
+  x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, false);  // row_shr:4
+  x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, false);  // row_shr:8
+  x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xa, 0xf, false);  // row_bcast:15 -> rows 1, 3
+  x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xc, 0xf, false);  // row_bcast:31 -> rows 2, 3
+  return x;
+}
+
 }  // namespace va
