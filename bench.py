@@ -261,42 +261,49 @@ def time_dense_va(wl, q, k, v, reps=5, warmup=2):
 # --------------------------------------------------------------- CPU oracle --
 
 def cpu_baseline(wl, q_cpu, k_cpu, v_cpu, threshold, seconds):
-    """The oracle (C selection + numpy attention, 1 thread) on sampled q-blocks
-    of head 0; TFLOP/s on the executed attention FLOPs of the sample."""
+    """The oracle (C selection + numpy attention, 1 thread) on sampled q-blocks,
+    head after head (each head's q-blocks in random order) until `seconds` of
+    CPU work; TFLOP/s on the executed attention FLOPs of the sample."""
     import numpy as np
     from threadpoolctl import threadpool_limits
 
     from oracle import oracle as orc
     qps, S, D = wl.q_pooling_size, q_cpu.shape[2], wl.D
     Sk = k_cpu.shape[2]
+    rep = wl.Hq // wl.Hk
     dt = {torch.bfloat16: "bfloat16", torch.float16: "float16", torch.float32: "float32"}[wl.dtype]
-    qh = q_cpu[:, :1].float().numpy()
-    kh = k_cpu[:, :1].float().numpy()
-    vh = v_cpu[:, :1].float().numpy()
     nqb = math.ceil(S / qps)
     gaps = orc.gap_from_threshold(threshold, 1, 1)
     bc, bi = orc.local_blocks(1, 1, S, qps, wl.causal)
-    order = np.random.default_rng(0).permutation(nqb)
-    flops, done, t0 = 0.0, 0, time.perf_counter()
+    rng = np.random.default_rng(0)
+    flops, done, heads, t0 = 0.0, 0, 0, time.perf_counter()
     with threadpool_limits(1):
-        _, qs = orc.pool(qh, qps, dt)
-        for J in order:
-            J = int(J)
-            c0 = (J * qps) // wl.chunk_size * (wl.chunk_size // qps)
-            ncc = min(wl.chunk_size // qps, nqb - c0)
-            cnt, lists = orc.select(qs, kh, c0, ncc, gaps, qps, wl.k_local_size, wl.group_k_block,
-                                    wl.causal, wl.causal, 64, rows=(J - c0, J - c0 + 1))
-            orc.attention(qh, kh, vh, qps, wl.causal, bc, bi, [[lists[0][0][J - c0:J - c0 + 1]]],
-                          J0=J, nc=1, acc=np.float32)
-            rows = min(qps, S - J * qps)
-            flops += 4.0 * D * rows * (int(cnt[0, 0, J - c0]) + local_keys(J, qps, Sk, wl.causal))
-            done += 1
+        for h in range(wl.Hq):
+            qh = q_cpu[:, h:h + 1].float().numpy()
+            kh = k_cpu[:, h // rep:h // rep + 1].float().numpy()
+            vh = v_cpu[:, h // rep:h // rep + 1].float().numpy()
+            _, qs = orc.pool(qh, qps, dt)
+            heads += 1
+            for J in rng.permutation(nqb):
+                J = int(J)
+                c0 = (J * qps) // wl.chunk_size * (wl.chunk_size // qps)
+                ncc = min(wl.chunk_size // qps, nqb - c0)
+                cnt, lists = orc.select(qs, kh, c0, ncc, gaps, qps, wl.k_local_size,
+                                        wl.group_k_block, wl.causal, wl.causal, 64,
+                                        rows=(J - c0, J - c0 + 1))
+                orc.attention(qh, kh, vh, qps, wl.causal, bc, bi,
+                              [[lists[0][0][J - c0:J - c0 + 1]]], J0=J, nc=1, acc=np.float32)
+                rows = min(qps, S - J * qps)
+                flops += 4.0 * D * rows * (int(cnt[0, 0, J - c0]) + local_keys(J, qps, Sk, wl.causal))
+                done += 1
+                if time.perf_counter() - t0 > seconds and done >= 4:
+                    break
             if time.perf_counter() - t0 > seconds and done >= 4:
                 break
     el = time.perf_counter() - t0
     return {"value": flops / el / 1e12, "unit": "TFLOP/s", "cores": 1, "kind": "port",
             "sample": f"oracle (C selection, numpy fp32 attention) on {done} random q-blocks of "
-                      f"head 0 of workload {wl.name}, {el:.1f} s",
+                      f"{heads} head(s) of workload {wl.name}, {el:.1f} s",
             "host_cpu": platform.processor() or platform.machine(),
             "host_threads_available": len(os.sched_getaffinity(0))}
 
