@@ -460,7 +460,15 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
   constexpr int kKeep = kStats ? H : 2 * H;
   if (ntiles > 0) {
     if (wave < ntiles) stage_ids(wave, wave);  // tiles 0 .. W-1
-    vm_lds_barrier();
+    // When tiles 0 and 1 are local blocks (their ids are LDS writes), their
+    // copies need no column ids: the barrier waits for LDS only and the
+    // column-id copies stay in flight next to K(0), K(1), V(0); the barrier
+    // after them (K(0) landed) also covers the older column-id copies, which
+    // copy_pairs(2) reads next.
+    if (t_init + t_diag >= 2)
+      lds_barrier();
+    else
+      vm_lds_barrier();
     // K(0), K(1), V(0); after QK(0), K(2) into K(0)'s slot.  The loop's
     // barriers leave the kKeep most recent copies of the wave in flight.
     uint64_t pr[H], pr1[H];
