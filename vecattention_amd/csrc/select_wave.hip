@@ -395,16 +395,19 @@ __global__ __launch_bounds__(256, 2) void select_wave_kernel(
   // stalling on a burst of MFMA issues and then running its VALU work alone.
   const int kfirst = (smin > seg_lo ? smin : seg_lo) / kWChunk * kWChunk;
   const int nchunks = wg_end > kfirst ? (wg_end - kfirst + kWChunk - 1) / kWChunk : 0;
-  f32x16_t acc[2], nxt[2];
+  f32x16_t acc_even[2], acc_odd[2];  // scores of the even / odd chunks
   if (nchunks > 0) {
     issue_chunk(kfirst, 0);
     if (nchunks > 1) issue_chunk(kfirst + kWChunk, 1);
     vm_lds_barrier();
-    if (kfirst < wave_end) score(0, acc);
+    if (kfirst < wave_end) score(0, acc_even);
   }
-  for (int c = 0; c < nchunks; ++c) {
+  // One chunk; the parity P = c & 1 is a compile-time constant so that the
+  // stage addresses fold into the instructions and the scores of chunk c
+  // (acc) and c+1 (nxt) alternate between two register sets with no copy.
+  auto chunk = [&](int c, auto parity_tag, f32x16_t (&acc)[2], f32x16_t (&nxt)[2]) {
+    constexpr int st = decltype(parity_tag)::value;
     const int kb0 = kfirst + c * kWChunk;
-    const int st = c & 1;
     vm_lds_barrier();  // chunk c+1 landed; every wave has scored chunk c (stage st is free)
     if (c + 2 < nchunks) issue_chunk(kb0 + 2 * kWChunk, st);
     if (kb0 < wave_end) {  // this wave's rows still need keys (uniform)
@@ -582,8 +585,10 @@ __global__ __launch_bounds__(256, 2) void select_wave_kernel(
       slots(7 * NSL / 8, NSL);
       if (mode != kPassMax) append(kb0, 1, bits[1]);
     }
-#pragma unroll
-    for (int bb = 0; bb < 2; ++bb) acc[bb] = nxt[bb];
+  };
+  for (int c = 0; c < nchunks; c += 2) {
+    chunk(c, std::integral_constant<int, 0>{}, acc_even, acc_odd);
+    if (c + 1 < nchunks) chunk(c + 1, std::integral_constant<int, 1>{}, acc_odd, acc_even);
   }
 
   if (mode == kPassMax) {
