@@ -364,6 +364,9 @@ E2E_CASES = [
     ("dit-like-2pass", 1, 2, 2, 9000, 128, torch.bfloat16, False, 64, 16, 8192, 4608, 0.3),
     ("causal-qps128-bk16", 1, 4, 4, 1300, 64, torch.bfloat16, True, 128, 16, 4, 512, 0.6),
     ("A-fp32-noncausal", 1, 4, 4, 4096, 64, torch.float32, False, 64, 16, 16, 4096, 0.35),
+    # batches: every (b, h) work item, strides over the batch dimension
+    ("batch2-causal-gqa", 2, 8, 2, 1536, 128, torch.bfloat16, True, 64, 16, 16, 1024, 0.5),
+    ("batch3-noncausal-fp16-d64", 3, 4, 2, 1100, 64, torch.float16, False, 64, 16, 8192, 1024, 0.3),
 ]
 
 
@@ -392,6 +395,19 @@ def test_prefill_per_head_threshold_tensor(device):
     out = VecAttention_prefill(q.to(device), k.to(device), v.to(device), th.to(device), 64, 16, 16,
                                False, 512)
     want, _ = orc.prefill(q, k, v, th.numpy(), 64, 16, 16, False, 512, 64, "bfloat16")
+    err = np.abs(out.float().cpu().numpy() - want)
+    assert err.max() <= ATOL_MAX and err.mean() <= ATOL_MEAN
+
+
+def test_prefill_per_batch_and_head_threshold_tensor(device):
+    # a (B, H) threshold tensor: every (b, h) its own gap
+    note("e2e per-(b,h)")
+    B, Hq, S, D = 2, 3, 900, 128
+    q, k, v = make_inputs(B, Hq, Hq, S, D, torch.bfloat16, seed=5)
+    th = torch.tensor([[0.9, 0.5, 0.1], [0.05, 0.3, 0.7]])
+    out = VecAttention_prefill(q.to(device), k.to(device), v.to(device), th.to(device), 64, 16, 16,
+                               True, 512)
+    want, _ = orc.prefill(q, k, v, th.numpy(), 64, 16, 16, True, 512, 64, "bfloat16")
     err = np.abs(out.float().cpu().numpy() - want)
     assert err.max() <= ATOL_MAX and err.mean() <= ATOL_MEAN
 
