@@ -94,6 +94,24 @@ def test_pool_bit_exact(device, dtype, S, qps):
     assert np.array_equal(scaled.float().cpu().numpy(), want_s)
 
 
+@pytest.mark.parametrize("dtype,D,offset", [(torch.bfloat16, 256, 0), (torch.float32, 256, 0),
+                                            (torch.float32, 36, 0), (torch.bfloat16, 200, 1),
+                                            (torch.float16, 24, 0)])
+def test_pool_head_dims_and_alignment(device, dtype, D, offset):
+    """Vectorised rows (16-byte loads, up to 64 lanes per row) and the
+    per-feature form (rows not 16-byte aligned: a one-element offset into the
+    buffer), at head dims up to 256."""
+    note("pool D", dtype, D, offset)
+    q, _, _ = make_inputs(1, 3, 3, 700, D, dtype, seed=D)
+    buf = torch.empty(q.numel() + offset, dtype=dtype, device=device)
+    qd = buf[offset:].view(q.shape)
+    qd.copy_(q.to(device))
+    scaled, pooled = stages.pool_scaled(qd, 64, want_pooled=True)
+    want_p, want_s = orc.pool(q, 64, DTN[dtype])
+    assert np.array_equal(pooled.float().cpu().numpy(), want_p)
+    assert np.array_equal(scaled.float().cpu().numpy(), want_s)
+
+
 def test_pool_strided_bshd_view(device):
     note("pool strided")
     q, _, _ = make_inputs(1, 4, 4, 640, 128, torch.bfloat16, seed=11)

