@@ -154,17 +154,31 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
   const int64_t hk = uint32_t(h) / (hq32 / uint32_t(Hk));
   const int64_t J = lay.J0 + jr;
 
+  // Segment counts of the row (lane s: segment s), loaded ahead of Q: the
+  // wait counter retires loads in issue order, so the scan below then waits
+  // for these alone and not for the Q rows too.
+  // A buffer load without a branch (lanes past nseg, and every lane when the
+  // row has a single count, read past the range and get 0), so that the wait
+  // counter's bookkeeping sees it issued before the Q rows on every path.
+  const bool seg_counts = counts != nullptr && nseg > 1;
+  const int c_seg = int(__builtin_amdgcn_raw_buffer_load_b32(
+      make_rsrc(seg_counts ? counts + (bh * lay.nc + jr) * nseg : counts,
+                seg_counts ? uint32_t(nseg) * 4u : 0u),
+      lane * 4, 0, 0));
+
   // ---- Q^T operand: lane holds row 32rh + l32, features [16s + 8hh, +8) ----
-  // (loads issued first; their latency overlaps the list bookkeeping below)
+  // (loads issued early; their latency overlaps the list bookkeeping below)
   const int qrow_local = 32 * rh + l32;
   const int64_t qpos = (kSplit ? 0 : J * QPS) + qrow_local;
   vec qreg[D / 16];
   {
-    const T* qr_ptr = q + b * sqb + h * sqh + qpos * sqs;
+    // Rows past Sq load row Sq - 1 and are zeroed: no branch around the loads.
+    const bool qin = qpos < Sq;
+    const T* qr_ptr = q + b * sqb + h * sqh + (qin ? qpos : Sq - 1) * sqs;
 #pragma unroll
     for (int s = 0; s < D / 16; ++s) {
-      uint4 raw = make_uint4(0, 0, 0, 0);
-      if (qpos < Sq) raw = *reinterpret_cast<const uint4*>(qr_ptr + 16 * s + 8 * hh);
+      uint4 raw = *reinterpret_cast<const uint4*>(qr_ptr + 16 * s + 8 * hh);
+      if (!qin) raw = make_uint4(0, 0, 0, 0);
       qreg[s] = __builtin_bit_cast(vec, raw);
     }
   }
@@ -185,7 +199,7 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
   } else if (counts) {  // whole wave: the scan exchanges lanes
     int c = 0;
     if (lane < nseg) {
-      c = counts[(bh * lay.nc + jr) * nseg + lane];
+      c = c_seg;
       const int room = int(cap) - seg_slot(lane);
       c = c < 0 ? 0 : (c > room ? (room > 0 ? room : 0) : c);
     }
