@@ -172,15 +172,13 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
   const int64_t qpos = (kSplit ? 0 : J * QPS) + qrow_local;
   vec qreg[D / 16];
   {
-    // Rows past Sq load row Sq - 1 and are zeroed: no branch around the loads.
-    const bool qin = qpos < Sq;
-    const T* qr_ptr = q + b * sqb + h * sqh + (qin ? qpos : Sq - 1) * sqs;
+    // Rows past Sq load row Sq - 1: no branch around the loads and nothing
+    // consumes them before the first QK^T.  Those rows' results are never
+    // written (every epilogue form skips qpos >= Sq).
+    const T* qr_ptr = q + b * sqb + h * sqh + (qpos < Sq ? qpos : Sq - 1) * sqs;
 #pragma unroll
-    for (int s = 0; s < D / 16; ++s) {
-      uint4 raw = *reinterpret_cast<const uint4*>(qr_ptr + 16 * s + 8 * hh);
-      if (!qin) raw = make_uint4(0, 0, 0, 0);
-      qreg[s] = __builtin_bit_cast(vec, raw);
-    }
+    for (int s = 0; s < D / 16; ++s)
+      qreg[s] = __builtin_bit_cast(vec, *reinterpret_cast<const uint4*>(qr_ptr + 16 * s + 8 * hh));
   }
 
   // Selected columns.  With nseg > 1 the row's list comes in key segments:
