@@ -2,8 +2,9 @@
 
 A step is one VecAttention_prefill call (pooling + TilingSelect selection +
 vector-sparse attention) on the seeded synthetic input of the workload, with
-inputs resident in HBM.  Default workload: B (Qwen2.5-VL-shaped 32K causal
-prefill, GQA 28/4, bf16, keep ~10%).
+inputs resident in HBM.  Default workload: C (Qwen2.5-VL-shaped 128K causal
+prefill, GQA 28/4, bf16, keep ~5%), the north-star shape; the same line
+carries workload B (the 32K prefill) under "extra_workloads".
 
 Prints ONE JSON line.  `value` is the end-to-end sparse-effective throughput
 F_attn / t_step in TFLOP/s, where t_step is the timed VecAttention_prefill
@@ -13,7 +14,7 @@ Extra fields: per-stage latencies (the same kernels, timed stage by stage with
 events on the launch stream), selection GB/s, the dense latencies on the
 same GPU (PyTorch SDPA and this library's va_dense_attn) and the speedups of
 the step over both, the roofline of the dominant kernel, and the CPU oracle
-timed on a bounded sample.
+timed on a bounded sample over every host core.
 
 Other modes (one JSON line each): --decode L (decode attention over an
 L-token KV cache), --tuner (the threshold tuner's recall/sparsity evaluation).
@@ -42,10 +43,16 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", default="B", help="workload key A..E")
+    ap.add_argument("--config", default="C", help="workload key A..E")
+    ap.add_argument("--extra", default=None,
+                    help="comma-separated workload keys measured after the headline and "
+                         "reported under extra_workloads (default: B when the headline is C; "
+                         "'none' for none)")
     ap.add_argument("--no-dense", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--cpu-workers", type=int, default=None,
+                    help="CPU baseline processes (default: every core of the affinity set)")
     ap.add_argument("--stage-reps", type=int, default=5)
     ap.add_argument("--extra-json", default=None, help="append the result line to this file too")
     ap.add_argument("--threshold", type=float, default=None,
@@ -115,15 +122,36 @@ def selectable(wl, S):
 
 # ------------------------------------------------------------------ traffic --
 
+def kernel_source_hash():
+    """sha256 (first 16 hex digits) over the HIP sources and headers of the
+    library, in name order: the key that ties a traffic profile to the
+    kernels it measured."""
+    import hashlib
+    csrc = os.path.join(ROOT, "vecattention_amd", "csrc")
+    h = hashlib.sha256()
+    for name in sorted(os.listdir(csrc)):
+        if name.endswith((".hip", ".h")):
+            h.update(name.encode())
+            with open(os.path.join(csrc, name), "rb") as f:
+                h.update(f.read())
+    return h.hexdigest()[:16]
+
+
 def profiled_traffic(workload, kernel):
-    """HBM bytes per launch of `kernel` on `workload` (FETCH_SIZE + WRITE_SIZE,
-    each scaled by the copy-kernel calibration) from the rocprofv3 --pmc runs
-    summarised in profiles/hbm_traffic.json; None when not profiled."""
+    """Bytes per launch of `kernel` on `workload` crossing from L2 to the data
+    fabric (FETCH_SIZE + WRITE_SIZE, each scaled by the copy-kernel
+    calibration; fabric reads include those the Infinity Cache serves), from
+    the rocprofv3 --pmc runs summarised in profiles/hbm_traffic.json.  None
+    when not profiled, or when the profile was taken on other kernel sources
+    than the ones built now (its source_hash differs)."""
     path = os.path.join(ROOT, "profiles", "hbm_traffic.json")
     try:
         with open(path) as f:
-            rec = json.load(f)["workloads"][workload][kernel]
+            doc = json.load(f)
+        rec = doc["workloads"][workload][kernel]
     except (OSError, KeyError, ValueError):
+        return None
+    if doc.get("source_hash") != kernel_source_hash():
         return None
     return int(round(rec["fetch_bytes"] + rec["write_bytes"]))
 
@@ -260,51 +288,85 @@ def time_dense_va(wl, q, k, v, reps=5, warmup=2):
 
 # --------------------------------------------------------------- CPU oracle --
 
-def cpu_baseline(wl, q_cpu, k_cpu, v_cpu, threshold, seconds):
-    """The oracle (C selection + numpy attention, 1 thread) on sampled q-blocks,
-    head after head (each head's q-blocks in random order) until `seconds` of
-    CPU work; TFLOP/s on the executed attention FLOPs of the sample."""
+def host_cpu_model():
+    """The CPU model named by /proc/cpuinfo (else the machine type)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
+
+
+def cpu_baseline(wl, q_cpu, k_cpu, v_cpu, threshold, seconds, workers=None):
+    """The CPU oracle (C selection + numpy fp32 attention, one thread per
+    process) on q-blocks sampled uniformly over the workload's (q head,
+    q-block) pairs, spread over one child process per host core in the
+    process's affinity set (oracle/sample_worker.py; the children never touch
+    the GPU).  Each child works through its share of the sample for `seconds`;
+    the value is the sample's executed attention FLOPs over the slowest
+    child's time, in TFLOP/s, with selection and attention times reported
+    separately."""
+    import json as _json
+    import shutil
+    import subprocess
+    import tempfile
+
     import numpy as np
-    from threadpoolctl import threadpool_limits
 
     from oracle import oracle as orc
     qps, S, D = wl.q_pooling_size, q_cpu.shape[2], wl.D
-    Sk = k_cpu.shape[2]
     rep = wl.Hq // wl.Hk
     dt = {torch.bfloat16: "bfloat16", torch.float16: "float16", torch.float32: "float32"}[wl.dtype]
     nqb = math.ceil(S / qps)
-    gaps = orc.gap_from_threshold(threshold, 1, 1)
-    bc, bi = orc.local_blocks(1, 1, S, qps, wl.causal)
+    n = workers or len(os.sched_getaffinity(0))
     rng = np.random.default_rng(0)
-    flops, done, heads, t0 = 0.0, 0, 0, time.perf_counter()
-    with threadpool_limits(1):
-        for h in range(wl.Hq):
+    # one q head per kv group (heads cost the same), q-blocks uniform over the
+    # sequence; enough samples that no child runs out before its time is up
+    heads = [g * rep for g in range(wl.Hk)][:4]
+    samples = [(int(rng.choice(heads)), int(rng.integers(0, nqb))) for _ in range(4000 * n)]
+    base = "/dev/shm" if os.path.isdir("/dev/shm") else None
+    tmp = tempfile.mkdtemp(prefix="va_cpu_", dir=base)
+    try:
+        for h in heads:
             qh = q_cpu[:, h:h + 1].float().numpy()
-            kh = k_cpu[:, h // rep:h // rep + 1].float().numpy()
-            vh = v_cpu[:, h // rep:h // rep + 1].float().numpy()
-            _, qs = orc.pool(qh, qps, dt)
-            heads += 1
-            for J in rng.permutation(nqb):
-                J = int(J)
-                c0 = (J * qps) // wl.chunk_size * (wl.chunk_size // qps)
-                ncc = min(wl.chunk_size // qps, nqb - c0)
-                cnt, lists = orc.select(qs, kh, c0, ncc, gaps, qps, wl.k_local_size,
-                                        wl.group_k_block, wl.causal, wl.causal, 64,
-                                        rows=(J - c0, J - c0 + 1))
-                orc.attention(qh, kh, vh, qps, wl.causal, bc, bi,
-                              [[lists[0][0][J - c0:J - c0 + 1]]], J0=J, nc=1, acc=np.float32)
-                rows = min(qps, S - J * qps)
-                flops += 4.0 * D * rows * (int(cnt[0, 0, J - c0]) + local_keys(J, qps, Sk, wl.causal))
-                done += 1
-                if time.perf_counter() - t0 > seconds and done >= 4:
-                    break
-            if time.perf_counter() - t0 > seconds and done >= 4:
-                break
-    el = time.perf_counter() - t0
-    return {"value": flops / el / 1e12, "unit": "TFLOP/s", "cores": 1, "kind": "port",
-            "sample": f"oracle (C selection, numpy fp32 attention) on {done} random q-blocks of "
-                      f"{heads} head(s) of workload {wl.name}, {el:.1f} s",
-            "host_cpu": platform.processor() or platform.machine(),
+            np.save(os.path.join(tmp, f"q_{h}.npy"), qh[0, 0])
+            np.save(os.path.join(tmp, f"qs_{h}.npy"), orc.pool(qh, qps, dt)[1][0, 0])
+        for g in sorted({h // rep for h in heads}):
+            np.save(os.path.join(tmp, f"k_{g}.npy"), k_cpu[0, g].float().numpy())
+            np.save(os.path.join(tmp, f"v_{g}.npy"), v_cpu[0, g].float().numpy())
+        meta = {"qps": qps, "bk": wl.k_local_size, "G": wl.group_k_block, "causal": wl.causal,
+                "chunk": wl.chunk_size, "S": S, "Sk": k_cpu.shape[2], "D": D, "rep": rep,
+                "threshold": threshold, "samples": samples}
+        with open(os.path.join(tmp, "meta.json"), "w") as f:
+            _json.dump(meta, f)
+        env = dict(os.environ, OMP_NUM_THREADS="1", OPENBLAS_NUM_THREADS="1",
+                   MKL_NUM_THREADS="1", HIP_VISIBLE_DEVICES="", CUDA_VISIBLE_DEVICES="")
+        procs = [subprocess.Popen([sys.executable, "-m", "oracle.sample_worker", tmp, str(w), str(n),
+                                   str(seconds)], cwd=ROOT, env=env, stdout=subprocess.PIPE,
+                                  text=True) for w in range(n)]
+        res = []
+        for p in procs:
+            out, _ = p.communicate()
+            if p.returncode != 0:
+                raise RuntimeError(f"cpu baseline worker exited with {p.returncode}")
+            res.append(_json.loads(out.strip().splitlines()[-1]))
+    finally:
+        shutil.rmtree(tmp, ignore_errors=True)
+    flops = sum(r["flops"] for r in res)
+    blocks = sum(r["blocks"] for r in res)
+    el = max(r["elapsed"] for r in res)
+    t_sel = sum(r["t_sel"] for r in res)
+    t_attn = sum(r["t_attn"] for r in res)
+    return {"value": flops / el / 1e12, "unit": "TFLOP/s", "cores": n, "kind": "port",
+            "sample": f"oracle (C selection, numpy fp32 attention) on {blocks} q-blocks drawn "
+                      f"uniformly over q heads {heads} and all {nqb} q-blocks of workload "
+                      f"{wl.name}, {n} processes x {el:.1f} s",
+            "selection_s_per_qblock": round(t_sel / max(blocks, 1), 5),
+            "attention_s_per_qblock": round(t_attn / max(blocks, 1), 5),
+            "host_cpu": host_cpu_model(),
             "host_threads_available": len(os.sched_getaffinity(0))}
 
 
@@ -486,24 +548,13 @@ def bench_decode(args, wl, dev):
 
 # --------------------------------------------------------------------- main --
 
-def main():
-    args = parse()
-    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for "
-              f"--gpus {args.gpus}); per-GPU sharding is by (batch, kv head) and needs no "
-              f"collective (see DESIGN.md).", file=sys.stderr)
-        sys.exit(2)
+def measure_prefill(args, wl, dev, with_cpu):
+    """Measure one workload: calibrated threshold, stage timing, the timed
+    VecAttention_prefill steps, the dense baselines and (optionally) the CPU
+    baseline.  Returns the result dictionary of the JSON line."""
     from vecattention_amd import VecAttention_prefill
-    from vecattention_amd.synth import WORKLOADS, workload_inputs
+    from vecattention_amd.synth import workload_inputs
 
-    wl = WORKLOADS[args.config]
-    dev = torch.device("cuda:0")
-    if args.tuner:
-        bench_tuner(args, wl, dev)
-        return
-    if args.decode:
-        bench_decode(args, wl, dev)
-        return
     t_gen = time.perf_counter()
     q_cpu, k_cpu, v_cpu = workload_inputs(wl, seed=0)
     q, k, v = q_cpu.to(dev), k_cpu.to(dev), v_cpu.to(dev)
@@ -567,6 +618,7 @@ def main():
     # value: the whole VecAttention_prefill step, as timed above
     e2e_tflops = F_attn / (ms_per_step * 1e-3) / 1e12
     attn_tflops = F_attn / (t_attn * 1e-3) / 1e12
+    traffic = profiled_traffic(wl.name, "attn_mfma_kernel")
     result = {
         "metric": METRIC,
         "value": round(e2e_tflops, 3),
@@ -601,11 +653,52 @@ def main():
         "roofline": {"bound": "mfma", "kernel": "attn_mfma_kernel",
                      "achieved": round(attn_tflops, 3), "peak": BF16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(attn_tflops / BF16_PEAK_TFLOPS, 4),
-                     "traffic": profiled_traffic(wl.name, "attn_mfma_kernel")},
+                     "traffic": traffic,
+                     "traffic_kind": "L2-to-fabric bytes per launch (FETCH_SIZE + WRITE_SIZE, "
+                                     "copy-calibrated; Infinity Cache hits included)"},
         "flops": {"attn_executed": F_attn, "dense": F_dense},
     }
-    if not args.no_cpu:
-        result["cpu_baseline"] = cpu_baseline(wl, q_cpu, k_cpu, v_cpu, th, args.cpu_seconds)
+    if with_cpu:
+        result["cpu_baseline"] = cpu_baseline(wl, q_cpu, k_cpu, v_cpu, th, args.cpu_seconds,
+                                              args.cpu_workers)
+    del q, k, v, out
+    torch.cuda.empty_cache()
+    return result
+
+
+EXTRA_KEYS = ("ms_per_step", "value", "config", "latency_ms", "sparse_attn_tflops", "selection_gbs",
+              "selection_hbm_frac", "dense_ms", "dense_backend", "speedup_vs_dense", "dense_va_ms",
+              "dense_va_tflops", "speedup_vs_dense_va", "roofline", "flops")
+
+
+def main():
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for "
+              f"--gpus {args.gpus}); per-GPU sharding is by (batch, kv head) and needs no "
+              f"collective (see DESIGN.md).", file=sys.stderr)
+        sys.exit(2)
+    from vecattention_amd.synth import WORKLOADS
+
+    wl = WORKLOADS[args.config]
+    dev = torch.device("cuda:0")
+    if args.tuner:
+        bench_tuner(args, wl, dev)
+        return
+    if args.decode:
+        bench_decode(args, wl, dev)
+        return
+    extra = args.extra if args.extra is not None else ("B" if args.config == "C" else "none")
+    extra = [] if extra.lower() == "none" else [x for x in extra.split(",") if x]
+    result = measure_prefill(args, wl, dev, with_cpu=not args.no_cpu)
+    if extra:
+        saved_th = args.threshold
+        args.threshold = None  # each extra workload calibrates its own threshold
+        result["extra_workloads"] = {}
+        for key in extra:
+            r = measure_prefill(args, WORKLOADS[key], dev, with_cpu=False)
+            result["extra_workloads"][r["config"]["workload"]] = {k: r[k] for k in EXTRA_KEYS}
+        args.threshold = saved_th
     line = json.dumps(result)
     print(line, flush=True)
     if args.extra_json:

@@ -23,18 +23,23 @@ Pieces and the reference lines they restate:
                       recall / sparsity evaluation: dense softmax per head,
                       boolean mask of local blocks and selected columns)
 
-Pinning (tests/test_oracle.py): closed forms for pooling and gap; hand-derived
+Pinning (tests/test_oracle.py): closed forms for pooling and gap (the tensor
+branch against torch's evaluation of the reference expression); hand-derived
 known answers for the selection rule (prefix maximum updated before the
-compare, group restarts, causal first-row tile rule, key tail); an
-independent brute force on exactly representable inputs; invariants (large
-gap selects every selectable key; larger gap selects a superset; chunk-size
-invariance; single-group equivalence); attention against torch's dense SDPA
-in float64 where the sparse set is all keys.
+compare, group restarts, causal first-row tile rule, key tail); a brute force
+written from the reference kernel's program structure (grid of BLOCK_SIZE_Q
+rows x groups, per-program tile range, running maximum per row, truncating
+causal division) on small-integer inputs whose scores are exact, over random
+tile sizes, groups, chunk origins, BLOCK_SIZE_Q and key tails; invariants
+(large gap selects every selectable key; larger gap selects a superset;
+chunk-size invariance; single-group equivalence); attention against torch's
+dense SDPA in float64 where the sparse set is all keys.
 """
 import ctypes
 import math
 import os
 import subprocess
+import sys
 
 import numpy as np
 
@@ -82,13 +87,12 @@ def dtype_code(name):
 
 
 def as_f32(x):
-    """torch tensor or array -> contiguous float32 numpy array (exact for bf16/fp16)."""
-    try:
-        import torch
-        if isinstance(x, torch.Tensor):
-            return np.ascontiguousarray(x.detach().float().cpu().numpy())
-    except ImportError:
-        pass
+    """torch tensor or array -> contiguous float32 numpy array (exact for bf16/fp16).
+    A torch tensor can only come from a caller that imported torch, so torch is
+    looked up, not imported (numpy-only callers stay free of it)."""
+    torch = sys.modules.get("torch")
+    if torch is not None and isinstance(x, torch.Tensor):
+        return np.ascontiguousarray(x.detach().float().cpu().numpy())
     return np.ascontiguousarray(np.asarray(x, dtype=np.float32))
 
 
@@ -105,12 +109,22 @@ def pool(q, qps, dtype):
 
 
 def gap_from_threshold(threshold, B, H):
-    """fp32 gap per (b, h) as spattn/src/VecAttention.py:48-52 (float branch:
-    -ln(th + 1e-9) in double, then fp32)."""
+    """fp32 gap per (b, h) as spattn/src/VecAttention.py:48-52.
+
+    Float branch: -ln(th + 1e-9) in double, then fp32 (the reference passes a
+    Python float).  Tensor branch, -log(threshold + 1e-9) on an fp32 tensor:
+    the fp32 sum, then the correctly rounded fp32 value of its logarithm (fp64
+    log, one rounding).  The reference evaluates the logarithm in fp32 on its
+    GPU, whose result is within one unit in the last place of this value; the
+    last bit of a per-head gap is therefore not pinned by the reference.
+    (numpy's float32 log is not correctly rounded: it is off by one unit for
+    about one threshold in six, so it is not used.)
+    """
     if np.ndim(threshold) == 0:
         return np.full(B * H, np.float32(-math.log(float(threshold) + 1e-9)), np.float32)
     t = np.asarray(threshold, np.float32)
-    g = (-np.log(t + np.float32(1e-9))).astype(np.float32)
+    s = (t + np.float32(1e-9)).astype(np.float32)
+    g = (-np.log(s.astype(np.float64))).astype(np.float32)
     return np.ascontiguousarray(np.broadcast_to(g, (B, H)).reshape(-1))
 
 
@@ -184,9 +198,9 @@ def attention(q, k, v, qps, causal, blk_count, blk_idx, lists, J0=0, nc=None, ac
     Causal alignment is bottom-right (row i of the query sequence sees keys
     <= i + Sk - Sq), as for each chunk of the reference.
     """
-    q = as_f32(q).astype(acc)
-    k = as_f32(k).astype(acc)
-    v = as_f32(v).astype(acc)
+    q = as_f32(q).astype(acc, copy=False)
+    k = as_f32(k).astype(acc, copy=False)
+    v = as_f32(v).astype(acc, copy=False)
     B, Hq, Sq, D = q.shape
     Hk, Sk = k.shape[1], k.shape[2]
     rep = Hq // Hk
@@ -218,12 +232,16 @@ def attention(q, k, v, qps, causal, blk_count, blk_idx, lists, J0=0, nc=None, ac
 
 
 def prefill(q, k, v, threshold, q_pooling_size=128, k_local_size=128, group_k_block=1,
-            causal=True, chunk_size=16 * 1024, bsq=64, dtype="bfloat16", acc=np.float64):
-    """Whole-path oracle: returns (out (B,Hq,S,D) in `acc`, per-chunk (counts, lists))."""
+            causal=True, chunk_size=16 * 1024, bsq=64, dtype="bfloat16", acc=np.float64,
+            gaps=None):
+    """Whole-path oracle: returns (out (B,Hq,S,D) in `acc`, per-chunk (counts, lists)).
+    `gaps` (fp32, B*Hq) replaces the gaps derived from `threshold` when given."""
     q, k, v = as_f32(q), as_f32(k), as_f32(v)
     B, Hq, S, D = q.shape
     Sk = k.shape[2]
-    gaps = gap_from_threshold(threshold, B, Hq)
+    if gaps is None:
+        gaps = gap_from_threshold(threshold, B, Hq)
+    gaps = np.ascontiguousarray(np.asarray(gaps, np.float32).reshape(-1))
     _, qs = pool(q, q_pooling_size, dtype)
     blk_count, blk_idx = local_blocks(B, Hq, S, q_pooling_size, causal)
     out = np.zeros((B, Hq, S, D), acc)
@@ -248,9 +266,10 @@ def seg_pr_perhead(q, k, block_size_q, block_size_k=16, group_size_k=16, thresho
     """(recall (H,), sparsity (H,)) in float64, restating model_tuner.py:118-226.
 
     q (B,H,S,D), k (B,Hk,Sk,D) float values of element type `dtype`;
-    threshold: per-head (H,) values.  gap = -log(th + 1e-50) in fp32
-    (model_tuner.py:150; 1e-50 is 0 in fp32).  Per chunk: pooled rows,
-    selection with wo_initial=causal (:183-187), then per (b, h) the dense
+    threshold: per-head (H,) values.  gap = -log(th + 1e-50) (model_tuner.py:150;
+    1e-50 is 0 in fp32): the fp32 sum, its log in fp64, rounded once to fp32.
+    Per chunk: pooled rows, selection with wo_initial=causal (:183-187), then
+    per (b, h) the dense
     softmax with the top-left causal mask (:139-143,193-199), the boolean mask
     of the blocks [off, min(off+64, Sk)) and the selected columns (:201-216),
     recall = masked row sums (:216,220) and sparsity += (1 - mean(mask count /
@@ -263,7 +282,8 @@ def seg_pr_perhead(q, k, block_size_q, block_size_k=16, group_size_k=16, thresho
     rep = H // Hk
     th = np.asarray(threshold, np.float32)
     with np.errstate(divide="ignore"):
-        gap = (-np.log(th + np.float32(1e-50))).astype(np.float32)
+        summed = (th + np.float32(1e-50)).astype(np.float32)
+        gap = (-np.log(summed.astype(np.float64))).astype(np.float32)
     gaps = np.ascontiguousarray(np.broadcast_to(gap, (B, H)).reshape(-1), np.float32)
     _, qs = pool(q.astype(np.float32), block_size_q, dtype)
     blk_count, blk_idx = local_blocks(B, H, S, block_size_q, causal)

@@ -28,8 +28,9 @@
  *               before the compare, truncating causal tile mask, NaN tail).
  *
  * Parity status: pinned by the checks in tests/test_oracle.py (closed forms,
- * hand-derived known answers, an independent brute force on exactly
- * representable inputs, and the invariants listed there).
+ * hand-derived known answers, a brute force written from the reference
+ * kernel's program structure on small-integer inputs whose scores are exact,
+ * and the invariants listed there).
  */
 #include <math.h>
 #include <stdint.h>

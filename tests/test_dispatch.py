@@ -32,6 +32,8 @@ def test_threshold_matrix_round_trip(tmp_path):
     ({"a": 1}, 2, 3),                  # not a list
     ([[0.1, 0.2, 0.3]], 2, 3),         # wrong layer count
     ([[0.1, 0.2], [0.3, 0.4]], 2, 3),  # wrong head count
+    ([[0.1, 0.2, 0.3], [0.4]], 2, 3),  # a later layer with the wrong head count
+    ([[0.1, 0.2, 0.3], 0.5], 2, 3),    # a layer that is not a list
 ])
 def test_threshold_matrix_errors(tmp_path, content, layers, heads):
     p = tmp_path / "bad.json"

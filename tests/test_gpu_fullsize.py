@@ -1,14 +1,17 @@
-"""Size-independent properties at the full sequence lengths of configs C
-(131072 keys, causal, GQA, chunks of 32768) and E (119056 keys, non-causal,
-one group per row, two-pass split selection), on a subset of heads (heads are
-independent: one kv group of C, two heads of E).  Run on an MI355X.
+"""Parity at the full sequence lengths of configs C (131072 keys, causal, GQA,
+chunks of 32768), D (32760 keys, non-causal, one group per row, two-pass split
+selection, a 56-row last q-block) and E (119056 keys, non-causal, two-pass
+split selection), on a subset of heads (heads are independent: one kv group
+of C, two heads of D and of E).  Run on an MI355X.
 
 - gap 1e6 selects every selectable key: counts equal the closed form, through
   the split (segmented) selection that VecAttention_prefill runs;
-- sampled rows of the full prefill: selection bit-exact and attention within
-  the north-star tolerance of the oracle;
-- the certified split selection equals the exact fp64 kernel on every row of
-  a chunk;
+- sampled rows: the split selection's lists (the ones the prefill's attention
+  reads) equal the oracle's bit for bit, at the threshold calibrated to the
+  workload's keep ratio and at a fixed one, and the prefill output of those
+  rows is within the north-star tolerance of the oracle;
+- the two-pass split selection equals the exact fp64 kernel on every row of a
+  chunk;
 - chunk-size invariance where the reference's rule makes it hold.
 """
 import math
@@ -18,10 +21,11 @@ import pytest
 import torch
 
 from oracle import oracle as orc
+from seglists import calibrate_threshold, pooled_oracle, select_chunk
 from vecattention_amd import VecAttention_prefill
 from vecattention_amd import _native as nat
 from vecattention_amd import stages
-from vecattention_amd.synth import make_inputs
+from vecattention_amd.synth import WORKLOADS, make_inputs
 
 pytestmark = pytest.mark.gpu
 
@@ -37,26 +41,57 @@ def segment_totals(counts):
     return counts.sum(dim=-1)
 
 
+def check_rows(q, k, v, qs_dev, kd, out_cpu, heads, rows, th, causal, G, chunk_rows=512,
+               qps=64, bk=16, rep=1):
+    """For each sampled (head, q-block J): the split selection's list equals
+    the oracle's, and the prefill output rows are within tolerance."""
+    S, Sk = q.shape[2], k.shape[2]
+    nqb = -(-S // qps)
+    gap = -math.log(th + 1e-9)
+    gaps = orc.gap_from_threshold(th, 1, 1)
+    bc, bi = orc.local_blocks(1, 1, S, qps, causal)
+    by_chunk = {}
+    for J in rows:
+        by_chunk.setdefault(J // chunk_rows * chunk_rows, []).append(J)
+    for J0, Js in sorted(by_chunk.items()):
+        nc = min(chunk_rows, nqb - J0)
+        gpu = select_chunk(qs_dev, kd, J0, nc, gap, causal, qps, bk, G)
+        for h in heads:
+            hk = h // rep
+            qh, kh, vh = q[:, h:h + 1], k[:, hk:hk + 1], v[:, hk:hk + 1]
+            qs = pooled_oracle(qh, qps)
+            for J in Js:
+                _, lists = orc.select(qs, kh, J0, nc, gaps, qps, bk, G, causal, causal, 64,
+                                      rows=(J - J0, J - J0 + 1))
+                want_list = lists[0][0][J - J0]
+                got_list = gpu.row(0, h, J - J0)
+                if not np.array_equal(got_list, want_list):
+                    diff = sorted(set(got_list.tolist()) ^ set(want_list.tolist()))[:10]
+                    raise AssertionError(f"h={h} J={J}: {len(got_list)} vs {len(want_list)} "
+                                         f"keys, differ at {diff}")
+                if out_cpu is not None:
+                    want = orc.attention(qh, kh, vh, qps, causal, bc, bi, [[[want_list]]], J0=J,
+                                         nc=1)
+                    r0, r1 = J * qps, min(S, (J + 1) * qps)
+                    err = np.abs(out_cpu[0, h, r0:r1] - want[0, 0])
+                    assert err.max() <= ATOL_MAX and err.mean() <= ATOL_MEAN, (h, J, err.max())
+
+
+# ------------------------------------------------------------------ config C --
+
 @pytest.fixture(scope="module")
 def config_c():
     # one kv group of C: 7 q heads over 1 kv head, 131072 keys
     q, k, v = make_inputs(1, 7, 1, 131072, 128, torch.bfloat16, seed=0)
-    return q, k, v, q.to(DEV), k.to(DEV), v.to(DEV)
-
-
-@pytest.fixture(scope="module")
-def config_e():
-    # two heads of E: 119056 keys, text tokens last, 33 frames of 3600 tokens
-    q, k, v = make_inputs(1, 2, 2, 119056, 128, torch.bfloat16, seed=0, sinks="text_last",
-                          frames=(33, 3600), text_tokens=256)
-    return q, k, v, q.to(DEV), k.to(DEV), v.to(DEV)
+    qd = q.to(DEV)
+    qs, _ = stages.pool_scaled(qd, 64)
+    return q, k, v, qd, k.to(DEV), v.to(DEV), qs
 
 
 def test_c_large_gap_selects_every_selectable_key(config_c):
     note("C all selectable")
-    _, _, _, qd, kd, _ = config_c
+    _, _, _, qd, kd, _, qs = config_c
     qps, S = 64, 131072
-    qs, _ = stages.pool_scaled(qd, qps)
     segk = stages.segment_keys(S, 16, 16)
     for J0 in (0, 1536):  # first and last 32K chunk
         cnt, _ = stages.select_segments(qs[:, :, J0:J0 + 512], kd, J0, 1e6, None, True, qps, 16,
@@ -68,42 +103,110 @@ def test_c_large_gap_selects_every_selectable_key(config_c):
         assert torch.equal(segment_totals(cnt).cpu(), want.to(torch.int64).expand(1, 7, 512))
 
 
-def test_c_sampled_rows_match_oracle(config_c):
-    note("C sampled rows")
-    q, k, v, qd, kd, vd = config_c
-    qps, S, th = 64, 131072, 0.84
-    out = VecAttention_prefill(qd, kd, vd, th, qps, 16, 16, True, 32768)
+@pytest.mark.parametrize("th", ["calibrated", 0.84])
+def test_c_sampled_rows_match_oracle(config_c, th):
+    q, k, v, qd, kd, vd, qs = config_c
+    if th == "calibrated":
+        th = calibrate_threshold(qs, kd, True, 64, 16, 16, WORKLOADS["C"].keep)
+    note("C sampled rows, threshold", th)
+    out = VecAttention_prefill(qd, kd, vd, th, 64, 16, 16, True, 32768)
     torch.cuda.synchronize()
     out_cpu = out.float().cpu().numpy()
-    gaps = orc.gap_from_threshold(th, 1, 1)
     rng = np.random.default_rng(1)
-    for h in (0, 6):
-        qh = q[:, h:h + 1]
-        _, qs = orc.pool(qh, qps, "bfloat16")
-        for J in sorted(rng.choice(np.arange(1536, 2048), 3, replace=False).tolist()) + [2047]:
-            _, lists = orc.select(qs, k, 1536, 512, gaps, qps, 16, 16, True, True, 64,
-                                  rows=(J - 1536, J - 1535))
-            bc, bi = orc.local_blocks(1, 1, S, qps, True)
-            row = lists[0][0][J - 1536]
-            want = orc.attention(qh, k, v, qps, True, bc, bi, [[[row]]], J0=J, nc=1)
-            err = np.abs(out_cpu[0, h, J * qps:(J + 1) * qps] - want[0, 0])
-            assert err.max() <= ATOL_MAX and err.mean() <= ATOL_MEAN, (h, J, err.max())
+    # rows of the first and the last chunk; 0 and 64 are first rows of a
+    # program (the causal first-row rule), 2047 is the longest row
+    rows = [1, 64] + sorted(rng.choice(np.arange(1536, 2048), 3, replace=False).tolist()) + [2047]
+    check_rows(q, k, v, qs, kd, out_cpu, (0, 6), rows, th, True, 16, rep=7)
 
 
 def test_c_chunking_invariant(config_c):
     # 16K and 32K chunks both start programs at multiples of 64 q-blocks
     note("C chunk invariance")
-    _, _, _, qd, kd, vd = config_c
+    _, _, _, qd, kd, vd, _ = config_c
     a = VecAttention_prefill(qd, kd, vd, 0.84, 64, 16, 16, True, 32768)
     b = VecAttention_prefill(qd, kd, vd, 0.84, 64, 16, 16, True, 16384)
     assert torch.equal(a, b)
 
 
+# ------------------------------------------------------------------ config D --
+
+@pytest.fixture(scope="module")
+def config_d():
+    # two heads of D: 32760 keys (21 frames of 1560 tokens), 512 q-blocks, the
+    # last of 56 rows
+    q, k, v = make_inputs(1, 2, 2, 32760, 128, torch.bfloat16, seed=0, frames=(21, 1560))
+    qd = q.to(DEV)
+    qs, _ = stages.pool_scaled(qd, 64)
+    return q, k, v, qd, k.to(DEV), v.to(DEV), qs
+
+
+def test_d_runs_two_pass_split():
+    # one group per row (G*BK >= Sk): the segments carry the running maximum
+    segk = stages.segment_keys(32760, 16, 8192)
+    assert segk == 4096
+    assert 16 * 8192 >= 32760
+
+
+def test_d_large_gap_selects_every_key(config_d):
+    note("D all keys")
+    _, _, _, _, kd, _, qs = config_d
+    S = 32760
+    segk = stages.segment_keys(S, 16, 8192)
+    cnt, _ = stages.select_segments(qs, kd, 0, 1e6, None, False, 64, 16, 8192, False, segk)
+    assert torch.equal(segment_totals(cnt).cpu(), torch.full((1, 2, 512), S, dtype=torch.int64))
+
+
+@pytest.mark.parametrize("th", ["calibrated", 0.3])
+def test_d_sampled_rows_match_oracle(config_d, th):
+    q, k, v, qd, kd, vd, qs = config_d
+    if th == "calibrated":
+        th = calibrate_threshold(qs, kd, False, 64, 16, 8192, WORKLOADS["D"].keep)
+    note("D sampled rows, threshold", th)
+    out = VecAttention_prefill(qd, kd, vd, th, 64, 16, 8192, False, 32768)
+    torch.cuda.synchronize()
+    out_cpu = out.float().cpu().numpy()
+    rng = np.random.default_rng(2)
+    rows = [0] + sorted(rng.choice(np.arange(1, 511), 5, replace=False).tolist()) + [511]
+    check_rows(q, k, v, qs, kd, out_cpu, (0, 1), rows, th, False, 8192)
+
+
+def test_d_split_selection_equals_exact_kernel(config_d):
+    note("D split == exact")
+    _, _, _, _, kd, _, qs = config_d
+    S = 32760
+    gap = -math.log(0.3 + 1e-9)
+    segk = stages.segment_keys(S, 16, 8192)
+    c1, i1 = stages.select_rows(qs, kd, 0, gap, None, False, 64, 16, 8192, False,
+                                kernel=nat.VA_SEL_EXACT)
+    c2, i2 = stages.select_segments(qs, kd, 0, gap, None, False, 64, 16, 8192, False, segk)
+    c1n, c2n = c1.cpu().numpy(), c2.cpu().numpy()
+    assert np.array_equal(c1n, c2n.sum(axis=-1))
+    a, b = i1.cpu().numpy(), i2.cpu().numpy()
+    nseg = c2n.shape[-1]
+    for h in range(2):
+        for jr in range(512):
+            o = stages.row_offset(S, 64, False, False, 0, 512, h, jr)
+            split = np.concatenate([b[o + s * segk:o + s * segk + c2n[0, h, jr, s]]
+                                    for s in range(nseg)])
+            assert np.array_equal(a[o:o + c1n[0, h, jr]], split), (h, jr)
+
+
+# ------------------------------------------------------------------ config E --
+
+@pytest.fixture(scope="module")
+def config_e():
+    # two heads of E: 119056 keys, text tokens last, 33 frames of 3600 tokens
+    q, k, v = make_inputs(1, 2, 2, 119056, 128, torch.bfloat16, seed=0, sinks="text_last",
+                          frames=(33, 3600), text_tokens=256)
+    qd = q.to(DEV)
+    qs, _ = stages.pool_scaled(qd, 64)
+    return q, k, v, qd, k.to(DEV), v.to(DEV), qs
+
+
 def test_e_large_gap_selects_every_key(config_e):
     note("E all keys")
-    _, _, _, qd, kd, _ = config_e
+    _, _, _, _, kd, _, qs = config_e
     qps, S = 64, 119056
-    qs, _ = stages.pool_scaled(qd, qps)
     segk = stages.segment_keys(S, 16, 8192)
     nqb = qs.shape[2]
     for J0 in (0, 1536):  # the first chunk and the partial last one
@@ -117,9 +220,8 @@ def test_e_split_selection_equals_exact_kernel(config_e):
     # the two-pass split selection (maxima pass + carry pass) against the fp64
     # kernel on every row of the last chunk, as index sets per row
     note("E split == exact")
-    _, _, _, qd, kd, _ = config_e
+    _, _, _, _, kd, _, qs = config_e
     qps, S = 64, 119056
-    qs, _ = stages.pool_scaled(qd, qps)
     nqb = qs.shape[2]
     J0 = 3 * 512
     nc = nqb - J0
@@ -142,26 +244,14 @@ def test_e_split_selection_equals_exact_kernel(config_e):
             assert np.array_equal(exact, split), (h, jr)
 
 
-def test_e_sampled_rows_match_oracle(config_e):
-    note("E sampled rows")
-    q, k, v, qd, kd, vd = config_e
-    qps, S, th = 64, 119056, 0.43
-    out = VecAttention_prefill(qd, kd, vd, th, qps, 16, 8192, False, 32768)
+@pytest.mark.parametrize("th", ["calibrated", 0.43])
+def test_e_sampled_rows_match_oracle(config_e, th):
+    q, k, v, qd, kd, vd, qs = config_e
+    if th == "calibrated":
+        th = calibrate_threshold(qs, kd, False, 64, 16, 8192, WORKLOADS["E"].keep)
+    note("E sampled rows, threshold", th)
+    out = VecAttention_prefill(qd, kd, vd, th, 64, 16, 8192, False, 32768)
     torch.cuda.synchronize()
     out_cpu = out.float().cpu().numpy()
-    gaps = orc.gap_from_threshold(th, 1, 1)
-    nqb = -(-S // qps)
-    bc, bi = orc.local_blocks(1, 1, S, qps, False)
-    for h in (0, 1):
-        qh, kh, vh = q[:, h:h + 1], k[:, h:h + 1], v[:, h:h + 1]
-        _, qs = orc.pool(qh, qps, "bfloat16")
-        for J in (0, 700, 1537, nqb - 1):
-            J0 = (J // 512) * 512
-            nc = min(512, nqb - J0)
-            _, lists = orc.select(qs, kh, J0, nc, gaps, qps, 16, 8192, False, False, 64,
-                                  rows=(J - J0, J - J0 + 1))
-            row = lists[0][0][J - J0]
-            want = orc.attention(qh, kh, vh, qps, False, bc, bi, [[[row]]], J0=J, nc=1)
-            r0, r1 = J * qps, min(S, (J + 1) * qps)
-            err = np.abs(out_cpu[0, h, r0:r1] - want[0, 0])
-            assert err.max() <= ATOL_MAX and err.mean() <= ATOL_MEAN, (h, J, err.max())
+    nqb = qs.shape[2]
+    check_rows(q, k, v, qs, kd, out_cpu, (0, 1), [0, 700, 1537, nqb - 1], th, False, 8192)

@@ -15,7 +15,8 @@ from oracle import oracle as orc
 from vecattention_amd import VecAttention_prefill
 from vecattention_amd import _native as nat
 from vecattention_amd import stages
-from vecattention_amd.synth import make_inputs
+from seglists import SegmentedLists, calibrate_threshold, select_chunk
+from vecattention_amd.synth import WORKLOADS, make_inputs
 
 pytestmark = pytest.mark.gpu
 
@@ -405,6 +406,59 @@ def test_vecattention_prefill_matches_oracle(device, case):
     assert err.max() <= tol[0] and err.mean() <= tol[1], (err.max(), err.mean())
 
 
+def _device_gaps(th, B, Hq, device):
+    """The fp32 gaps VecAttention_prefill computes on the device for a
+    threshold tensor (-torch.log(th + 1e-9) there), as a host array."""
+    from vecattention_amd.vecattention import threshold_to_gap
+    _, g = threshold_to_gap(th.to(device), B, Hq, device)
+    return g.reshape(-1).cpu().numpy()
+
+
+def _ulps(a, b):
+    return np.abs(a.view(np.int32).astype(np.int64) - b.view(np.int32).astype(np.int64))
+
+
+def test_device_gaps_equal_oracle(device):
+    # The gaps the prefill computes on the device for a threshold tensor are
+    # the oracle's (the correctly rounded fp32 of -log(th + 1e-9)) bit for bit.
+    th = torch.cat([torch.rand(4096, generator=torch.Generator().manual_seed(0)),
+                    torch.logspace(-7, 0, 4096)]).reshape(-1, 8)
+    g_dev = _device_gaps(th, th.shape[0], 8, device)
+    g_orc = orc.gap_from_threshold(th.numpy(), th.shape[0], 8)
+    d = _ulps(g_dev, g_orc)
+    note(f"device gaps: {int((d > 0).sum())} of {d.size} differ from the oracle "
+         f"(max {int(d.max())} ulp)")
+    assert d.max() == 0
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_per_head_gaps_select_bit_exact(device, causal):
+    # Per-head thresholds through the prefill's split selection: lists equal
+    # the oracle's, fed the gaps the product computed on the device.
+    note("per-head lists", causal)
+    B, Hq, Hk, S, D = 1, 4, 2, 9000, 128
+    q, k, v = make_inputs(B, Hq, Hk, S, D, torch.bfloat16, seed=6)
+    th = torch.tensor([0.9, 0.5, 0.1, 0.01])
+    gaps = _device_gaps(th, B, Hq, device)
+    G = 16 if causal else 8192
+    qd, kd = q.to(device), k.to(device)
+    qs_gpu, _ = stages.pool_scaled(qd, 64)
+    segk = stages.segment_keys(S, 16, G)
+    assert segk > 0
+    nqb = qs_gpu.shape[2]
+    _, qs = orc.pool(q, 64, "bfloat16")
+    for J0 in (0, 128):
+        nc = min(128, nqb - J0)
+        cnt, idx = stages.select_segments(qs_gpu[:, :, J0:J0 + nc], kd, J0, 0.0,
+                                          torch.from_numpy(gaps).to(device), causal, 64, 16, G,
+                                          causal, segk)
+        got = SegmentedLists(cnt, idx, J0, nc, 64, S, causal, causal, segk)
+        _, want = orc.select(qs, k, J0, nc, gaps, 64, 16, G, causal, causal, 64)
+        for h in range(Hq):
+            for jr in range(nc):
+                assert np.array_equal(got.row(0, h, jr), want[0][h][jr]), (J0, h, jr)
+
+
 def test_prefill_per_head_threshold_tensor(device):
     note("e2e per-head")
     B, Hq, S, D = 1, 4, 1024, 128
@@ -412,7 +466,8 @@ def test_prefill_per_head_threshold_tensor(device):
     th = torch.tensor([0.9, 0.5, 0.1, 0.01])
     out = VecAttention_prefill(q.to(device), k.to(device), v.to(device), th.to(device), 64, 16, 16,
                                False, 512)
-    want, _ = orc.prefill(q, k, v, th.numpy(), 64, 16, 16, False, 512, 64, "bfloat16")
+    want, _ = orc.prefill(q, k, v, th.numpy(), 64, 16, 16, False, 512, 64, "bfloat16",
+                          gaps=_device_gaps(th, B, Hq, device))
     err = np.abs(out.float().cpu().numpy() - want)
     assert err.max() <= ATOL_MAX and err.mean() <= ATOL_MEAN
 
@@ -425,7 +480,8 @@ def test_prefill_per_batch_and_head_threshold_tensor(device):
     th = torch.tensor([[0.9, 0.5, 0.1], [0.05, 0.3, 0.7]])
     out = VecAttention_prefill(q.to(device), k.to(device), v.to(device), th.to(device), 64, 16, 16,
                                True, 512)
-    want, _ = orc.prefill(q, k, v, th.numpy(), 64, 16, 16, True, 512, 64, "bfloat16")
+    want, _ = orc.prefill(q, k, v, th.numpy(), 64, 16, 16, True, 512, 64, "bfloat16",
+                          gaps=_device_gaps(th, B, Hq, device))
     err = np.abs(out.float().cpu().numpy() - want)
     assert err.max() <= ATOL_MAX and err.mean() <= ATOL_MEAN
 
@@ -449,30 +505,31 @@ def test_full_size_large_gap_selects_every_selectable_key(config_b):
     assert torch.equal(cnt.cpu(), want.to(torch.int32).expand(1, 28, nqb))
 
 
-def test_full_size_rows_match_oracle(config_b):
-    # Bit-exact selection and attention on sampled rows of the full 32K config.
-    note("full-size sampled rows")
+@pytest.mark.parametrize("th", ["calibrated", 0.35])
+def test_full_size_rows_match_oracle(config_b, th):
+    # Sampled rows of the full 32K config: the split selection's lists (the
+    # ones VecAttention_prefill's attention reads: 8 segments of 4096 keys)
+    # equal the oracle's bit for bit, and the prefill output is within tolerance.
     q, k, v, qd, kd, vd = config_b
     qps = 64
-    out = VecAttention_prefill(qd, kd, vd, 0.35, qps, 16, 16, True, 32768)
     qs_gpu, _ = stages.pool_scaled(qd, qps)
-    cnt, idx = stages.select_rows(qs_gpu, kd, 0, -math.log(0.35 + 1e-9), None, True, qps, 16, 16,
-                                  True)
+    if th == "calibrated":
+        th = calibrate_threshold(qs_gpu, kd, True, qps, 16, 16, WORKLOADS["B"].keep)
+    note("full-size sampled rows, threshold", th)
+    out = VecAttention_prefill(qd, kd, vd, th, qps, 16, 16, True, 32768)
+    gpu = select_chunk(qs_gpu, kd, 0, 512, -math.log(th + 1e-9), True, qps, 16, 16)
     torch.cuda.synchronize()
     out_cpu = out.float().cpu().numpy()
-    cnt_cpu, idx_cpu = cnt.cpu().numpy(), idx.cpu().numpy()
-    gaps = orc.gap_from_threshold(0.35, 1, 28)
+    gaps = orc.gap_from_threshold(th, 1, 28)
+    bc, bi = orc.local_blocks(1, 1, 32768, qps, True)
     rng = np.random.default_rng(0)
     for h in (0, 13, 27):
         qh, kh, vh = q[:, h:h + 1], k[:, h // 7:h // 7 + 1], v[:, h // 7:h // 7 + 1]
         _, qs = orc.pool(qh, qps, "bfloat16")
-        for J in sorted(rng.choice(np.arange(1, 512), 4, replace=False).tolist()) + [511]:
+        for J in [64] + sorted(rng.choice(np.arange(1, 512), 4, replace=False).tolist()) + [511]:
             _, lists = orc.select(qs, kh, 0, 512, gaps[:1], qps, 16, 16, True, True, 64,
                                   rows=(J, J + 1))
-            off = stages.row_offset(32768, qps, True, True, 0, 512, h, J)
-            c = cnt_cpu[0, h, J]
-            assert np.array_equal(idx_cpu[off:off + c], lists[0][0][J]), (h, J)
-            bc, bi = orc.local_blocks(1, 1, 32768, qps, True)
+            assert np.array_equal(gpu.row(0, h, J), lists[0][0][J]), (h, J)
             want = orc.attention(qh, kh, vh, qps, True, bc, bi, [[lists[0][0][J:J + 1]]], J0=J,
                                  nc=1)
             err = np.abs(out_cpu[0, h, J * qps:(J + 1) * qps] - want[0, 0])

@@ -95,6 +95,28 @@ def test_gap_closed_form():
     assert g[0] == np.float32(0.10536051541566849)
 
 
+def test_gap_tensor_branch_correctly_rounded():
+    # spattn/src/VecAttention.py:50: gap = -torch.log(threshold + 1e-9) on an
+    # fp32 tensor.  The oracle's per-head gaps are the correctly rounded fp32
+    # values of that expression: the fp32 sum, then ln in fp64 rounded once.
+    # Checked against an fp64 log of the sum computed with math.log (an
+    # independent libm path) and against torch's fp32 evaluation of the
+    # reference expression, which is faithful (within one unit in the last
+    # place).  (B, H) and (H,) shapes broadcast as in the kernel.
+    rng = np.random.default_rng(0)
+    th = np.concatenate([rng.random(4000), np.geomspace(1e-7, 1.0, 4000)]).astype(np.float32)
+    th = th.reshape(-1, 8)
+    g = orc.gap_from_threshold(th, th.shape[0], 8).reshape(th.shape)
+    s = (th + np.float32(1e-9)).astype(np.float32)
+    want = np.array([[np.float32(-math.log(float(x))) for x in row] for row in s], np.float32)
+    assert g.dtype == np.float32 and np.array_equal(g, want)
+    torch32 = (-torch.log(torch.from_numpy(th) + 1e-9)).numpy()
+    ulp = np.abs(g.view(np.int32).astype(np.int64) - torch32.view(np.int32).astype(np.int64))
+    assert ulp.max() <= 1
+    g1 = orc.gap_from_threshold(th[0], 3, 8).reshape(3, 8)
+    assert np.array_equal(g1, np.broadcast_to(want[0], (3, 8)))
+
+
 # -------------------------------------------------------- selection KATs ----
 
 def _select_scores(scores, gap, bk, group, causal=False, wo_init=False, qps=64, J0=0, bsq=64,

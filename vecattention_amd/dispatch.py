@@ -182,45 +182,60 @@ def select_cfg_threshold(config, step_ctx: DiffusionStepContext, layer_idx: int,
     step_ctx.pre_time_step = cur
 
 
+def _read_matrix_rows(path: str, num_layers: int, num_heads: int):
+    """Rows of a threshold matrix file: JSON holding one list of num_heads
+    numbers per layer.  Every row is checked, not only the first."""
+    with open(path, "r") as f:
+        doc = json.load(f)
+    if not isinstance(doc, list):
+        raise ValueError(f"expected a JSON list of layers, found {type(doc).__name__}")
+    if len(doc) != num_layers:
+        raise ValueError(f"{len(doc)} layers in the file, {num_layers} expected")
+    for layer, row in enumerate(doc):
+        if not isinstance(row, list) or len(row) != num_heads:
+            got = len(row) if isinstance(row, list) else type(row).__name__
+            raise ValueError(f"layer {layer}: {got} heads, {num_heads} expected")
+    return doc
+
+
 def _load_threshold_pt(thr_path: Optional[str], num_layers: int = NUM_LAYERS,
                        num_heads: int = NUM_HEADS,
                        device: torch.device = torch.device("cpu")) -> torch.Tensor:
-    """(num_layers, num_heads) fp32 threshold matrix from a JSON list of lists
-    (eval/DiTEvalKit/utils/misc.py:44-64); any problem raises RuntimeError."""
+    """Per-layer, per-head thresholds of a DiT model as a contiguous
+    (num_layers, num_heads) float32 tensor on `device`.
+
+    File format (the one eval/DiTEvalKit/utils/misc.py:44-64 reads): a JSON
+    list with one entry per layer, each a list of one threshold per head.
+    A missing or unreadable file, or one of another shape, raises
+    RuntimeError naming the file.
+    """
     try:
-        with open(thr_path, "r") as f:
-            thr_json = json.load(f)
-        if not isinstance(thr_json, list):
-            raise ValueError(f"Threshold matrix must be a list, got {type(thr_json)}")
-        if len(thr_json) != num_layers:
-            raise ValueError(f"Threshold matrix length must be {num_layers}, got {len(thr_json)}")
-        if len(thr_json[0]) != num_heads:
-            raise ValueError(f"Threshold matrix heads per layer must be {num_heads}, got {len(thr_json[0])}")
-        return torch.tensor(thr_json, dtype=torch.float32, device=device).contiguous()
-    except Exception as e:
-        raise RuntimeError(f"Cannot load threshold file {thr_path}: {e}")
+        rows = _read_matrix_rows(thr_path, num_layers, num_heads)
+        mat = torch.tensor(rows, dtype=torch.float32)
+    except (OSError, ValueError, TypeError) as err:
+        raise RuntimeError(f"threshold file {thr_path!r} unusable: {err}") from err
+    return mat.to(device).contiguous()
 
 
 def _save_threshold_pt(thr_path: str, thr_mat: Union[torch.Tensor, float],
                        num_layers: int = NUM_LAYERS) -> str:
-    """Save a per-layer threshold vector with torch.save
-    (eval/DiTEvalKit/utils/misc.py:67-93): a float or a 1-element tensor is
-    broadcast to (num_layers,); a (num_layers,) tensor is kept."""
-    valid = False
-    if not isinstance(thr_mat, torch.Tensor) and not isinstance(thr_mat, float):
-        raise TypeError(f"thr_mat must be Tensor or float, not {type(thr_mat)}")
+    """Write one threshold per layer with torch.save, as a (num_layers,)
+    float32 tensor (the file eval/DiTEvalKit/utils/misc.py:67-93 writes).
+
+    `thr_mat` is a Python float (the same value for every layer), a
+    one-element tensor (likewise) or a (num_layers,) tensor.  Other types
+    raise TypeError, other shapes ValueError.  Returns the path.
+    """
     if isinstance(thr_mat, float):
-        thr_mat = torch.full((num_layers,), thr_mat, dtype=torch.float32)
-        valid = True
-    elif thr_mat.ndim == 1:
-        if thr_mat.shape[0] == num_layers:
-            valid = True
-        elif thr_mat.shape[0] == 1:
-            thr_mat = thr_mat.repeat(num_layers)
-            valid = True
-    if not valid:
-        raise ValueError(f"thr_mat shape {thr_mat.shape} cannot be broadcast to ({num_layers})")
-    torch.save(thr_mat, thr_path)
+        vec = torch.full((num_layers,), thr_mat, dtype=torch.float32)
+    elif isinstance(thr_mat, torch.Tensor):
+        if thr_mat.dim() != 1 or thr_mat.numel() not in (1, num_layers):
+            raise ValueError(f"a threshold tensor of shape {tuple(thr_mat.shape)} does not give "
+                             f"one value per layer for {num_layers} layers")
+        vec = thr_mat.expand(num_layers).clone() if thr_mat.numel() == 1 else thr_mat
+    else:
+        raise TypeError(f"thresholds must be a float or a tensor, not {type(thr_mat).__name__}")
+    torch.save(vec, thr_path)
     return thr_path
 
 

@@ -35,9 +35,11 @@ def _bf16_exact(t):
 
 
 def _gaps(threshold, B, H, device):
-    """gap = -log(threshold + 1e-50) as model_tuner.py:150, in the threshold's
-    dtype (for fp32, 1e-50 rounds to 0), as fp32 per (b, h) for the selection."""
-    gap = -torch.log(threshold + 1e-50)
+    """gap = -log(threshold + 1e-50) as model_tuner.py:150: the sum in the
+    threshold's dtype (for fp32, 1e-50 rounds to 0), its logarithm in fp64
+    rounded once to fp32 (the correctly rounded value of the reference's fp32
+    logarithm), as fp32 per (b, h) for the selection."""
+    gap = -torch.log((threshold + 1e-50).to(torch.float64))
     gap = gap.to(device=device, dtype=torch.float32)
     if gap.dim() == 0:
         gap = gap.expand(B, H)

@@ -34,12 +34,16 @@ def threshold_to_gap(threshold, batch_size, num_heads, device):
     Returns (gap_scalar: float, gaps: fp32 device tensor of B*H or None).
     A float threshold gives gap = -ln(threshold + 1e-9) in double precision,
     consumed as fp32 by the kernel (the reference passes it as a Triton
-    constexpr).  A tensor threshold gives -log(threshold + 1e-9) evaluated by
-    torch in the tensor's dtype; a (H,) tensor is shared by every batch row and
-    a (B, H) tensor is used as is.
+    constexpr).  A tensor threshold gives -log(threshold + 1e-9): the sum in
+    the tensor's dtype, as the reference's expression, and the logarithm of
+    that sum in fp64, rounded once to fp32.  The reference evaluates the
+    logarithm in fp32 on its GPU; an fp32 logarithm is at best this correctly
+    rounded value, and the device's fp32 logarithm here is not always it (up
+    to two units in the last place off), so the gap is not taken from it.  A
+    (H,) tensor is shared by every batch row and a (B, H) tensor is used as is.
     """
     if isinstance(threshold, torch.Tensor):
-        gap = -torch.log(threshold + 1e-9)
+        gap = -torch.log((threshold + 1e-9).to(torch.float64))
         gap = gap.to(device=device, dtype=torch.float32)
         if gap.dim() == 0:
             gap = gap.expand(batch_size, num_heads)
