@@ -231,6 +231,24 @@ int va_decode_attn(int dtype, const void* q, int64_t sqh, const void* k, int64_t
                    void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
+ * va_decode_attn without a workspace: no counterpart in the reference.  For
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  Same arguments,
+ * kernels and results as va_decode_attn; the partial softmax states live in a
+ * device array inside the library, one per GPU, of
+ * va_decode_noalloc_scratch_bytes() bytes (8 MiB), held until the process
+ * ends.  Sizes whose va_decode_workspace_size() exceeds it return
+ * VA_ERR_UNSUPPORTED.  The entry point calls no allocator.  Calls on one GPU
+ * share the array: calls ordered on one stream are safe, calls that overlap
+ * on one GPU (unordered streams) race.
+ */
+int64_t va_decode_noalloc_scratch_bytes(void);
+int va_decode_attn_noalloc(int dtype, const void* q, int64_t sqh, const void* k, int64_t skh,
+                           int64_t sks, const void* v, int64_t svh, int64_t svs, void* out,
+                           int64_t soh, int64_t Hq, int64_t Hk, int64_t L, int64_t D,
+                           float softmax_scale, int kernel, void* stream);
+
+/*
  * va_sparse_attn on the segmented lists of va_select_segments (counts of shape
  * (B, Hq, nc, ceil(Sk/segment_keys))); MFMA kernel only.  No counterpart in
  * the reference: it is the second half of va_prefill's chunk step.

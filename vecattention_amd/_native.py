@@ -63,6 +63,9 @@ SIGNATURES = {
     "va_decode_workspace_size": (_i64, [_i64, _i64, _i64, _i64]),
     "va_decode_attn": (_int, [_int, _vp, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64,
                               _i64, _i64, _i64, _f32, _int, _vp, _i64, _vp]),
+    "va_decode_noalloc_scratch_bytes": (_i64, []),
+    "va_decode_attn_noalloc": (_int, [_int, _vp, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _vp,
+                                      _i64, _i64, _i64, _i64, _i64, _f32, _int, _vp]),
     "va_prefill_workspace_size": (_i64, [_int, _i64, _i64, _i64, _i64, _i64, _i64, _int, _i64]),
     "va_prefill": (_int, [_int, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _vp, _i64, _i64,
                           _i64, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _f32,

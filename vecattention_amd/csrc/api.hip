@@ -606,10 +606,26 @@ int64_t va_decode_workspace_size(int64_t Hq, int64_t Hk, int64_t L, int64_t D) {
   return align256(((2 * Hq * nsplit + 3) / 4 * 4 + Hq * nsplit * D) * 4);
 }
 
-int va_decode_attn(int dtype, const void* q, int64_t sqh, const void* k, int64_t skh,
-                   int64_t sks, const void* v, int64_t svh, int64_t svs, void* out, int64_t soh,
-                   int64_t Hq, int64_t Hk, int64_t L, int64_t D, float softmax_scale, int kernel,
-                   void* workspace, int64_t workspace_bytes, void* stream) {
+}  // extern "C"
+
+namespace va {
+
+int api_error(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+// Decode attention with the partial softmax states in `workspace`
+// (va_decode_attn, and the allocation-free variant with its static array).
+int decode_run(int dtype, const void* q, int64_t sqh, const void* k, int64_t skh, int64_t sks,
+               const void* v, int64_t svh, int64_t svs, void* out, int64_t soh, int64_t Hq,
+               int64_t Hk, int64_t L, int64_t D, float softmax_scale, int kernel,
+               void* workspace, int64_t workspace_bytes, void* stream) {
   if (!dtype_ok(dtype)) return fail(VA_ERR_ARG, "unknown dtype %d", dtype);
   if (!q || !k || !v || !out) return fail(VA_ERR_ARG, "null tensor pointer");
   if (Hq <= 0 || Hk <= 0 || L <= 0 || D <= 0) return fail(VA_ERR_ARG, "non-positive size");
@@ -662,6 +678,18 @@ int va_decode_attn(int dtype, const void* q, int64_t sqh, const void* k, int64_t
   rc = hip_check(va::launch_decode_merge(dtype, D, part, Hk, rep, nsplit, out, rep * soh, soh, st),
                  "decode merge launch");
   return rc ? rc : ok();
+}
+
+}  // namespace va
+
+extern "C" {
+
+int va_decode_attn(int dtype, const void* q, int64_t sqh, const void* k, int64_t skh,
+                   int64_t sks, const void* v, int64_t svh, int64_t svs, void* out, int64_t soh,
+                   int64_t Hq, int64_t Hk, int64_t L, int64_t D, float softmax_scale, int kernel,
+                   void* workspace, int64_t workspace_bytes, void* stream) {
+  return va::decode_run(dtype, q, sqh, k, skh, sks, v, svh, svs, out, soh, Hq, Hk, L, D,
+                        softmax_scale, kernel, workspace, workspace_bytes, stream);
 }
 
 // Workspace of va_prefill: [scaled pooled q][counts][indices][key norms]
