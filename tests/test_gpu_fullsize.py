@@ -12,7 +12,9 @@ of C, two heads of D and of E).  Run on an MI355X.
   rows is within the north-star tolerance of the oracle;
 - the two-pass split selection equals the exact fp64 kernel on every row of a
   chunk;
-- chunk-size invariance where the reference's rule makes it hold.
+- chunk-size invariance where the reference's rule makes it hold;
+- with all 28 heads of C, the prefill's causal row groups (the index buffer
+  holds one group of a chunk at a time) give the same output as whole chunks.
 """
 import math
 
@@ -126,6 +128,32 @@ def test_c_chunking_invariant(config_c):
     a = VecAttention_prefill(qd, kd, vd, 0.84, 64, 16, 16, True, 32768)
     b = VecAttention_prefill(qd, kd, vd, 0.84, 64, 16, 16, True, 16384)
     assert torch.equal(a, b)
+
+
+def test_c_all_heads_row_groups_equal_whole_chunks():
+    # All 28 q heads of C: VecAttention_prefill holds the lists of one row
+    # group of a chunk at a time (the last chunk's whole index capacity, 6.2
+    # GiB, exceeds its budget), the stage path below selects and attends whole
+    # chunks.  Groups start at multiples of BLOCK_SIZE_Q from the chunk origin,
+    # so the lists and therefore the outputs are identical.
+    note("C all heads: row groups == whole chunks")
+    wl = WORKLOADS["C"]
+    q, k, v = make_inputs(1, 28, 4, 131072, 128, torch.bfloat16, seed=1)
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    del q, k, v
+    th = 0.8385383879401624
+    out = VecAttention_prefill(qd, kd, vd, th, 64, 16, 16, True, wl.chunk_size)
+    ref = torch.empty_like(qd)
+    qs, _ = stages.pool_scaled(qd, 64)
+    segk = stages.segment_keys(131072, 16, 16)
+    gap = -math.log(th + 1e-9)
+    for J0 in range(0, 2048, 512):
+        cnt, idx = stages.select_segments(qs[:, :, J0:J0 + 512], kd, J0, gap, None, True, 64, 16, 16,
+                                          True, segk)
+        stages.sparse_attention(qd, kd, vd, ref, J0, 512, cnt, idx, True, 64, segk=segk)
+        del cnt, idx
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)
 
 
 # ------------------------------------------------------------------ config D --

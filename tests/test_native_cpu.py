@@ -105,13 +105,24 @@ def test_prefill_argument_errors_before_launch(L):
     assert f(*a) == nat.VA_ERR_UNSUPPORTED    # causal with Sq != Sk
 
 
-def test_workspace_size_covers_largest_chunk(L):
-    # causal: the last chunk has the largest index capacity.
+def test_workspace_size_covers_largest_row_group(L):
+    # causal 128K: the index buffer holds one row group of the last chunk at a
+    # time (128 q-block rows, a multiple of BLOCK_SIZE_Q = 64, at most 2 GiB of
+    # slots or one group), not the whole 32K chunk.
     B, Hq, S, D, qps, chunk = 1, 28, 131072, 128, 64, 32768
+    qs_bytes = B * Hq * (S // qps) * D * 2
     ws = L.va_prefill_workspace_size(nat.VA_BF16, B, Hq, S, S, D, qps, 1, chunk)
-    last = L.va_select_index_capacity(B, Hq, S, qps, 1, 1, (S - chunk) // qps, chunk // qps, 0)
-    assert ws >= last * 4 + B * Hq * (S // qps) * D * 2
-    assert ws < last * 4 + B * Hq * (S // qps) * D * 2 + 1 << 20
+    whole = L.va_select_index_capacity(B, Hq, S, qps, 1, 1, (S - chunk) // qps, chunk // qps, 0)
+    group = L.va_select_index_capacity(B, Hq, S, qps, 1, 1, S // qps - 128, 128, 0)
+    assert group * 4 <= 2 << 30
+    assert ws >= group * 4 + qs_bytes
+    assert ws < whole * 4
+    assert ws < 2 * 2 ** 30 + qs_bytes + (64 << 20)
+    # non-causal chunks are not split: every row sees every key
+    S2, H2 = 119056, 24
+    ws2 = L.va_prefill_workspace_size(nat.VA_BF16, B, H2, S2, S2, D, qps, 0, chunk)
+    full = L.va_select_index_capacity(B, H2, S2, qps, 0, 0, 0, chunk // qps, 0)
+    assert ws2 >= full * 4 + B * H2 * (-(-S2 // qps)) * D * 2
 
 
 def _dense(L, **over):
