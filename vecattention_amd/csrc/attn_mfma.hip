@@ -36,6 +36,7 @@
 //
 // Algorithmic work per gathered key: 4*D FLOPs per query row (QK^T and PV).
 #include <type_traits>
+#include <utility>
 
 #include "keylist.h"
 #include "lanes.h"
@@ -49,6 +50,18 @@ constexpr uint32_t kOutOfRange = 0xfffffff0u;  // voffset past every buffer's ra
 constexpr float kRescaleSlack = 8.f;           // log2 of the largest kept probability
 
 typedef short s16x4_t __attribute__((ext_vector_type(4)));
+
+// f(std::integral_constant<int, i>) for i = 0 .. N-1, in order.
+template <typename F, int... I>
+__device__ inline void static_for_impl(F& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ inline void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+template <uint32_t V>
+using lds_off = std::integral_constant<uint32_t, V>;
 
 template <int D, int QPS>
 struct AttnShape {
@@ -250,7 +263,6 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
   const __amdgpu_buffer_rsrc_t vrs = make_rsrc_rows(vh, uint32_t(svs * 2), uint32_t(Sk));
   const __amdgpu_buffer_rsrc_t irs =
       make_rsrc(cols, uint32_t(nseg > 1 ? (cap > 0 ? cap : 0) : n_col) * 4u);
-  const uint32_t smem_lds = lds_addr(smem);
 
   // Copy geometry.  Copy x of this wave fills rows [(wave*H + x)*RPC, +RPC) of
   // a tile; this lane fetches physical chunk p of row R_x, i.e. logical chunk
@@ -274,7 +286,11 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
   // [sv[sc], sc_next) at slots position + sc_base.  Positions only grow from
   // tile to tile, so the cursor moves forward once per segment (empty
   // segments are stepped over), and a tile with no segment boundary inside
-  // it costs one add per lane.
+  // it costs one add per lane.  Every slot past the key count of a tile, and
+  // every slot of a tile past the end of the list, gets key 2^32 - 1: its
+  // copies read zeros and move no data.  The slots of the selected columns
+  // are copied from the index list, where positions past its end read as 0;
+  // copy_pairs replaces those keys in the one partial column tile.
   const int kNoBoundary = 0x7fffffff;
   auto boundary = [&](int sg) {  // start of segment sg, or none
     return sg < nseg ? __builtin_amdgcn_readlane(sv, sg) : kNoBoundary;
@@ -282,10 +298,14 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
   int sc = 0, sc_base = 0, sc_next = nseg > 1 ? boundary(1) : kNoBoundary;
   auto stage_ids = [&](int u, int slot) {
     int32_t* dst = ids + slot * kTileKeys;
-    if (u < t_init) {
-      dst[lane] = u * kTileKeys + w_slot;
+    if (u >= ntiles) {
+      dst[lane] = -1;
+    } else if (u < t_init) {
+      const int key = u * kTileKeys + w_slot;
+      dst[lane] = key < n_init ? key : -1;
     } else if (u < t_init + t_diag) {
-      dst[lane] = diag0 + (u - t_init) * kTileKeys + w_slot;
+      const int d = (u - t_init) * kTileKeys + w_slot;
+      dst[lane] = d < n_diag ? diag0 + d : -1;
     } else {
       const int p0 = (u - t_init - t_diag) * kTileKeys, p = p0 + w_slot;
       while (sc_next <= p0) {  // the tile starts past segment sc
@@ -311,16 +331,15 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
   // Copy addresses of tile u: for each of this lane's H copies, the (row,
   // byte offset) pair of its 16-byte chunk, the row being the key id in ids
   // slot idslot; K and V copies of a tile use the same pairs.  Keys outside
-  // [0, Sk) read zeros; rows past the tile's key count and every row of a
-  // tile past the end of the list are given row 2^32 - 1 (also zeros), so
-  // their copies fill slots that are masked or never read.  Only partial
-  // tiles (a uniform branch) test the row count: a full tile costs no VALU.
+  // [0, Sk) read zeros.  In the partial column tile (one per list, a uniform
+  // test), rows past the list's end get key 2^32 - 1.
+  const int p_col = n_col % kTileKeys != 0 ? ntiles - 1 : -1;
   auto copy_pairs = [&](int u, int idslot, uint64_t (&pr)[H]) {
-    const int lim = tile_info(u).lim;
     uint32_t key[H];
 #pragma unroll
     for (int x = 0; x < H; ++x) key[x] = uint32_t(ids[idslot * kTileKeys + id_pos + x]);
-    if (lim < kTileKeys) {
+    if (u == p_col) {
+      const int lim = n_col - (u - t_init - t_diag) * kTileKeys;
 #pragma unroll
       for (int x = 0; x < H; ++x)  // row (wave*H + x)*RPC + qr holds a key below lim
         if (qr >= lim - (wave * H + x) * RPC) key[x] = 0xffffffffu;
@@ -328,12 +347,17 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
 #pragma unroll
     for (int x = 0; x < H; ++x) pr[x] = uint64_t(key[x]) | (uint64_t(cchunk[x]) << 32);
   };
-  // Copy x of this wave into the K or V tile at LDS address base.
-  auto copy_k = [&](uint32_t base, int x, uint64_t pr) {
-    copy16_row_to_lds(krs, base + uint32_t((wave * H + x) * 1024), pr);
+  // Copy x of this wave into the K or V tile at LDS offset kBase of the
+  // stages (a compile-time constant): M0 = this wave's copy base + offset.
+  const uint32_t lds_copy_base =
+      uint32_t(__builtin_amdgcn_readfirstlane(int(lds_addr(smem) + uint32_t(wave * H * 1024))));
+  auto copy_k = [&](auto base_tag, auto x_tag, uint64_t pr) {
+    copy16_row_to_lds_at<decltype(base_tag)::value + decltype(x_tag)::value * 1024u>(
+        krs, lds_copy_base, pr);
   };
-  auto copy_v = [&](uint32_t base, int x, uint64_t pr) {
-    copy16_row_to_lds(vrs, base + uint32_t((wave * H + x) * 1024), pr);
+  auto copy_v = [&](auto base_tag, auto x_tag, uint64_t pr) {
+    copy16_row_to_lds_at<decltype(base_tag)::value + decltype(x_tag)::value * 1024u>(
+        vrs, lds_copy_base, pr);
   };
 
   // Wait for Q here: otherwise the compiler places the wait at the first MFMA
@@ -395,7 +419,15 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
   };
   // Mask tile u's scores: empty slots, the causal diagonal, every slot of a
   // tile past the end of the list.  Slot of s[e]: 32kc + 8(e/4) + 4hh + e%4.
+  // Tiles that may need masking, found with two comparisons: [m_lo, m_hi)
+  // holds the partial last tile of the initial blocks and the diagonal tiles,
+  // and every tile from m_col on is the partial last column tile or lies past
+  // the end of the list.
+  const int m_lo = t_init - (n_init % kTileKeys != 0 ? 1 : 0);
+  const uint32_t m_span = uint32_t(t_init + t_diag - m_lo);
+  const int m_col = ntiles - (n_col % kTileKeys != 0 ? 1 : 0);
   auto mask = [&](int u, f32x16_t& s) {
+    if (uint32_t(u - m_lo) >= m_span && u < m_col) return;  // uniform: a full column tile
     const TileInfo ti = tile_info(u);
     if (ti.diag || ti.lim < kTileKeys) {  // rare: partial, diagonal or empty tiles
 #pragma unroll
@@ -471,7 +503,7 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
   // K(t+1) and K(t+2)).
   constexpr int kKeep = kStats ? H : 2 * H;
   if (ntiles > 0) {
-    if (wave < ntiles) stage_ids(wave, wave);  // tiles 0 .. W-1
+    stage_ids(wave, wave);  // tiles 0 .. W-1
     // When tiles 0 and 1 are local blocks (their ids are LDS writes), their
     // copies need no column ids: the barrier waits for LDS only and the
     // column-id copies stay in flight next to K(0), K(1), V(0); the barrier
@@ -486,14 +518,10 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
     uint64_t pr[H], pr1[H];
     copy_pairs(0, 0, pr);
     copy_pairs(1, 1, pr1);
-#pragma unroll
-    for (int x = 0; x < H; ++x) copy_k(smem_lds, x, pr[x]);
-#pragma unroll
-    for (int x = 0; x < H; ++x) copy_k(smem_lds + uint32_t(S::kStageBytes), x, pr1[x]);
-    if constexpr (!kStats) {
-#pragma unroll
-      for (int x = 0; x < H; ++x) copy_v(smem_lds + uint32_t(S::kTileBytes), x, pr[x]);
-    }
+    static_for<H>([&](auto x) { copy_k(lds_off<0>{}, x, pr[x]); });
+    static_for<H>([&](auto x) { copy_k(lds_off<S::kStageBytes>{}, x, pr1[x]); });
+    if constexpr (!kStats)
+      static_for<H>([&](auto x) { copy_v(lds_off<S::kTileBytes>{}, x, pr[x]); });
     vm_lds_barrier_keep<kKeep>();  // K(0) landed
     s_cur = qk(smem);
     mask(0, s_cur);
@@ -503,8 +531,7 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
     rescale(max_halves(tmax));
     lds_barrier();  // every wave is done with K(0)
     copy_pairs(2, 2, pr);
-#pragma unroll
-    for (int x = 0; x < H; ++x) copy_k(smem_lds, x, pr[x]);
+    static_for<H>([&](auto x) { copy_k(lds_off<0>{}, x, pr[x]); });
   }
   // One iteration; the parity P = t & 1 is a compile-time constant so that
   // the LDS slot addresses fold into the instructions' offsets and S(t),
@@ -518,7 +545,7 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
     vm_lds_barrier_keep<kKeep>();  // K(t+1) landed; every wave is done with PV(t-1)
     if (P == 0 && t % W == 0) {  // every wave stages one of tiles t+W .. t+2W-1
       const int u = t + W + wave;
-      if (u < ntiles) stage_ids(u, u % S::kIdSlots);
+      stage_ids(u, u % S::kIdSlots);
     }
     const unsigned char* kb = smem + k_next;
 #pragma unroll
@@ -541,9 +568,9 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
             __builtin_bit_cast(vec, *reinterpret_cast<const uint4*>(kb + koff[st + kAhead]));
       s_next = M::run(a[st], qreg[st], s_next);  // past the last tile: masked away below
       if (st == 0) copy_pairs(t + 1, (t + 1) % S::kIdSlots, cpr);
-#pragma unroll
-      for (int c = 0; c < H; ++c)  // copy c goes out after MFMA c * NQK / H
-        if (!kStats && c * NQK / H == st) copy_v(smem_lds + v_next, c, cpr[c]);
+      static_for<H>([&](auto c) {  // copy c goes out after MFMA c * NQK / H
+        if (!kStats && c * NQK / H == st) copy_v(lds_off<v_next>{}, c, cpr[c]);
+      });
       // this step's share of the softmax of S(t)
 #pragma unroll
       for (int e = st * 16 / NQK; e < (st + 1) * 16 / NQK; ++e) {
@@ -556,8 +583,7 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
     if constexpr (kStats) {  // row sums of P(t), maximum of S(t+1), copies of K(t+3)
       vm_lds_barrier_keep<kKeep>();  // every wave is done with K(t+1)
       copy_pairs(t + 3, (t + 3) % S::kIdSlots, cpr);
-#pragma unroll
-      for (int c = 0; c < H; ++c) copy_k(smem_lds + k_next, c, cpr[c]);
+      static_for<H>([&](auto c) { copy_k(lds_off<k_next>{}, c, cpr[c]); });
       float ps[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) ps[e] = pr[e] + pr[e + 8];
@@ -585,9 +611,9 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
       __builtin_amdgcn_sched_barrier(0);
       if (f + kVAhead < NPV) vf[f + kVAhead] = read_v(vb, f + kVAhead);
       pv_mfma(f, vf[f], bfrag);
-#pragma unroll
-      for (int c = 0; c < H; ++c)  // copy c goes out after MFMA c * NPV / H
-        if (c * NPV / H == f) copy_k(smem_lds + k_next, c, cpr[c]);
+      static_for<H>([&](auto c) {  // copy c goes out after MFMA c * NPV / H
+        if (c * NPV / H == f) copy_k(lds_off<k_next>{}, c, cpr[c]);
+      });
 #pragma unroll
       for (int j = f * 8 / NPV; j < (f + 1) * 8 / NPV; ++j)
         lsum = M::add_pair(bfrag[j / 4], j % 4, lsum);

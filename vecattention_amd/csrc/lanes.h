@@ -63,6 +63,16 @@ __device__ inline void copy16_row_to_lds(__amdgpu_buffer_rsrc_t r, uint32_t lds,
                : "s"(__builtin_amdgcn_readfirstlane(int(lds))), "v"(index_offset), "s"(r)
                : "memory");
 }
+// The same with the LDS address given as a wave-uniform base plus a
+// compile-time offset, so that setting M0 costs one scalar add.
+template <uint32_t kOffset>
+__device__ inline void copy16_row_to_lds_at(__amdgpu_buffer_rsrc_t r, uint32_t lds_base,
+                                            uint64_t index_offset) {
+  asm volatile("s_add_u32 m0, %0, %3\n\tbuffer_load_dwordx4 %1, %2, 0 idxen offen sc1 lds"
+               :
+               : "s"(lds_base), "v"(index_offset), "s"(r), "n"(kOffset)
+               : "memory");
+}
 // One dword per lane, device scope (read once, as copy16_row_to_lds).
 __device__ inline void copy4_to_lds(__amdgpu_buffer_rsrc_t r, uint32_t lds, uint32_t voffset) {
   asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen sc1 lds"
