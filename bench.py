@@ -138,10 +138,11 @@ def kernel_source_hash():
 
 
 def profiled_traffic(workload, kernel):
-    """Bytes per launch of `kernel` on `workload` crossing from L2 to the data
-    fabric (FETCH_SIZE + WRITE_SIZE, each scaled by the copy-kernel
-    calibration; fabric reads include those the Infinity Cache serves), from
-    the rocprofv3 --pmc runs summarised in profiles/hbm_traffic.json.  None
+    """Bytes per launch of `kernel` on `workload` crossing between L2 and the
+    data fabric (reads + writes; fabric reads include those the Infinity
+    Cache serves), counted exactly from the TCC_EA0 request-size counters in
+    the rocprofv3 --pmc runs summarised in profiles/hbm_traffic.json, and the
+    compulsory bytes of that launch (None where not recorded).  (None, None)
     when not profiled, or when the profile was taken on other kernel sources
     than the ones built now (its source_hash differs)."""
     path = os.path.join(ROOT, "profiles", "hbm_traffic.json")
@@ -150,10 +151,10 @@ def profiled_traffic(workload, kernel):
             doc = json.load(f)
         rec = doc["workloads"][workload][kernel]
     except (OSError, KeyError, ValueError):
-        return None
+        return None, None
     if doc.get("source_hash") != kernel_source_hash():
-        return None
-    return int(round(rec["fetch_bytes"] + rec["write_bytes"]))
+        return None, None
+    return int(round(rec["fetch_bytes"] + rec["write_bytes"])), rec.get("compulsory_bytes")
 
 
 # ------------------------------------------------------------------- stages --
@@ -618,7 +619,7 @@ def measure_prefill(args, wl, dev, with_cpu):
     # value: the whole VecAttention_prefill step, as timed above
     e2e_tflops = F_attn / (ms_per_step * 1e-3) / 1e12
     attn_tflops = F_attn / (t_attn * 1e-3) / 1e12
-    traffic = profiled_traffic(wl.name, "attn_mfma_kernel")
+    traffic, compulsory = profiled_traffic(wl.name, "attn_mfma_kernel")
     result = {
         "metric": METRIC,
         "value": round(e2e_tflops, 3),
@@ -654,8 +655,10 @@ def measure_prefill(args, wl, dev, with_cpu):
                      "achieved": round(attn_tflops, 3), "peak": BF16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(attn_tflops / BF16_PEAK_TFLOPS, 4),
                      "traffic": traffic,
-                     "traffic_kind": "L2-to-fabric bytes per launch (FETCH_SIZE + WRITE_SIZE, "
-                                     "copy-calibrated; Infinity Cache hits included)"},
+                     "traffic_kind": "L2<->fabric bytes per launch (exact, from the TCC_EA0 "
+                                     "request-size counters; Infinity Cache hits included)",
+                     "traffic_over_compulsory": (round(traffic / compulsory, 2)
+                                                 if traffic and compulsory else None)},
         "flops": {"attn_executed": F_attn, "dense": F_dense},
     }
     if with_cpu:
