@@ -379,7 +379,7 @@ E2E_CASES = [
     # name, B, Hq, Hk, S, D, dtype, causal, qps, bk, G, chunk, threshold
     ("vlm-like-causal", 1, 8, 2, 2048, 128, torch.bfloat16, True, 64, 16, 16, 1024, 0.5),
     ("dit-like-noncausal", 1, 4, 4, 2000, 128, torch.bfloat16, False, 64, 16, 8192, 1024, 0.3),
-    # long enough for the two-pass split selection (segments of 4096 keys)
+    # long enough for the two-pass split selection (segments of 2048 keys)
     ("dit-like-2pass", 1, 2, 2, 9000, 128, torch.bfloat16, False, 64, 16, 8192, 4608, 0.3),
     ("causal-qps128-bk16", 1, 4, 4, 1300, 64, torch.bfloat16, True, 128, 16, 4, 512, 0.6),
     ("A-fp32-noncausal", 1, 4, 4, 4096, 64, torch.float32, False, 64, 16, 16, 4096, 0.35),
@@ -508,7 +508,7 @@ def test_full_size_large_gap_selects_every_selectable_key(config_b):
 @pytest.mark.parametrize("th", ["calibrated", 0.35])
 def test_full_size_rows_match_oracle(config_b, th):
     # Sampled rows of the full 32K config: the split selection's lists (the
-    # ones VecAttention_prefill's attention reads: 8 segments of 4096 keys)
+    # ones VecAttention_prefill's attention reads: 16 segments of 2048 keys)
     # equal the oracle's bit for bit, and the prefill output is within tolerance.
     q, k, v, qd, kd, vd = config_b
     qps = 64
