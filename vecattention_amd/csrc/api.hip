@@ -835,8 +835,22 @@ int va_prefill(int dtype, const void* q, int64_t sqb, int64_t sqh, int64_t sqs, 
       }
     }
   }
-  const int nseg = segk > 0 ? int(cdiv(Sk, segk)) : 1;
   const float scale = float(1.0 / std::sqrt(double(D)));
+  // Segment length of a row group: groups of few rows (the later groups of a
+  // long causal prefill) halve the segments, down to 2048 keys and at most 64
+  // segments, until the selection has kMinSelectBlocks work-groups (each
+  // covers 128 rows of one segment); the attention of the group reads the
+  // lists with the same length.
+  const int64_t gspan = segk > 0 && !two_pass ? bk * effective_group(group, Sk, bk) : 0;
+  auto group_segk = [&](int64_t nc) {
+    constexpr int64_t kMinSelectBlocks = 1536, kMinSeg = 2048;
+    int64_t sg = segk;
+    if (gspan <= 0) return sg;
+    while (sg / 2 >= kMinSeg && (sg / 2) % gspan == 0 && cdiv(Sk, sg / 2) <= kMaxSegments &&
+           cdiv(nc, 128) * cdiv(Sk, sg) * B * Hq < kMinSelectBlocks)
+      sg /= 2;
+    return sg;
+  };
   const int64_t unit = group_unit(bsq);
   for (int64_t i = 0; i < Sq; i += chunk_size) {
     const int64_t rows = (Sq - i < chunk_size) ? (Sq - i) : chunk_size;
@@ -848,22 +862,24 @@ int va_prefill(int dtype, const void* q, int64_t sqb, int64_t sqh, int64_t sqs, 
       const int64_t b = group_end(B, Hq, Sk, qps, causal, Jc, nrows, a, unit);
       const int64_t J0 = Jc + a, nc = b - a;
       a = b;
+      const int64_t segk_g = group_segk(nc);
+      const int nseg = segk_g > 0 ? int(cdiv(Sk, segk_g)) : 1;
       const int64_t es = esize(dtype);
       const void* qs_chunk = static_cast<const char*>(qs) + J0 * D * es;
       if (two_pass) {
         rc = select_impl(dtype, qs_chunk, Hq * nqb * D, nqb * D, D, k, skb, skh, sks, B, Hq, Hk,
                          Sk, D, qps, bk, group, causal, causal, J0, nc, bsq, gap, gaps, 0, counts,
-                         indices, which, knorm, segk, st, carry, va::kPassMax);
+                         indices, which, knorm, segk_g, st, carry, va::kPassMax);
         if (rc) return rc;
       }
       rc = select_impl(dtype, qs_chunk, Hq * nqb * D, nqb * D, D, k, skb, skh, sks, B, Hq, Hk,
                        Sk, D, qps, bk, group, causal, causal, J0, nc, bsq, gap, gaps, 0, counts,
-                       indices, which, knorm, segk, st, carry,
+                       indices, which, knorm, segk_g, st, carry,
                        two_pass ? va::kPassCarry : va::kPassPlain);
       if (rc) return rc;
       rc = sparse_attn_impl(dtype, q, sqb, sqh, sqs, k, skb, skh, sks, v, svb, svh, svs, out, sob,
                             soh, sos, B, Hq, Hk, Sq, Sk, D, qps, causal, causal, J0, nc, 0, counts,
-                            indices, scale, VA_ATTN_AUTO, nseg, segk, st);
+                            indices, scale, VA_ATTN_AUTO, nseg, segk_g, st);
       if (rc) return rc;
     }
   }
