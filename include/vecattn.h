@@ -268,6 +268,31 @@ int64_t va_prefill_workspace_size(int dtype, int64_t B, int64_t Hq, int64_t Sq, 
                                   int64_t chunk_size);
 
 /*
+ * Kernels va_prefill runs for these tensors and parameters, as a bit set
+ * (negative on invalid sizes): the selection on the certified MFMA wave kernel
+ * (VA_KERNELS_SELECT_WAVE), the 64-row MFMA kernel (VA_KERNELS_SELECT_MFMA) or
+ * the exact fp64 kernel (VA_KERNELS_SELECT_EXACT: fp32 inputs, D outside
+ * {64, 128}, k_local_size outside {16, 32, 64}, unaligned K); the attention on
+ * the MFMA kernel (VA_KERNELS_ATTN_MFMA) or the per-row kernel
+ * (VA_KERNELS_ATTN_ROW: fp32, D or q_pooling_size outside {64, 128}, K/V row
+ * strides of 16 KiB or more, unaligned tensors); VA_KERNELS_SPLIT when the
+ * selection runs in key segments.  The exact selection and the per-row
+ * attention are several times slower than the MFMA kernels.  No counterpart
+ * in the reference: it lets callers see which path a configuration takes.
+ */
+#define VA_KERNELS_SELECT_WAVE 1
+#define VA_KERNELS_SELECT_MFMA 2
+#define VA_KERNELS_SELECT_EXACT 4
+#define VA_KERNELS_ATTN_MFMA 16
+#define VA_KERNELS_ATTN_ROW 32
+#define VA_KERNELS_SPLIT 64
+int va_prefill_kernels(int dtype, const void* q, int64_t sqb, int64_t sqh, int64_t sqs,
+                       const void* k, int64_t skb, int64_t skh, int64_t sks, const void* v,
+                       int64_t svb, int64_t svh, int64_t svs, const void* out, int64_t sob,
+                       int64_t soh, int64_t sos, int64_t Sk, int64_t D, int64_t q_pooling_size,
+                       int64_t k_local_size, int64_t group_k_block);
+
+/*
  * The whole VecAttention prefill: pooling, then per query chunk selection and
  * vector-sparse attention, all on `stream` with no host synchronisation.
  * Replaces spattn/src/VecAttention.py:10-123 (VecAttention_prefill).

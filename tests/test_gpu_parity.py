@@ -406,6 +406,30 @@ def test_vecattention_prefill_matches_oracle(device, case):
     assert err.max() <= tol[0] and err.mean() <= tol[1], (err.max(), err.mean())
 
 
+def test_reference_default_tiles_warn_and_match_oracle(device):
+    # The reference signature's defaults (q_pooling_size 128, k_local_size 128,
+    # group_k_block 1) take the exact fp64 selection: the result matches the
+    # oracle and the slower path is announced once; the MFMA tiles stay silent.
+    import warnings
+    from vecattention_amd import vecattention as va_mod
+    note("default tiles")
+    B, Hq, Hk, S, D = 1, 4, 2, 1300, 128
+    q, k, v = make_inputs(B, Hq, Hk, S, D, torch.bfloat16, seed=4)
+    qd, kd, vd = q.to(device), k.to(device), v.to(device)
+    va_mod._warned_paths.clear()
+    with pytest.warns(RuntimeWarning, match="exact fp64 kernel"):
+        out = VecAttention_prefill(qd, kd, vd, threshold=0.5)
+    torch.cuda.synchronize()
+    want, _ = orc.prefill(q, k, v, 0.5, 128, 128, 1, True, 16 * 1024, 64, "bfloat16")
+    err = np.abs(out.float().cpu().numpy() - want)
+    assert err.max() <= ATOL_MAX and err.mean() <= ATOL_MEAN, (err.max(), err.mean())
+    with warnings.catch_warnings():
+        warnings.simplefilter("error", RuntimeWarning)
+        VecAttention_prefill(qd, kd, vd, threshold=0.5, q_pooling_size=64, k_local_size=16,
+                             group_k_block=16)
+    torch.cuda.synchronize()
+
+
 def _device_gaps(th, B, Hq, device):
     """The fp32 gaps VecAttention_prefill computes on the device for a
     threshold tensor (-torch.log(th + 1e-9) there), as a host array."""

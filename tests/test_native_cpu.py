@@ -200,3 +200,41 @@ def test_decode_argument_errors_before_launch(L):
     assert _decode(L, ws=None) == nat.VA_ERR_WORKSPACE
     assert _decode(L, ws_bytes=need - 256) == nat.VA_ERR_WORKSPACE
     assert _decode(L, kernel=9) == nat.VA_ERR_ARG
+
+
+def _plan(L, dtype=nat.VA_BF16, D=128, qps=64, bk=16, G=16, Sk=32768, kv_row=None, align=256):
+    # va_prefill_kernels only inspects addresses and strides (no device access):
+    # plain integers stand for the tensors' addresses.
+    row = D if kv_row is None else kv_row
+    q, k, v, out = align, 2 * align, 3 * align, 4 * align
+    return L.va_prefill_kernels(dtype, q, 8 * Sk * D, Sk * D, D, k, 8 * Sk * row, Sk * row, row,
+                                v, 8 * Sk * row, Sk * row, row, out, 8 * Sk * D, Sk * D, D, Sk, D,
+                                qps, bk, G)
+
+
+def test_prefill_kernels_reports_the_mfma_path(L):
+    f = _plan(L)
+    assert f == nat.VA_KERNELS_SELECT_WAVE | nat.VA_KERNELS_ATTN_MFMA | nat.VA_KERNELS_SPLIT
+    # one group per row (DiT group_k_block): the two-pass split
+    f = _plan(L, G=8192, Sk=32760)
+    assert f == nat.VA_KERNELS_SELECT_WAVE | nat.VA_KERNELS_ATTN_MFMA | nat.VA_KERNELS_SPLIT
+
+
+def test_prefill_kernels_reports_the_slow_paths(L):
+    # the reference signature's default k_local_size (128): exact selection
+    f = _plan(L, qps=128, bk=128, G=1)
+    assert f & nat.VA_KERNELS_SELECT_EXACT and f & nat.VA_KERNELS_ATTN_MFMA
+    assert not f & nat.VA_KERNELS_SPLIT
+    # fp32 inputs: exact selection and the per-row attention
+    f = _plan(L, dtype=nat.VA_F32)
+    assert f == nat.VA_KERNELS_SELECT_EXACT | nat.VA_KERNELS_ATTN_ROW
+    # head_dim 96: neither MFMA kernel
+    f = _plan(L, D=96)
+    assert f & nat.VA_KERNELS_SELECT_EXACT and f & nat.VA_KERNELS_ATTN_ROW
+    # K/V rows 16 KiB apart: the attention's buffer record stride no longer fits
+    f = _plan(L, kv_row=8192)
+    assert f & nat.VA_KERNELS_ATTN_ROW
+    # unaligned keys
+    f = _plan(L, align=258)
+    assert f & nat.VA_KERNELS_SELECT_EXACT and f & nat.VA_KERNELS_ATTN_ROW
+    assert _plan(L, D=0) < 0

@@ -765,6 +765,38 @@ int64_t va_prefill_workspace_size(int dtype, int64_t B, int64_t Hq, int64_t Sq, 
   return a + b + c + d + e;
 }
 
+int va_prefill_kernels(int dtype, const void* q, int64_t sqb, int64_t sqh, int64_t sqs,
+                       const void* k, int64_t skb, int64_t skh, int64_t sks, const void* v,
+                       int64_t svb, int64_t svh, int64_t svs, const void* out, int64_t sob,
+                       int64_t soh, int64_t sos, int64_t Sk, int64_t D, int64_t qps, int64_t bk,
+                       int64_t group) {
+  if (!dtype_ok(dtype) || Sk <= 0 || D <= 0 || qps <= 0 || bk <= 0 || group <= 0)
+    return fail(VA_ERR_ARG, "invalid prefill sizes");
+  // The pooled queries live in the 256-byte aligned workspace with element
+  // strides that are multiples of D: any aligned address and D strides stand
+  // for them.
+  const void* qs = reinterpret_cast<const void*>(uintptr_t(256));
+  int flags = 0;
+  const bool wave = select_wave_ok(dtype, qs, D, D, D, k, skb, skh, sks, Sk, D, bk, group);
+  if (wave)
+    flags |= VA_KERNELS_SELECT_WAVE;
+  else if (select_mfma_ok(dtype, qs, D, D, D, k, skb, skh, sks, D, bk))
+    flags |= VA_KERNELS_SELECT_MFMA;
+  else
+    flags |= VA_KERNELS_SELECT_EXACT;
+  const int64_t sq[3] = {sqb, sqh, sqs}, sk[3] = {skb, skh, sks}, sv[3] = {svb, svh, svs},
+                so[3] = {sob, soh, sos};
+  const bool attn = attn_mfma_check(dtype, q, sq, k, sk, v, sv, out, so, Sk, D, qps).ok();
+  flags |= attn ? VA_KERNELS_ATTN_MFMA : VA_KERNELS_ATTN_ROW;
+  if (wave && attn) {
+    const int64_t g = effective_group(group, Sk, bk);
+    if (va::select_wave_segment_keys(Sk, bk, g) > 0 || va::select_wave_carry_segment_keys(Sk, bk, g) > 0)
+      flags |= VA_KERNELS_SPLIT;
+  }
+  ok();
+  return flags;
+}
+
 int va_prefill(int dtype, const void* q, int64_t sqb, int64_t sqh, int64_t sqs, const void* k,
                int64_t skb, int64_t skh, int64_t sks, const void* v, int64_t svb, int64_t svh,
                int64_t svs, void* out, int64_t sob, int64_t soh, int64_t sos, int64_t B,

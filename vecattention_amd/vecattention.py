@@ -7,6 +7,7 @@ pooling, TilingSelect selection and vector-sparse attention, chunk by chunk on
 the current stream with no host synchronisation.
 """
 import math
+import warnings
 from typing import Union
 
 import torch
@@ -80,6 +81,28 @@ def _check_inputs(q, k, v):
         raise AssertionError(f"query heads {Hq} not a multiple of key heads {k.shape[1]}")
 
 
+_warned_paths = set()
+
+
+def _warn_slow_path(flags, dtype, head_dim, q_pooling_size, k_local_size):
+    """Warn once per configuration when va_prefill leaves the MFMA kernels."""
+    reasons = []
+    if flags & nat.VA_KERNELS_SELECT_EXACT:
+        reasons.append("the selection runs on the exact fp64 kernel (the MFMA selection takes "
+                       "bf16/fp16, head_dim 64 or 128, k_local_size 16, 32 or 64 and 16-byte "
+                       "aligned keys)")
+    if flags & nat.VA_KERNELS_ATTN_ROW:
+        reasons.append("the attention runs on the per-row kernel (the MFMA attention takes "
+                       "bf16/fp16, head_dim and q_pooling_size 64 or 128, aligned tensors and "
+                       "key/value row strides under 16 KiB)")
+    key = (flags, str(dtype), head_dim, q_pooling_size, k_local_size)
+    if reasons and key not in _warned_paths:
+        _warned_paths.add(key)
+        warnings.warn("VecAttention_prefill: " + "; ".join(reasons) +
+                      "; expect several times the time of the MFMA path", RuntimeWarning,
+                      stacklevel=3)
+
+
 def _feature_contiguous(t):
     return t if t.stride(-1) == 1 else t.contiguous()
 
@@ -130,6 +153,14 @@ def VecAttention_prefill(
     dt = nat.dtype_code(q)
     L = nat.lib()
     attn_output = torch.empty(B, Hq, S, D, dtype=q.dtype, device=q.device)
+    flags = L.va_prefill_kernels(
+        dt, nat.ptr(q), q.stride(0), q.stride(1), q.stride(2), nat.ptr(k), k.stride(0),
+        k.stride(1), k.stride(2), nat.ptr(v), v.stride(0), v.stride(1), v.stride(2),
+        nat.ptr(attn_output), attn_output.stride(0), attn_output.stride(1), attn_output.stride(2),
+        Sk, D, q_pooling_size, k_local_size, group_k_block)
+    if flags < 0:
+        nat.check("va_prefill_kernels", flags)
+    _warn_slow_path(flags, q.dtype, D, q_pooling_size, k_local_size)
     ws_bytes = L.va_prefill_workspace_size(dt, B, Hq, S, Sk, D, q_pooling_size, int(causal),
                                            chunk_size)
     if ws_bytes < 0:
