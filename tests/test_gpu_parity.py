@@ -155,6 +155,33 @@ def select_or_skip(*args, **kw):
 @pytest.mark.parametrize("kernel", SEL_KERNELS, ids=SEL_IDS)
 @pytest.mark.parametrize("case", SELECT_CASES, ids=[c[0] for c in SELECT_CASES])
 def test_select_bit_exact(device, case, kernel):
+    _select_case(device, case, kernel)
+
+
+# Tiles of 128 and 256 keys (the reference signature's default k_local_size is
+# 128): the 64-row MFMA kernel takes them (a tile is 8 or 16 of its 16-key
+# segments, one or two per 256-key chunk); the wave kernel does not.
+BIG_TILE_CASES = [
+    # name, B, Hq, Hk, S, D, dtype, causal, qps, bk, G, keep, chunk_rows
+    ("bf16-causal-qps128-bk128-G1", 1, 4, 2, 2048, 128, torch.bfloat16, True, 128, 128, 1, 0.10,
+     None),
+    ("bf16-causal-qps128-bk128-G4-chunked", 1, 4, 1, 3000, 128, torch.bfloat16, True, 128, 128,
+     4, 0.10, 8),
+    ("fp16-noncausal-bk256-G2-tail", 2, 4, 2, 1800, 64, torch.float16, False, 64, 256, 2, 0.15,
+     None),
+    ("bf16-noncausal-bk128-G8192", 1, 2, 2, 2500, 128, torch.bfloat16, False, 64, 128, 8192, 0.10,
+     None),
+]
+
+
+@pytest.mark.parametrize("kernel", [nat.VA_SEL_EXACT, nat.VA_SEL_AUTO, nat.VA_SEL_MFMA],
+                         ids=["exact", "auto", "mfma"])
+@pytest.mark.parametrize("case", BIG_TILE_CASES, ids=[c[0] for c in BIG_TILE_CASES])
+def test_select_big_tiles_bit_exact(device, case, kernel):
+    _select_case(device, case, kernel)
+
+
+def _select_case(device, case, kernel):
     name, B, Hq, Hk, S, D, dtype, causal, qps, bk, G, keep, chunk_rows = case
     note("select", name, kernel)
     q, k, _ = make_inputs(B, Hq, Hk, S, D, dtype, seed=len(name))
@@ -264,11 +291,19 @@ MFMA_STRESS = [
     ("noncausal-G8192-bk32", 2, 1, 2500, 128, False, 32, 8192, 0.12),
     ("noncausal-G3-bk64-gap0", 2, 2, 1500, 64, False, 64, 3, 0.0),
     ("causal-G5-bk16", 2, 2, 2048, 64, True, 16, 5, 0.05),
+    # tiles of 128 / 256 keys (MFMA kernel only): exact ties, groups over chunks
+    ("noncausal-G2-bk128-gap0", 2, 2, 1500, 128, False, 128, 2, 0.0),
+    ("noncausal-G3-bk256-gap0", 2, 1, 1300, 64, False, 256, 3, 0.0),
 ]
 
 
-@pytest.mark.parametrize("kernel", [nat.VA_SEL_MFMA, nat.VA_SEL_WAVE], ids=["mfma", "wave"])
-@pytest.mark.parametrize("case", MFMA_STRESS, ids=[c[0] for c in MFMA_STRESS])
+# (the wave kernel takes tiles of at most 64 keys)
+STRESS_PARAMS = [pytest.param(case, kern, id=f"{case[0]}-{kid}") for case in MFMA_STRESS
+                 for kern, kid in ((nat.VA_SEL_MFMA, "mfma"), (nat.VA_SEL_WAVE, "wave"))
+                 if not (kern == nat.VA_SEL_WAVE and case[6] > 64)]
+
+
+@pytest.mark.parametrize("case,kernel", STRESS_PARAMS)
 def test_select_mfma_exact_fallback(device, case, kernel):
     # Exact ties at gap 0 and groups straddling chunks drive the certified
     # kernels through their exact paths (ambiguous pairs, carried maxima).
@@ -406,28 +441,39 @@ def test_vecattention_prefill_matches_oracle(device, case):
     assert err.max() <= tol[0] and err.mean() <= tol[1], (err.max(), err.mean())
 
 
-def test_reference_default_tiles_warn_and_match_oracle(device):
+def test_reference_default_tiles_take_the_mfma_kernels(device):
     # The reference signature's defaults (q_pooling_size 128, k_local_size 128,
-    # group_k_block 1) take the exact fp64 selection: the result matches the
-    # oracle and the slower path is announced once; the MFMA tiles stay silent.
+    # group_k_block 1) run on the MFMA selection and attention without a
+    # warning, and match the oracle.
     import warnings
-    from vecattention_amd import vecattention as va_mod
     note("default tiles")
     B, Hq, Hk, S, D = 1, 4, 2, 1300, 128
     q, k, v = make_inputs(B, Hq, Hk, S, D, torch.bfloat16, seed=4)
     qd, kd, vd = q.to(device), k.to(device), v.to(device)
-    va_mod._warned_paths.clear()
-    with pytest.warns(RuntimeWarning, match="exact fp64 kernel"):
+    with warnings.catch_warnings():
+        warnings.simplefilter("error", RuntimeWarning)
         out = VecAttention_prefill(qd, kd, vd, threshold=0.5)
     torch.cuda.synchronize()
     want, _ = orc.prefill(q, k, v, 0.5, 128, 128, 1, True, 16 * 1024, 64, "bfloat16")
     err = np.abs(out.float().cpu().numpy() - want)
     assert err.max() <= ATOL_MAX and err.mean() <= ATOL_MEAN, (err.max(), err.mean())
-    with warnings.catch_warnings():
-        warnings.simplefilter("error", RuntimeWarning)
-        VecAttention_prefill(qd, kd, vd, threshold=0.5, q_pooling_size=64, k_local_size=16,
-                             group_k_block=16)
+
+
+def test_slow_path_is_announced_and_matches_oracle(device):
+    # head_dim 96 has no MFMA kernel: the exact selection and the per-row
+    # attention run, the prefill warns once, and the result matches the oracle.
+    from vecattention_amd import vecattention as va_mod
+    note("slow path")
+    B, Hq, Hk, S, D = 1, 2, 1, 700, 96
+    q, k, v = make_inputs(B, Hq, Hk, S, D, torch.bfloat16, seed=5)
+    va_mod._warned_paths.clear()
+    with pytest.warns(RuntimeWarning, match="exact fp64 kernel"):
+        out = VecAttention_prefill(q.to(device), k.to(device), v.to(device), threshold=0.5,
+                                   q_pooling_size=64, k_local_size=16, group_k_block=16)
     torch.cuda.synchronize()
+    want, _ = orc.prefill(q, k, v, 0.5, 64, 16, 16, True, 16 * 1024, 64, "bfloat16")
+    err = np.abs(out.float().cpu().numpy() - want)
+    assert err.max() <= ATOL_MAX and err.mean() <= ATOL_MEAN, (err.max(), err.mean())
 
 
 def _device_gaps(th, B, Hq, device):

@@ -221,10 +221,12 @@ def test_prefill_kernels_reports_the_mfma_path(L):
 
 
 def test_prefill_kernels_reports_the_slow_paths(L):
-    # the reference signature's default k_local_size (128): exact selection
+    # the reference signature's default tiles (q_pooling_size and k_local_size
+    # 128): the 64-row MFMA selection (the wave kernel takes tiles up to 64)
     f = _plan(L, qps=128, bk=128, G=1)
-    assert f & nat.VA_KERNELS_SELECT_EXACT and f & nat.VA_KERNELS_ATTN_MFMA
-    assert not f & nat.VA_KERNELS_SPLIT
+    assert f == nat.VA_KERNELS_SELECT_MFMA | nat.VA_KERNELS_ATTN_MFMA
+    assert _plan(L, bk=256, G=2) == nat.VA_KERNELS_SELECT_MFMA | nat.VA_KERNELS_ATTN_MFMA
+    assert _plan(L, bk=512, G=1) & nat.VA_KERNELS_SELECT_EXACT
     # fp32 inputs: exact selection and the per-row attention
     f = _plan(L, dtype=nat.VA_F32)
     assert f == nat.VA_KERNELS_SELECT_EXACT | nat.VA_KERNELS_ATTN_ROW

@@ -188,8 +188,11 @@ __global__ __launch_bounds__(256) void select_mfma_kernel(
           vec, *reinterpret_cast<const uint4*>(&Qs[(rb * 32 + l32) * STR + (D / 2) * hh + 8 * s]));
 
   const int nseg_tile = bk / 16;           // segments per tile
-  const int ntile = kMKC / bk;             // tiles per chunk
-  const int tpt = ntile / 4;               // tiles per thread in phase B
+  const int ntile = kMKC / bk;             // tiles per chunk (1 .. 16)
+  // Tiles per thread in phase B (4 threads per row); with fewer than 4 tiles
+  // (bk >= 128) the first ntile threads take one each and the rest idle.
+  const int tpt = ntile >= 4 ? ntile / 4 : 1;
+  const int last_part = (ntile - 1) / tpt;  // the thread that holds the last tile
   const int64_t kfirst = kstart / kMKC * kMKC;
   // Does the last group of the chunk at kb0 continue into the next chunk?
   // (key offsets < 2^31; 32-bit arithmetic)
@@ -283,7 +286,7 @@ __global__ __launch_bounds__(256) void select_mfma_kernel(
       for (int i = 0; i < 4; ++i) {
         lp[i] = v;
         lf[i] = f;
-        if (i < tpt) {
+        if (i < tpt && part * tpt + i < ntile) {
           const int t = part * tpt + i;
           float tv = -__builtin_inff();
           for (int j = 0; j < nseg_tile; ++j) tv = __builtin_fmaxf(tv, tm[row][t * nseg_tile + j]);
@@ -308,7 +311,7 @@ __global__ __launch_bounds__(256) void select_mfma_kernel(
       float mlast = 0.f;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        if (i < tpt) {
+        if (i < tpt && part * tpt + i < ntile) {
           const int t = part * tpt + i;
           const float mt = lf[i] ? lp[i] : __builtin_fmaxf(in_v, lp[i]);
           for (int j = 0; j < nseg_tile; ++j) mh[row][t * nseg_tile + j] = mt;
@@ -317,7 +320,7 @@ __global__ __launch_bounds__(256) void select_mfma_kernel(
       }
       // A group continuing into the next chunk needs its maximum carried
       // exactly: flag the row when a tile of that group can hold it.
-      if (part == 3 && row < rows_here && cont) {
+      if (part == last_part && row < rows_here && cont) {
         const float win = rwin[row];
         for (int t = ntile - 1; t >= 0; --t) {
           float tv = -__builtin_inff();
@@ -544,7 +547,7 @@ __global__ __launch_bounds__(256) void select_mfma_kernel(
 
 bool select_mfma_supported(int dtype, int64_t D, int64_t bk) {
   return (dtype == kBF16 || dtype == kF16) && (D == 64 || D == 128) &&
-         (bk == 16 || bk == 32 || bk == 64);
+         (bk == 16 || bk == 32 || bk == 64 || bk == 128 || bk == 256);
 }
 
 template <typename T, int D>
