@@ -297,6 +297,46 @@ MFMA_STRESS = [
 ]
 
 
+MFMA_SPLIT_CASES = [
+    # name, Hq, Hk, S, D, dtype, causal, qps, bk, G, keep, segk, chunk_rows
+    ("causal-qps128-bk128-G1-seg512", 4, 2, 3000, 128, torch.bfloat16, True, 128, 128, 1, 0.10,
+     512, None),
+    ("causal-qps128-bk128-G2-seg1024-chunked", 2, 1, 4500, 128, torch.bfloat16, True, 128, 128,
+     2, 0.10, 1024, 9),
+    ("noncausal-bk256-G2-seg512-gap0", 2, 2, 2300, 64, torch.float16, False, 64, 256, 2, None,
+     512, None),
+]
+
+
+@pytest.mark.parametrize("case", MFMA_SPLIT_CASES, ids=[c[0] for c in MFMA_SPLIT_CASES])
+def test_select_segments_mfma_kernel_bit_exact(device, case):
+    # Tiles of 128 / 256 keys split into key segments (whole 256-key chunks)
+    # on the 64-row MFMA kernel: per-segment lists, concatenated, equal the
+    # oracle's rows; the plan query reports the split.
+    name, Hq, Hk, S, D, dtype, causal, qps, bk, G, keep, segk, chunk_rows = case
+    note("select segments mfma", name)
+    q, k, v = make_inputs(1, Hq, Hk, S, D, dtype, seed=S + segk + bk)
+    if keep is None:
+        gaps = np.zeros(Hq, np.float32)
+    else:
+        gaps = orc.gap_from_threshold(calibrated_threshold(keep, q, k, qps, bk, G, causal), 1, Hq)
+    _, qs_cpu = orc.pool(q, qps, DTN[dtype])
+    nqb = qs_cpu.shape[2]
+    qs, _ = stages.pool_scaled(q.to(device), qps)
+    kd = k.to(device)
+    step = chunk_rows or nqb
+    for J0 in range(0, nqb, step):
+        nc = min(step, nqb - J0)
+        want_c, want = orc.select(qs_cpu, k, J0, nc, gaps, qps, bk, G, causal, causal, 64)
+        cnt, idx = stages.select_segments(qs[:, :, J0:J0 + nc], kd, J0, float(gaps[0]), None,
+                                          causal, qps, bk, G, causal, segk)
+        lists = SegmentedLists(cnt, idx, J0, nc, qps, S, causal, causal, segk)
+        for h in range(Hq):
+            for jr in range(nc):
+                assert np.array_equal(lists.row(0, h, jr), want[0][h][jr]), (name, h, J0 + jr)
+    assert want_c.sum() > 0
+
+
 # (the wave kernel takes tiles of at most 64 keys)
 STRESS_PARAMS = [pytest.param(case, kern, id=f"{case[0]}-{kid}") for case in MFMA_STRESS
                  for kern, kid in ((nat.VA_SEL_MFMA, "mfma"), (nat.VA_SEL_WAVE, "wave"))

@@ -223,9 +223,12 @@ def test_prefill_kernels_reports_the_mfma_path(L):
 def test_prefill_kernels_reports_the_slow_paths(L):
     # the reference signature's default tiles (q_pooling_size and k_local_size
     # 128): the 64-row MFMA selection (the wave kernel takes tiles up to 64)
-    f = _plan(L, qps=128, bk=128, G=1)
-    assert f == nat.VA_KERNELS_SELECT_MFMA | nat.VA_KERNELS_ATTN_MFMA
-    assert _plan(L, bk=256, G=2) == nat.VA_KERNELS_SELECT_MFMA | nat.VA_KERNELS_ATTN_MFMA
+    # in key segments of whole 256-key chunks
+    mfma = nat.VA_KERNELS_SELECT_MFMA | nat.VA_KERNELS_ATTN_MFMA | nat.VA_KERNELS_SPLIT
+    assert _plan(L, qps=128, bk=128, G=1) == mfma
+    assert _plan(L, bk=256, G=2) == mfma
+    # one group per row: no carry pass on this kernel, so no split
+    assert _plan(L, bk=128, G=8192) == nat.VA_KERNELS_SELECT_MFMA | nat.VA_KERNELS_ATTN_MFMA
     assert _plan(L, bk=512, G=1) & nat.VA_KERNELS_SELECT_EXACT
     # fp32 inputs: exact selection and the per-row attention
     f = _plan(L, dtype=nat.VA_F32)

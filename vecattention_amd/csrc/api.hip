@@ -33,7 +33,7 @@ hipError_t launch_select_mfma(int dtype, const void* qs, int64_t sqb, int64_t sq
                               int64_t Hq, int64_t Hk, int64_t Sk, int64_t D, int64_t qps,
                               int64_t bk, int64_t group, int causal, int64_t bsq, float gap,
                               const float* gaps, const float* kmax, const RowLayout& lay,
-                              int32_t* counts, int32_t* indices, hipStream_t stream);
+                              int32_t* counts, int32_t* indices, int64_t segk, hipStream_t stream);
 bool select_wave_supported(int dtype, int64_t D, int64_t bk, int64_t group);
 hipError_t launch_select_wave(int dtype, const void* qs, int64_t sqb, int64_t sqh, int64_t sqn,
                               const void* k, int64_t skb, int64_t skh, int64_t sks, int64_t B,
@@ -218,7 +218,7 @@ static int select_impl(int dtype, const void* qs, int64_t sqb, int64_t sqh, int6
   else if (which == kSelMfma)
     e = va::launch_select_mfma(dtype, qs, sqb, sqh, sqn, k, skb, skh, sks, B, Hq, Hk, Sk, D, qps,
                                bk, group, causal, bsq, gap, gaps, kmax, lay, counts, indices,
-                               stream);
+                               segk, stream);
   else
     e = va::launch_select_exact(dtype, qs, sqb, sqh, sqn, k, skb, skh, sks, B, Hq, Hk, Sk, D,
                                 qps, bk, group, causal, bsq, gap, gaps, lay, counts, indices,
@@ -337,8 +337,6 @@ int va_select_segments(int dtype, const void* qs, int64_t sqb, int64_t sqh, int6
   if (!counts || !indices) return fail(VA_ERR_ARG, "null output pointer");
   if (dense_stride < 0 || (dense_stride > 0 && dense_stride < Sk))
     return fail(VA_ERR_ARG, "invalid dense_stride");
-  if (!select_wave_ok(dtype, qs, sqb, sqh, sqn, k, skb, skh, sks, Sk, D, bk, group))
-    return fail(VA_ERR_UNSUPPORTED, "segmented selection needs the wave selection kernel");
   const int64_t gs = bk * effective_group(group, Sk, bk);
   if (segment_keys <= 0 || segment_keys % 64 || cdiv(Sk, segment_keys) > 64 ||
       (segment_keys % gs != 0 && gs < Sk))
@@ -346,6 +344,17 @@ int va_select_segments(int dtype, const void* qs, int64_t sqb, int64_t sqh, int6
                             "(%lld keys) unless one group covers the row, at most 64 segments",
                 (long long)segment_keys, (long long)gs);
   const bool two_pass = segments_two_pass(Sk, bk, group, segment_keys);
+  // The wave kernel takes every split; the 64-row MFMA kernel (tiles of 128
+  // and 256 keys) takes segments of whole 256-key chunks that start groups.
+  const SelKernel which =
+      select_wave_ok(dtype, qs, sqb, sqh, sqn, k, skb, skh, sks, Sk, D, bk, group) ? kSelWave
+      : (!two_pass && segment_keys % 256 == 0 &&
+         select_mfma_ok(dtype, qs, sqb, sqh, sqn, k, skb, skh, sks, D, bk))
+          ? kSelMfma
+          : kSelExact;
+  if (which == kSelExact)
+    return fail(VA_ERR_UNSUPPORTED, "segmented selection needs the wave selection kernel, or "
+                                    "the MFMA kernel with segments of whole 256-key chunks");
   const int64_t need = va_select_segments_scratch_floats(B, Hq, Hk, Sk, nc, segment_keys, bk, group);
   if (!scratch || scratch_floats < need)
     return fail(VA_ERR_ARG, "segmented selection needs %lld scratch floats", (long long)need);
@@ -362,7 +371,7 @@ int va_select_segments(int dtype, const void* qs, int64_t sqb, int64_t sqh, int6
   }
   rc = select_impl(dtype, qs, sqb, sqh, sqn, k, skb, skh, sks, B, Hq, Hk, Sk, D, qps, bk, group,
                    causal, wo_init, J0, nc, bsq, gap, gaps, dense_stride, counts, indices,
-                   kSelWave, scratch, segment_keys, st, carry,
+                   which, scratch, segment_keys, st, carry,
                    two_pass ? va::kPassCarry : va::kPassPlain);
   return rc ? rc : ok();
 }
@@ -788,9 +797,11 @@ int va_prefill_kernels(int dtype, const void* q, int64_t sqb, int64_t sqh, int64
                 so[3] = {sob, soh, sos};
   const bool attn = attn_mfma_check(dtype, q, sq, k, sk, v, sv, out, so, Sk, D, qps).ok();
   flags |= attn ? VA_KERNELS_ATTN_MFMA : VA_KERNELS_ATTN_ROW;
-  if (wave && attn) {
+  if (attn && (flags & (VA_KERNELS_SELECT_WAVE | VA_KERNELS_SELECT_MFMA))) {
     const int64_t g = effective_group(group, Sk, bk);
-    if (va::select_wave_segment_keys(Sk, bk, g) > 0 || va::select_wave_carry_segment_keys(Sk, bk, g) > 0)
+    const int64_t sg = va::select_wave_segment_keys(Sk, bk, g);
+    if (wave ? (sg > 0 || va::select_wave_carry_segment_keys(Sk, bk, g) > 0)
+             : (sg > 0 && sg % 256 == 0))
       flags |= VA_KERNELS_SPLIT;
   }
   ok();
@@ -857,14 +868,18 @@ int va_prefill(int dtype, const void* q, int64_t sqb, int64_t sqh, int64_t sqs, 
   {
     const int64_t sq[3] = {sqb, sqh, sqs}, sk[3] = {skb, skh, sks}, sv[3] = {svb, svh, svs},
                   so[3] = {sob, soh, sos};
-    if (which == kSelWave &&
-        attn_mfma_check(dtype, q, sq, k, sk, v, sv, out, so, Sk, D, qps).ok()) {
-      const int64_t g = effective_group(group, Sk, bk);
+    const bool attn = attn_mfma_check(dtype, q, sq, k, sk, v, sv, out, so, Sk, D, qps).ok();
+    const int64_t g = effective_group(group, Sk, bk);
+    if (which == kSelWave && attn) {
       segk = va::select_wave_segment_keys(Sk, bk, g);
       if (segk == 0) {
         segk = va::select_wave_carry_segment_keys(Sk, bk, g);
         two_pass = segk > 0;
       }
+    } else if (which == kSelMfma && attn) {
+      // the 64-row MFMA kernel splits at whole 256-key chunks (no carry pass)
+      const int64_t sg = va::select_wave_segment_keys(Sk, bk, g);
+      if (sg > 0 && sg % 256 == 0) segk = sg;
     }
   }
   const float scale = float(1.0 / std::sqrt(double(D)));
@@ -874,12 +889,14 @@ int va_prefill(int dtype, const void* q, int64_t sqb, int64_t sqh, int64_t sqs, 
   // covers 128 rows of one segment); the attention of the group reads the
   // lists with the same length.
   const int64_t gspan = segk > 0 && !two_pass ? bk * effective_group(group, Sk, bk) : 0;
+  const int64_t wg_rows = which == kSelWave ? 128 : 64;  // pooled rows per selection work-group
   auto group_segk = [&](int64_t nc) {
     constexpr int64_t kMinSelectBlocks = 1536, kMinSeg = 2048;
     int64_t sg = segk;
     if (gspan <= 0) return sg;
-    while (sg / 2 >= kMinSeg && (sg / 2) % gspan == 0 && cdiv(Sk, sg / 2) <= kMaxSegments &&
-           cdiv(nc, 128) * cdiv(Sk, sg) * B * Hq < kMinSelectBlocks)
+    while (sg / 2 >= kMinSeg && (sg / 2) % gspan == 0 && (sg / 2) % 256 == 0 &&
+           cdiv(Sk, sg / 2) <= kMaxSegments &&
+           cdiv(nc, wg_rows) * cdiv(Sk, sg) * B * Hq < kMinSelectBlocks)
       sg /= 2;
     return sg;
   };

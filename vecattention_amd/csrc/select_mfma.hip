@@ -87,7 +87,8 @@ __global__ __launch_bounds__(256) void select_mfma_kernel(
     int64_t skb, int64_t skh, int64_t sks, int64_t B, int64_t Hq, int64_t Hk, int64_t Sk,
     int64_t qps, int bk, uint32_t gspan, int causal, int64_t bsq, float gap_scalar,
     const float* __restrict__ gaps, const float* __restrict__ kmax, RowLayout lay,
-    int32_t* __restrict__ counts, int32_t* __restrict__ indices, int64_t nrowsets) {
+    int32_t* __restrict__ counts, int32_t* __restrict__ indices, int64_t nrowsets, int segk,
+    int nseg) {
   using M = Mfma<T>;
   using vec = typename M::vec;
   constexpr int NS = D / 16;        // MFMA steps over the features
@@ -117,9 +118,15 @@ __global__ __launch_bounds__(256) void select_mfma_kernel(
   const int wave = tid >> 6, lane = tid & 63;
   const int l32 = lane & 31, hh = lane >> 5;
 
-  const WorkOrder wo{nrowsets, B, Hq, Hk, causal == 0};
-  int64_t rs, bh;
-  if (!wo.map_item(blockIdx.x, rs, bh)) return;  // idle block (uniform)
+  const WorkOrder wo{nrowsets * nseg, B, Hq, Hk, causal == 0};
+  int64_t item, bh;
+  if (!wo.map_item(blockIdx.x, item, bh)) return;  // idle block (uniform)
+  // Key segment [seg*segk, (seg+1)*segk) of the split selection (one segment
+  // covering every key when nseg == 1); segments are multiples of the group
+  // span and of the 256-key chunk, so each starts a group and a chunk.
+  const int64_t rs = item / nseg;
+  const int seg = int(item % nseg);
+  const int64_t seg_lo = nseg > 1 ? int64_t(seg) * segk : 0;
   const int64_t b = bh / Hq, h = bh % Hq, hk = h / (Hq / Hk);
   const int64_t jr0 = rs * kMR;
   const int64_t nc = lay.nc, J0 = lay.J0;
@@ -128,12 +135,16 @@ __global__ __launch_bounds__(256) void select_mfma_kernel(
   const float kn = kmax[b * Hk + hk];
   const int64_t smin = lay.smin();
   const int lbk = __builtin_ctz(uint32_t(bk));  // bk is a power of two
-  const int64_t kstart = smin;
+  const int64_t kstart = seg_lo > smin ? seg_lo : smin;
   int64_t kend = Sk;
   if (causal) {
     const int64_t lim = (J0 + jr0 + rows_here - 1) * qps;
     if (lim < kend) kend = lim;
   }
+  if (nseg > 1 && seg_lo + segk < kend) kend = seg_lo + segk;
+  // The segment writes its keys from slot kstart - smin of each row (the slot
+  // of its first selectable key): segments never overlap.
+  const int64_t seg_slot = kstart - smin;
   const T* qbase = qs + b * sqb + h * sqh;
   const T* kbh = k + b * skb + hk * skh;
 
@@ -175,8 +186,9 @@ __global__ __launch_bounds__(256) void select_mfma_kernel(
     int64_t lim = 0x7fffffff;
     if (causal) lim = (r == 0) ? (J - 1) * qps + 1 : J * qps;
     klim[tid] = int32_t(lim < 0 ? 0 : (lim > 0x7fffffff ? 0x7fffffff : lim));
-    rowoff[tid] = tid < rows_here ? lay.row_offset(bh, jr) : 0;
-    rowcap[tid] = tid < rows_here ? lay.capacity(J) : 0;
+    rowoff[tid] = tid < rows_here ? lay.row_offset(bh, jr) + seg_slot : 0;
+    const int64_t capr = tid < rows_here ? lay.capacity(J) - seg_slot : 0;
+    rowcap[tid] = capr > 0 ? capr : 0;
   }
   // Q^T operands of all 64 rows: row 32*rb + l32, features (D/2)*hh + 8*s.
   vec qop[2][NS];
@@ -541,7 +553,7 @@ __global__ __launch_bounds__(256) void select_mfma_kernel(
   if (tid < rows_here) {
     const int64_t cap = rowcap[tid];
     const int32_t c = rcnt[tid];
-    counts[bh * nc + jr0 + tid] = (c < cap) ? c : int32_t(cap);
+    counts[(bh * nc + jr0 + tid) * nseg + seg] = (c < cap) ? c : int32_t(cap);
   }
 }
 
@@ -557,17 +569,18 @@ static hipError_t launch_select_mfma_td(const void* qs, int64_t sqb, int64_t sqh
                                         int64_t bk, int64_t group, int causal, int64_t bsq,
                                         float gap, const float* gaps, const float* kmax,
                                         const RowLayout& lay, int32_t* counts, int32_t* indices,
-                                        hipStream_t stream) {
+                                        int64_t segk, hipStream_t stream) {
   const int64_t nrowsets = (lay.nc + kMR - 1) / kMR;
+  const int64_t nseg = segk > 0 ? (Sk + segk - 1) / segk : 1;
   // Group span in keys, capped at 2^31 (key offsets are below 2^31, so a span
   // that large has its only boundary at 0 either way).
   const int64_t gs = (group > (int64_t(1) << 31) / bk) ? (int64_t(1) << 31) : bk * group;
   const uint32_t gspan32 = uint32_t(gs);
-  const int64_t nblocks = WorkOrder{nrowsets, B, Hq, Hk, causal == 0}.grid_items();
+  const int64_t nblocks = WorkOrder{nrowsets * nseg, B, Hq, Hk, causal == 0}.grid_items();
   hipLaunchKernelGGL((select_mfma_kernel<T, D>), dim3(unsigned(nblocks)), dim3(256), 0,
                      stream, static_cast<const T*>(qs), sqb, sqh, sqn, static_cast<const T*>(k),
                      skb, skh, sks, B, Hq, Hk, Sk, qps, int(bk), gspan32, causal, bsq, gap, gaps,
-                     kmax, lay, counts, indices, nrowsets);
+                     kmax, lay, counts, indices, nrowsets, int(segk), int(nseg));
   return hipGetLastError();
 }
 
@@ -576,11 +589,12 @@ hipError_t launch_select_mfma(int dtype, const void* qs, int64_t sqb, int64_t sq
                               int64_t Hq, int64_t Hk, int64_t Sk, int64_t D, int64_t qps,
                               int64_t bk, int64_t group, int causal, int64_t bsq, float gap,
                               const float* gaps, const float* kmax, const RowLayout& lay,
-                              int32_t* counts, int32_t* indices, hipStream_t stream) {
+                              int32_t* counts, int32_t* indices, int64_t segk,
+                              hipStream_t stream) {
 #define VA_SEL_CASE(TT, DD)                                                                     \
   return launch_select_mfma_td<TT, DD>(qs, sqb, sqh, sqn, k, skb, skh, sks, B, Hq, Hk, Sk, qps, \
                                        bk, group, causal, bsq, gap, gaps, kmax, lay, counts,    \
-                                       indices, stream);
+                                       indices, segk, stream);
   if (dtype == kBF16 && D == 128) { VA_SEL_CASE(bf16_t, 128) }
   if (dtype == kBF16 && D == 64) { VA_SEL_CASE(bf16_t, 64) }
   if (dtype == kF16 && D == 128) { VA_SEL_CASE(f16_t, 128) }
