@@ -272,7 +272,9 @@ int64_t va_prefill_workspace_size(int dtype, int64_t B, int64_t Hq, int64_t Sq, 
  * (negative on invalid sizes): the selection on the certified MFMA wave kernel
  * (VA_KERNELS_SELECT_WAVE), the 64-row MFMA kernel (VA_KERNELS_SELECT_MFMA) or
  * the exact fp64 kernel (VA_KERNELS_SELECT_EXACT: fp32 inputs, D outside
- * {64, 128}, k_local_size outside {16, 32, 64}, unaligned K); the attention on
+ * {64, 128}, k_local_size outside {16, 32, 64, 128, 256}, unaligned K; the
+ * wave kernel takes tiles of 16 to 64 keys, the 64-row MFMA kernel 128 and
+ * 256); the attention on
  * the MFMA kernel (VA_KERNELS_ATTN_MFMA) or the per-row kernel
  * (VA_KERNELS_ATTN_ROW: fp32, D or q_pooling_size outside {64, 128}, K/V row
  * strides of 16 KiB or more, unaligned tensors); VA_KERNELS_SPLIT when the

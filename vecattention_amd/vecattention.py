@@ -89,7 +89,7 @@ def _warn_slow_path(flags, dtype, head_dim, q_pooling_size, k_local_size):
     reasons = []
     if flags & nat.VA_KERNELS_SELECT_EXACT:
         reasons.append("the selection runs on the exact fp64 kernel (the MFMA selection takes "
-                       "bf16/fp16, head_dim 64 or 128, k_local_size 16, 32 or 64 and 16-byte "
+                       "bf16/fp16, head_dim 64 or 128, k_local_size 16 to 256 and 16-byte "
                        "aligned keys)")
     if flags & nat.VA_KERNELS_ATTN_ROW:
         reasons.append("the attention runs on the per-row kernel (the MFMA attention takes "
