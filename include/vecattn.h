@@ -42,7 +42,13 @@ enum {
   VA_ERR_WORKSPACE = -4     /* workspace smaller than its *_workspace_size() query */
 };
 
-enum { VA_ATTN_AUTO = 0, VA_ATTN_MFMA = 1, VA_ATTN_SIMPLE = 2 };
+enum {
+  VA_ATTN_AUTO = 0,
+  VA_ATTN_MFMA = 1,
+  VA_ATTN_SIMPLE = 2,
+  VA_ATTN_MFMA_STAGED = 3,
+  VA_ATTN_MFMA_RING = 4
+};
 enum { VA_SEL_AUTO = 0, VA_SEL_EXACT = 1, VA_SEL_MFMA = 2, VA_SEL_WAVE = 3 };
 
 /* Library version (major*10000 + minor*100 + patch). */
@@ -158,7 +164,13 @@ int64_t va_select_row_offset(int64_t Sk, int64_t q_pooling_size, int causal, int
  * spattn/src/VecAttention.py:104-121 (vertical + local-block semantics of
  * spattn/threshold/model_tuner.py:193-216).  Rows with no key are 0.
  * `kernel`: VA_ATTN_AUTO (MFMA for bf16/fp16, D in {64,128}, qps in {64,128};
- * otherwise the per-row kernel), VA_ATTN_MFMA or VA_ATTN_SIMPLE.
+ * otherwise the per-row kernel), VA_ATTN_MFMA or VA_ATTN_SIMPLE.  The MFMA
+ * kernel's loop has two forms at D = 128, qps = 64, which VA_ATTN_AUTO and
+ * VA_ATTN_MFMA pick by shape: staged (two stages of a K and a V tile, two
+ * work-groups per CU) and ring (three tile slots, three work-groups per CU);
+ * VA_ATTN_MFMA_STAGED and VA_ATTN_MFMA_RING force one (the ring form only at
+ * D = 128, qps = 64, bf16/fp16; VA_ERR_UNSUPPORTED otherwise).  Both run the
+ * same arithmetic in the same order, so their outputs are bit-identical.
  */
 int va_sparse_attn(int dtype, const void* q, int64_t sqb, int64_t sqh, int64_t sqs,
                    const void* k, int64_t skb, int64_t skh, int64_t sks, const void* v,
@@ -277,8 +289,9 @@ int64_t va_prefill_workspace_size(int dtype, int64_t B, int64_t Hq, int64_t Sq, 
  * 256); the attention on
  * the MFMA kernel (VA_KERNELS_ATTN_MFMA) or the per-row kernel
  * (VA_KERNELS_ATTN_ROW: fp32, D or q_pooling_size outside {64, 128}, K/V row
- * strides of 16 KiB or more, unaligned tensors); VA_KERNELS_SPLIT when the
- * selection runs in key segments.  The exact selection and the per-row
+ * strides of 16 KiB or more, unaligned tensors), with VA_KERNELS_ATTN_RING
+ * when that kernel runs its ring form (see va_sparse_attn); VA_KERNELS_SPLIT
+ * when the selection runs in key segments.  The exact selection and the per-row
  * attention are several times slower than the MFMA kernels.  No counterpart
  * in the reference: it lets callers see which path a configuration takes.
  */
@@ -288,11 +301,12 @@ int64_t va_prefill_workspace_size(int dtype, int64_t B, int64_t Hq, int64_t Sq, 
 #define VA_KERNELS_ATTN_MFMA 16
 #define VA_KERNELS_ATTN_ROW 32
 #define VA_KERNELS_SPLIT 64
+#define VA_KERNELS_ATTN_RING 128
 int va_prefill_kernels(int dtype, const void* q, int64_t sqb, int64_t sqh, int64_t sqs,
                        const void* k, int64_t skb, int64_t skh, int64_t sks, const void* v,
                        int64_t svb, int64_t svh, int64_t svs, const void* out, int64_t sob,
-                       int64_t soh, int64_t sos, int64_t Sk, int64_t D, int64_t q_pooling_size,
-                       int64_t k_local_size, int64_t group_k_block);
+                       int64_t soh, int64_t sos, int64_t Hq, int64_t Hk, int64_t Sk, int64_t D,
+                       int64_t q_pooling_size, int64_t k_local_size, int64_t group_k_block);
 
 /*
  * The whole VecAttention prefill: pooling, then per query chunk selection and

@@ -393,21 +393,18 @@ ATTN_CASES = [
 ]
 
 
-@pytest.mark.parametrize("kernel", [nat.VA_ATTN_AUTO, nat.VA_ATTN_SIMPLE], ids=["auto", "simple"])
-@pytest.mark.parametrize("case", ATTN_CASES, ids=[c[0] for c in ATTN_CASES])
-def test_sparse_attention_matches_oracle(device, case, kernel):
+ATTN_KERNELS = [nat.VA_ATTN_AUTO, nat.VA_ATTN_SIMPLE, nat.VA_ATTN_MFMA_STAGED,
+                nat.VA_ATTN_MFMA_RING]
+
+
+def _oracle_lists_as_layout(q, k, case):
+    # The oracle's selection of the case, laid out as the index workspace.
     name, B, Hq, Hk, Sq, Sk, D, dtype, causal, qps, keep = case
-    note("attn", name, kernel)
-    g = torch.Generator().manual_seed(len(name))
-    q, k, v = make_inputs(B, Hq, Hk, max(Sq, Sk), D, dtype, seed=len(name) + 1)
-    q = q[:, :, :Sq].contiguous()
-    k, v = k[:, :, :Sk].contiguous(), v[:, :, :Sk].contiguous()
     th = calibrated_threshold(keep, q, k, qps, 16, 16, causal) if Sq == Sk else 0.3
     _, qs_cpu = orc.pool(q, qps, DTN[dtype])
     nqb = qs_cpu.shape[2]
     gaps = orc.gap_from_threshold(th, B, Hq)
     _, lists = orc.select(qs_cpu, k, 0, nqb, gaps, qps, 16, 16, causal, causal, 64)
-    # Feed the oracle's lists to the GPU kernel through the index layout.
     caps = [orc.row_capacity(J, qps, Sk, causal, causal) for J in range(nqb)]
     idx = np.zeros(max(sum(caps) * B * Hq, 1), np.int32)
     cnt = np.zeros((B, Hq, nqb), np.int32)
@@ -419,15 +416,55 @@ def test_sparse_attention_matches_oracle(device, case, kernel):
                 idx[base:base + len(l)] = l
                 cnt[b, h, J] = len(l)
                 base += caps[J]
+    return nqb, lists, torch.from_numpy(cnt), torch.from_numpy(idx)
+
+
+@pytest.mark.parametrize("kernel", ATTN_KERNELS, ids=["auto", "simple", "staged", "ring"])
+@pytest.mark.parametrize("case", ATTN_CASES, ids=[c[0] for c in ATTN_CASES])
+def test_sparse_attention_matches_oracle(device, case, kernel):
+    name, B, Hq, Hk, Sq, Sk, D, dtype, causal, qps, keep = case
+    note("attn", name, kernel)
+    q, k, v = make_inputs(B, Hq, Hk, max(Sq, Sk), D, dtype, seed=len(name) + 1)
+    q = q[:, :, :Sq].contiguous()
+    k, v = k[:, :, :Sk].contiguous(), v[:, :, :Sk].contiguous()
+    nqb, lists, cnt, idx = _oracle_lists_as_layout(q, k, case)
     out = torch.zeros(B, Hq, Sq, D, dtype=dtype, device=device)
-    stages.sparse_attention(q.to(device), k.to(device), v.to(device), out, 0, nqb,
-                            torch.from_numpy(cnt).to(device), torch.from_numpy(idx).to(device),
-                            causal, qps, kernel=kernel)
+    run = lambda: stages.sparse_attention(q.to(device), k.to(device), v.to(device), out, 0, nqb,
+                                          cnt.to(device), idx.to(device), causal, qps,
+                                          kernel=kernel)
+    mfma_ok = dtype != torch.float32
+    ring_ok = mfma_ok and D == 128 and qps == 64
+    if (kernel == nat.VA_ATTN_MFMA_RING and not ring_ok) or (
+            kernel == nat.VA_ATTN_MFMA_STAGED and not mfma_ok):
+        with pytest.raises(NotImplementedError):  # the form does not exist for this shape
+            run()
+        return
+    run()
     bc, bi = orc.local_blocks(B, Hq, Sq, qps, causal)
     want = orc.attention(q, k, v, qps, causal, bc, bi, lists)
     err = np.abs(out.float().cpu().numpy() - want)
     tol = (ATOL_MAX_F32, ATOL_MEAN_F32) if dtype == torch.float32 else (ATOL_MAX, ATOL_MEAN)
     assert err.max() <= tol[0] and err.mean() <= tol[1], (err.max(), err.mean())
+
+
+@pytest.mark.parametrize("case", [c for c in ATTN_CASES if c[6] == 128 and c[9] == 64 and
+                                  c[7] != torch.float32], ids=lambda c: c[0])
+def test_attention_forms_are_bit_identical(device, case):
+    # The staged and ring forms of the MFMA loop run the same arithmetic in
+    # the same order.
+    name, B, Hq, Hk, Sq, Sk, D, dtype, causal, qps, keep = case
+    note("attn forms", name)
+    q, k, v = make_inputs(B, Hq, Hk, max(Sq, Sk), D, dtype, seed=len(name) + 7)
+    q = q[:, :, :Sq].contiguous()
+    k, v = k[:, :, :Sk].contiguous(), v[:, :, :Sk].contiguous()
+    nqb, _, cnt, idx = _oracle_lists_as_layout(q, k, case)
+    outs = []
+    for kernel in (nat.VA_ATTN_MFMA_STAGED, nat.VA_ATTN_MFMA_RING):
+        out = torch.full((B, Hq, Sq, D), 7.0, dtype=dtype, device=device)
+        stages.sparse_attention(q.to(device), k.to(device), v.to(device), out, 0, nqb,
+                                cnt.to(device), idx.to(device), causal, qps, kernel=kernel)
+        outs.append(out)
+    assert torch.equal(outs[0], outs[1])
 
 
 def test_mfma_all_keys_equals_dense_sdpa(device):

@@ -202,22 +202,29 @@ def test_decode_argument_errors_before_launch(L):
     assert _decode(L, kernel=9) == nat.VA_ERR_ARG
 
 
-def _plan(L, dtype=nat.VA_BF16, D=128, qps=64, bk=16, G=16, Sk=32768, kv_row=None, align=256):
+def _plan(L, dtype=nat.VA_BF16, D=128, qps=64, bk=16, G=16, Sk=32768, kv_row=None, align=256,
+          Hq=28, Hk=4):
     # va_prefill_kernels only inspects addresses and strides (no device access):
     # plain integers stand for the tensors' addresses.
     row = D if kv_row is None else kv_row
     q, k, v, out = align, 2 * align, 3 * align, 4 * align
     return L.va_prefill_kernels(dtype, q, 8 * Sk * D, Sk * D, D, k, 8 * Sk * row, Sk * row, row,
-                                v, 8 * Sk * row, Sk * row, row, out, 8 * Sk * D, Sk * D, D, Sk, D,
-                                qps, bk, G)
+                                v, 8 * Sk * row, Sk * row, row, out, 8 * Sk * D, Sk * D, D, Hq,
+                                Hk, Sk, D, qps, bk, G)
 
 
 def test_prefill_kernels_reports_the_mfma_path(L):
-    f = _plan(L)
-    assert f == nat.VA_KERNELS_SELECT_WAVE | nat.VA_KERNELS_ATTN_MFMA | nat.VA_KERNELS_SPLIT
+    fast = nat.VA_KERNELS_SELECT_WAVE | nat.VA_KERNELS_ATTN_MFMA | nat.VA_KERNELS_SPLIT
+    ring = nat.VA_KERNELS_ATTN_RING
+    assert _plan(L) == fast | ring                            # 32K causal GQA
+    assert _plan(L, Sk=131072) == fast | ring                 # 128K: 7 q heads per kv head
     # one group per row (DiT group_k_block): the two-pass split
-    f = _plan(L, G=8192, Sk=32760)
-    assert f == nat.VA_KERNELS_SELECT_WAVE | nat.VA_KERNELS_ATTN_MFMA | nat.VA_KERNELS_SPLIT
+    assert _plan(L, G=8192, Sk=32760, Hq=12, Hk=12) == fast | ring
+    # unshared kv heads whose K and V pass 32 MiB a head: the staged form
+    assert _plan(L, G=8192, Sk=119056, Hq=24, Hk=24) == fast
+    # the ring form exists for D = 128 and 64-row blocks only
+    assert not _plan(L, D=64) & ring and not _plan(L, qps=128) & ring
+    assert _plan(L, Hq=6, Hk=4) == nat.VA_ERR_ARG             # q heads not a multiple
 
 
 def test_prefill_kernels_reports_the_slow_paths(L):
@@ -226,9 +233,10 @@ def test_prefill_kernels_reports_the_slow_paths(L):
     # in key segments of whole 256-key chunks
     mfma = nat.VA_KERNELS_SELECT_MFMA | nat.VA_KERNELS_ATTN_MFMA | nat.VA_KERNELS_SPLIT
     assert _plan(L, qps=128, bk=128, G=1) == mfma
-    assert _plan(L, bk=256, G=2) == mfma
+    assert _plan(L, bk=256, G=2) == mfma | nat.VA_KERNELS_ATTN_RING
     # one group per row: no carry pass on this kernel, so no split
-    assert _plan(L, bk=128, G=8192) == nat.VA_KERNELS_SELECT_MFMA | nat.VA_KERNELS_ATTN_MFMA
+    assert _plan(L, bk=128, G=8192) == (nat.VA_KERNELS_SELECT_MFMA | nat.VA_KERNELS_ATTN_MFMA |
+                                        nat.VA_KERNELS_ATTN_RING)
     assert _plan(L, bk=512, G=1) & nat.VA_KERNELS_SELECT_EXACT
     # fp32 inputs: exact selection and the per-row attention
     f = _plan(L, dtype=nat.VA_F32)

@@ -16,9 +16,11 @@ LIB_PATH = os.path.join(_HERE, "libvecattn.so")
 VA_F32, VA_BF16, VA_F16 = 0, 1, 2
 VA_OK, VA_ERR_ARG, VA_ERR_UNSUPPORTED, VA_ERR_HIP, VA_ERR_WORKSPACE = 0, -1, -2, -3, -4
 VA_ATTN_AUTO, VA_ATTN_MFMA, VA_ATTN_SIMPLE = 0, 1, 2
+VA_ATTN_MFMA_STAGED, VA_ATTN_MFMA_RING = 3, 4  # forms of the MFMA kernel's loop
 VA_SEL_AUTO, VA_SEL_EXACT, VA_SEL_MFMA, VA_SEL_WAVE = 0, 1, 2, 3
 VA_KERNELS_SELECT_WAVE, VA_KERNELS_SELECT_MFMA, VA_KERNELS_SELECT_EXACT = 1, 2, 4
 VA_KERNELS_ATTN_MFMA, VA_KERNELS_ATTN_ROW, VA_KERNELS_SPLIT = 16, 32, 64
+VA_KERNELS_ATTN_RING = 128
 
 _DTYPES = {torch.float32: VA_F32, torch.bfloat16: VA_BF16, torch.float16: VA_F16}
 
@@ -71,7 +73,7 @@ SIGNATURES = {
     "va_prefill_workspace_size": (_i64, [_int, _i64, _i64, _i64, _i64, _i64, _i64, _int, _i64]),
     "va_prefill_kernels": (_int, [_int, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _vp, _i64,
                                   _i64, _i64, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
-                                  _i64]),
+                                  _i64, _i64, _i64]),
     "va_prefill": (_int, [_int, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _vp, _i64, _i64,
                           _i64, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _f32,
                           _vp, _i64, _i64, _i64, _int, _i64, _i64, _vp, _i64, _vp]),

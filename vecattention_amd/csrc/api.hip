@@ -54,8 +54,10 @@ hipError_t launch_attn_mfma(int dtype, int64_t D, int64_t qps, const void* q, co
                             void* out, const int64_t* so, int64_t B, int64_t Hq, int64_t Hk,
                             int64_t Sq, int64_t Sk, int causal, float scale_log2,
                             const int32_t* counts, const int32_t* indices, const RowLayout& lay,
-                            int nseg, int segk, int64_t dense_qoff, float* stats,
+                            int nseg, int segk, int64_t dense_qoff, float* stats, int form,
                             hipStream_t stream);
+bool attn_mfma_ring_supported(int dtype, int64_t D, int64_t qps);
+bool ring_form_preferred(int64_t Hq, int64_t Hk, int64_t Sk, int64_t D);
 hipError_t launch_attn_split(int dtype, int64_t D, const void* q, const int64_t* sq,
                              const void* k, const int64_t* sk, const void* v, const int64_t* sv,
                              int64_t B, int64_t H, int64_t Sq, int64_t Sk, float scale_log2,
@@ -420,6 +422,14 @@ static int attn_dispatch(int dtype, const void* q, const int64_t* sq, const void
                                   : attn_mfma_check(dtype, q, sq, k, sk, v, sv, out, so, Sk, D, qps);
   const bool mfma_shape = chk.shape, mfma_align = chk.align, mfma_span = chk.span;
   bool use_mfma = false;
+  int form = va::kAttnFormAuto;
+  if (kernel == VA_ATTN_MFMA_STAGED || kernel == VA_ATTN_MFMA_RING) {
+    if (kernel == VA_ATTN_MFMA_RING && (stats || !va::attn_mfma_ring_supported(dtype, D, qps)))
+      return fail(VA_ERR_UNSUPPORTED, "the ring form needs bf16/fp16, D = 128, qps = 64 and "
+                                      "attention output (not row statistics)");
+    form = kernel == VA_ATTN_MFMA_RING ? va::kAttnFormRing : va::kAttnFormStaged;
+    kernel = VA_ATTN_MFMA;
+  }
   if (kernel == VA_ATTN_MFMA) {
     if (!mfma_shape)
       return fail(VA_ERR_UNSUPPORTED, "MFMA attention needs bf16/fp16, D in {64,128}, qps in {64,128}");
@@ -441,7 +451,7 @@ static int attn_dispatch(int dtype, const void* q, const int64_t* sq, const void
   hipError_t e = use_mfma
                      ? va::launch_attn_mfma(dtype, D, qps, q, sq, k, sk, v, sv, out, so, B, Hq,
                                             Hk, Sq, Sk, causal, scale_log2, counts, indices, lay,
-                                            nseg, int(segk), -1, stats, stream)
+                                            nseg, int(segk), -1, stats, form, stream)
                      : va::launch_attn_simple(dtype, q, sq, k, sk, v, sv, out, so, B, Hq, Hk, Sq,
                                               Sk, D, qps, causal, scale_log2, counts, indices,
                                               lay, -1, stats, stream);
@@ -517,7 +527,7 @@ int va_dense_attn(int dtype, const void* q, int64_t sqb, int64_t sqh, int64_t sq
   const hipError_t e = va::launch_attn_mfma(
       dtype, D, qps, q, sq, k, sk, v, sv, out, so, B, Hq, Hk, Sq, Sk, causal,
       softmax_scale * 1.4426950408889634f, nullptr, nullptr, lay, 1, 0,
-      causal ? Sk - Sq : 0, nullptr, static_cast<hipStream_t>(stream));
+      causal ? Sk - Sq : 0, nullptr, va::kAttnFormAuto, static_cast<hipStream_t>(stream));
   const int rc = hip_check(e, "dense attention launch");
   return rc ? rc : ok();
 }
@@ -572,7 +582,7 @@ int va_dense_row_stats(int dtype, const void* q, int64_t sqb, int64_t sqh, int64
   const hipError_t e =
       use_mfma ? va::launch_attn_mfma(dtype, D, qps, q, sq, k, sk, nullptr, sk, nullptr, sq, B, Hq,
                                       Hk, Sq, Sk, causal, scale_log2, nullptr, nullptr, lay, 1, 0,
-                                      qoff, stats, st)
+                                      qoff, stats, va::kAttnFormAuto, st)
                : va::launch_attn_simple(dtype, q, sq, k, sk, nullptr, sk, nullptr, sq, B, Hq, Hk,
                                         Sq, Sk, D, qps, causal, scale_log2, nullptr, nullptr, lay,
                                         qoff, stats, st);
@@ -777,9 +787,10 @@ int64_t va_prefill_workspace_size(int dtype, int64_t B, int64_t Hq, int64_t Sq, 
 int va_prefill_kernels(int dtype, const void* q, int64_t sqb, int64_t sqh, int64_t sqs,
                        const void* k, int64_t skb, int64_t skh, int64_t sks, const void* v,
                        int64_t svb, int64_t svh, int64_t svs, const void* out, int64_t sob,
-                       int64_t soh, int64_t sos, int64_t Sk, int64_t D, int64_t qps, int64_t bk,
-                       int64_t group) {
-  if (!dtype_ok(dtype) || Sk <= 0 || D <= 0 || qps <= 0 || bk <= 0 || group <= 0)
+                       int64_t soh, int64_t sos, int64_t Hq, int64_t Hk, int64_t Sk, int64_t D,
+                       int64_t qps, int64_t bk, int64_t group) {
+  if (!dtype_ok(dtype) || Hq <= 0 || Hk <= 0 || Hq % Hk != 0 || Sk <= 0 || D <= 0 || qps <= 0 ||
+      bk <= 0 || group <= 0)
     return fail(VA_ERR_ARG, "invalid prefill sizes");
   // The pooled queries live in the 256-byte aligned workspace with element
   // strides that are multiples of D: any aligned address and D strides stand
@@ -797,6 +808,8 @@ int va_prefill_kernels(int dtype, const void* q, int64_t sqb, int64_t sqh, int64
                 so[3] = {sob, soh, sos};
   const bool attn = attn_mfma_check(dtype, q, sq, k, sk, v, sv, out, so, Sk, D, qps).ok();
   flags |= attn ? VA_KERNELS_ATTN_MFMA : VA_KERNELS_ATTN_ROW;
+  if (attn && va::attn_mfma_ring_supported(dtype, D, qps) && va::ring_form_preferred(Hq, Hk, Sk, D))
+    flags |= VA_KERNELS_ATTN_RING;
   if (attn && (flags & (VA_KERNELS_SELECT_WAVE | VA_KERNELS_SELECT_MFMA))) {
     const int64_t g = effective_group(group, Sk, bk);
     const int64_t sg = va::select_wave_segment_keys(Sk, bk, g);

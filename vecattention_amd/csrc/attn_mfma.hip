@@ -63,7 +63,7 @@ __device__ inline void static_for(F&& f) {
 template <uint32_t V>
 using lds_off = std::integral_constant<uint32_t, V>;
 
-template <int D, int QPS>
+template <int D, int QPS, bool kRing3 = false>
 struct AttnShape {
   static constexpr int kRowHalves = QPS / 32;
   static constexpr int kWaves = 2 * kRowHalves;
@@ -75,7 +75,9 @@ struct AttnShape {
   static constexpr int kRowsPerCopy = 1024 / kRowBytes;      // rows per 1 KB copy
   static constexpr int kCopiesPerWave = kTileBytes / 1024 / kWaves;  // per operand
   static constexpr int kMergeBytes = kRowHalves * 64 * (D / 2 + 4) * 4;
-  static constexpr int kDataBytes = 2 * kStageBytes > kMergeBytes ? 2 * kStageBytes : kMergeBytes;
+  // Two stages of a K and a V tile, or (kRing3) a ring of three tile slots.
+  static constexpr int kRingBytes = kRing3 ? 3 * kTileBytes : 2 * kStageBytes;
+  static constexpr int kDataBytes = kRingBytes > kMergeBytes ? kRingBytes : kMergeBytes;
   // Key ids: a ring of 2 * kWaves tile slots; every kWaves tiles each wave
   // stages the ids of one tile kWaves to 2 * kWaves - 1 tiles ahead.
   static constexpr int kIdSlots = 2 * kWaves;
@@ -134,8 +136,8 @@ struct TileInfo {
 // at stats[((bh * Sq + i) * nc + J) * 2], the output after all of them (from
 // the next multiple of 4 floats, P = ceil(2 * B * Hq * nc * Sq / 4) * 4), at
 // stats + P + ((bh * Sq + i) * nc + J) * D.
-template <typename T, int D, int QPS, bool kDense, bool kStats, bool kSplit>
-__global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == kThreads
+template <typename T, int D, int QPS, bool kDense, bool kStats, bool kSplit, bool kRing3>
+__global__ __launch_bounds__(QPS * 4, kRing3 ? 3 : 2) void attn_mfma_kernel(  // QPS * 4 == kThreads
     const T* __restrict__ q, int64_t sqb, int64_t sqh, int64_t sqs,
     const T* __restrict__ k, int64_t skb, int64_t skh, int64_t sks,
     const T* __restrict__ v, int64_t svb, int64_t svh, int64_t svs,
@@ -143,7 +145,8 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
     int64_t Hq, int64_t Hk, int64_t Sq, int64_t Sk, int causal, float scale_log2,
     const int32_t* __restrict__ counts, const int32_t* __restrict__ indices,
     RowLayout lay, int nseg, int segk, int64_t dense_qoff, float* __restrict__ stats) {
-  using S = AttnShape<D, QPS>;
+  using S = AttnShape<D, QPS, kRing3>;
+  static_assert(!kRing3 || (!kDense && !kStats && !kSplit), "the ring form is the sparse kernel's");
   using M = Mfma<T>;
   using vec = typename M::vec;
   constexpr int NCH = S::kChunks;
@@ -502,6 +505,143 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
   // tiles ahead (K only under kStats, where the copies of tile t+1 are
   // K(t+1) and K(t+2)).
   constexpr int kKeep = kStats ? H : 2 * H;
+  if constexpr (kRing3) {
+    // Ring of three tile slots (three work-groups fit a CU's LDS): operand
+    // o_i (o_2t = K(t), o_2t+1 = V(t)) sits in slot i % 3.  Step i waits until
+    // o_i has landed (the H copies of o_i+1 stay in flight), passes a barrier
+    // (every wave is done with o_i-1), issues the copies of o_i+2 into the
+    // slot of o_i-1 and computes on o_i, so each copy has one tile to land.
+    // A wave runs QK(t), the softmax of S(t) and PV(t) in order, without the
+    // two score sets of the staged pipeline: the other waves of its SIMD fill
+    // its waits.  Iteration t % 3 fixes the slots, so the loop runs three
+    // tiles per trip with compile-time LDS offsets.  Ids: as the staged
+    // pipeline (every W tiles each wave stages one of tiles t+W .. t+2W-1);
+    // the ids of tile u are first read at step K(u-1), at least W-1 tiles
+    // after they were staged.
+    // Registers (three waves per SIMD allow 168): the operand offsets are
+    // rebuilt from one base per operand each step instead of being kept.  At
+    // D = 128 the swizzle only flips offset bits that the feature step owns:
+    // koff[s] = koff[0] ^ 32s, voff[i][r] = voff[0][r] ^ 64i, and the chunk
+    // offset of copy x is cchunk[0] ^ 16x (rows (4 wave + x) * 4 + qr have
+    // swizzle 4qr + x).  Each base passes through an empty asm per step so
+    // that the compiler does not hoist the eight offsets out of the loop.
+    static_assert(D == 128 && S::kRowsPerCopy == 4 && H == 4, "offset identities assume D = 128");
+    constexpr uint32_t TB = uint32_t(S::kTileBytes);
+    const uint32_t k0 = koff[0], v00 = voff[0][0], v01 = voff[0][1], c0 = cchunk[0];
+    auto copy_pairs3 = [&](int u, int idslot, uint32_t cbase, uint64_t (&pr)[H]) {
+      uint32_t key[H];
+#pragma unroll
+      for (int x = 0; x < H; ++x) key[x] = uint32_t(ids[idslot * kTileKeys + id_pos + x]);
+      if (u == p_col) {
+        const int lim = n_col - (u - t_init - t_diag) * kTileKeys;
+#pragma unroll
+        for (int x = 0; x < H; ++x)
+          if (qr >= lim - (wave * H + x) * RPC) key[x] = 0xffffffffu;
+      }
+#pragma unroll
+      for (int x = 0; x < H; ++x) pr[x] = uint64_t(key[x]) | (uint64_t(cbase ^ (16u * x)) << 32);
+    };
+    auto read_v3 = [&](const unsigned char* vbuf, uint32_t va, uint32_t vb1, int f) {
+      const int sub = f / (D / 32), i = f % (D / 32);
+      const unsigned char* p0 = vbuf + (va ^ uint32_t(64 * i)) + sub * 16 * S::kRowBytes;
+      const unsigned char* p1 = vbuf + (vb1 ^ uint32_t(64 * i)) + sub * 16 * S::kRowBytes;
+      const s16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (__attribute__((address_space(3))) s16x4_t*)(p0));
+      const s16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (__attribute__((address_space(3))) s16x4_t*)(p1));
+      const s16x4_t both[2] = {lo, hi};
+      return __builtin_bit_cast(vec, both);
+    };
+    if (ntiles > 0) {
+      stage_ids(wave, wave);  // tiles 0 .. W-1
+      // Tile 0's ids are LDS writes when it is a local block; column-id
+      // copies of later tiles are covered by the waits of the first steps.
+      if (t_init + t_diag >= 1)
+        lds_barrier();
+      else
+        vm_lds_barrier();
+      uint64_t pr[H];
+      copy_pairs(0, 0, pr);
+      static_for<H>([&](auto x) { copy_k(lds_off<0>{}, x, pr[x]); });
+      static_for<H>([&](auto x) { copy_v(lds_off<TB>{}, x, pr[x]); });
+    }
+    auto step = [&](int t, auto r_tag) {
+      constexpr int r = decltype(r_tag)::value;
+      constexpr uint32_t k_this = uint32_t((2 * r) % 3) * TB;
+      constexpr uint32_t v_this = uint32_t((2 * r + 1) % 3) * TB;
+      constexpr uint32_t k_next = uint32_t((2 * r + 2) % 3) * TB;
+      constexpr uint32_t v_next = k_this;
+      // ---- K(t): S(t) = QK(t), its softmax; copies of K(t+1)
+      vm_lds_barrier_keep<H>();  // K(t) landed; every wave is done with V(t-1)
+      if (t % W == 0) {
+        const int u = t + W + wave;
+        stage_ids(u, u % S::kIdSlots);
+      }
+      uint32_t kx = k0, cx = c0;
+      asm volatile("" : "+v"(kx), "+v"(cx));
+      uint64_t cpr[H];
+      copy_pairs3(t + 1, (t + 1) % S::kIdSlots, cx, cpr);
+      const unsigned char* kb = smem + k_this;
+      constexpr int kAhead = 2, kVAhead = 2;
+      vec a[NQK];
+#pragma unroll
+      for (int st = 0; st < kAhead; ++st)
+        a[st] = __builtin_bit_cast(vec,
+                                   *reinterpret_cast<const uint4*>(kb + (kx ^ uint32_t(32 * st))));
+      f32x16_t sc;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) sc[e] = 0.f;
+#pragma unroll
+      for (int st = 0; st < NQK; ++st) {
+        __builtin_amdgcn_sched_barrier(0);
+        if (st + kAhead < NQK)
+          a[st + kAhead] = __builtin_bit_cast(
+              vec, *reinterpret_cast<const uint4*>(kb + (kx ^ uint32_t(32 * (st + kAhead)))));
+        sc = M::run(a[st], qreg[st], sc);
+        static_for<H>([&](auto c) {  // copy c goes out after MFMA c * NQK / H
+          if (c * NQK / H == st) copy_k(lds_off<k_next>{}, c, cpr[c]);
+        });
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      mask(t, sc);
+      float tmax = -__builtin_inff();
+#pragma unroll
+      for (int e = 0; e < 16; e += 2) tmax = max3_plain(tmax, sc[e], sc[e + 1]);
+      rescale(max_halves(tmax));
+      float pr[16];
+#pragma unroll
+      for (int e = 0; e < 16; ++e)
+        pr[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[e], scale_log2, mneg));
+      const vec bfrag[2] = {M::pack(pr), M::pack(pr + 8)};
+      // ---- V(t): PV(t) with the row sums of P(t); copies of V(t+1)
+      vm_lds_barrier_keep<H>();  // V(t) landed; every wave is done with K(t)
+      uint32_t va = v00, vb1 = v01, cy = c0;
+      asm volatile("" : "+v"(va), "+v"(vb1), "+v"(cy));
+      copy_pairs3(t + 1, (t + 1) % S::kIdSlots, cy, cpr);
+      const unsigned char* vb = smem + v_this;
+      vec vf[NPV];
+#pragma unroll
+      for (int f = 0; f < kVAhead; ++f) vf[f] = read_v3(vb, va, vb1, f);
+#pragma unroll
+      for (int f = 0; f < NPV; ++f) {
+        __builtin_amdgcn_sched_barrier(0);
+        if (f + kVAhead < NPV) vf[f + kVAhead] = read_v3(vb, va, vb1, f + kVAhead);
+        pv_mfma(f, vf[f], bfrag);
+        static_for<H>([&](auto c) {  // copy c goes out after MFMA c * NPV / H
+          if (c * NPV / H == f) copy_v(lds_off<v_next>{}, c, cpr[c]);
+        });
+#pragma unroll
+        for (int j = f * 8 / NPV; j < (f + 1) * 8 / NPV; ++j)
+          lsum = M::add_pair(bfrag[j / 4], j % 4, lsum);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    for (int t = 0; t < ntiles; t += 3) {
+      step(t, std::integral_constant<int, 0>{});
+      if (t + 1 < ntiles) step(t + 1, std::integral_constant<int, 1>{});
+      if (t + 2 < ntiles) step(t + 2, std::integral_constant<int, 2>{});
+    }
+  } else {
   if (ntiles > 0) {
     stage_ids(wave, wave);  // tiles 0 .. W-1
     // When tiles 0 and 1 are local blocks (their ids are LDS writes), their
@@ -629,6 +769,7 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
     iteration(t, std::integral_constant<int, 0>{}, s_cur, s_alt);
     if (t + 1 < ntiles) iteration(t + 1, std::integral_constant<int, 1>{}, s_alt, s_cur);
   }
+  }  // staged pipeline
 
   // ---- merge the two key halves, normalise, store --------------------------
   vm_lds_barrier();  // every wave is done with the stages, the last copies have landed
@@ -724,6 +865,16 @@ __global__ __launch_bounds__(QPS * 4, 2) void attn_mfma_kernel(  // QPS * 4 == k
     finish(std::integral_constant<int, 1>{});
 }
 
+// Form of the sparse loop at D = 128 with 64-row blocks when the caller
+// leaves it open: the staged pipeline where the kv heads are not shared and
+// one head's K and V exceed 32 MiB (their gathers mostly miss L2, and the
+// fabric's latency wants the staged form's longer copy lead: 119056 keys,
+// 24 heads, +2.5% on the ring), the ring form otherwise (32K and 128K causal
+// GQA, 32760 non-causal: -1.5 to -2.7% of a prefill, same-box A/B).
+bool ring_form_preferred(int64_t Hq, int64_t Hk, int64_t Sk, int64_t D) {
+  return !(Hq == Hk && Sk * D * 2 * 2 > (int64_t(32) << 20));
+}
+
 template <typename T, int D, int QPS, bool kDense, bool kStats, bool kSplit = false>
 static hipError_t launch_attn_mfma_k(const void* q, const int64_t* sq, const void* k,
                                      const int64_t* sk, const void* v, const int64_t* sv,
@@ -731,18 +882,29 @@ static hipError_t launch_attn_mfma_k(const void* q, const int64_t* sq, const voi
                                      int64_t Hk, int64_t Sq, int64_t Sk, int causal,
                                      float scale_log2, const int32_t* counts,
                                      const int32_t* indices, const RowLayout& lay, int nseg,
-                                     int segk, int64_t dense_qoff, float* stats,
+                                     int segk, int64_t dense_qoff, float* stats, int form,
                                      hipStream_t stream) {
   static const int64_t zero[3] = {0, 0, 0};
   if (kStats) sv = so = zero;  // no V, no output
   const int64_t nblocks = WorkOrder{lay.nc, B, Hq, Hk, causal == 0}.grid_items();
-  hipLaunchKernelGGL((attn_mfma_kernel<T, D, QPS, kDense, kStats, kSplit>), dim3(unsigned(nblocks)),
-                     dim3(AttnShape<D, QPS>::kThreads), 0, stream, static_cast<const T*>(q),
-                     sq[0], sq[1], sq[2], static_cast<const T*>(k), sk[0], sk[1], sk[2],
-                     static_cast<const T*>(v), sv[0], sv[1], sv[2], static_cast<T*>(out), so[0],
-                     so[1], so[2], B, Hq, Hk, Sq, Sk, causal, scale_log2, counts, indices, lay,
-                     nseg, segk, (kDense || kSplit) ? dense_qoff : 0, stats);
-  return hipGetLastError();
+  constexpr bool kRingOk = !kDense && !kStats && !kSplit && QPS == 64 && D == 128;
+  bool ring = false;
+  if constexpr (kRingOk)
+    ring = form == kAttnFormRing || (form == kAttnFormAuto && ring_form_preferred(Hq, Hk, Sk, D));
+  else if (form == kAttnFormRing)
+    return hipErrorInvalidValue;
+  auto go = [&](auto kernel) {
+    hipLaunchKernelGGL(kernel, dim3(unsigned(nblocks)), dim3(AttnShape<D, QPS>::kThreads), 0,
+                       stream, static_cast<const T*>(q), sq[0], sq[1], sq[2],
+                       static_cast<const T*>(k), sk[0], sk[1], sk[2], static_cast<const T*>(v),
+                       sv[0], sv[1], sv[2], static_cast<T*>(out), so[0], so[1], so[2], B, Hq, Hk,
+                       Sq, Sk, causal, scale_log2, counts, indices, lay, nseg, segk,
+                       (kDense || kSplit) ? dense_qoff : 0, stats);
+    return hipGetLastError();
+  };
+  if constexpr (kRingOk)
+    if (ring) return go(attn_mfma_kernel<T, D, QPS, kDense, kStats, kSplit, true>);
+  return go(attn_mfma_kernel<T, D, QPS, kDense, kStats, kSplit, false>);
 }
 
 // dense_qoff >= 0: dense key lists (64-row blocks only); stats != nullptr: the
@@ -754,13 +916,13 @@ static hipError_t launch_attn_mfma_tdq(const void* q, const int64_t* sq, const v
                                        int64_t Hk, int64_t Sq, int64_t Sk, int causal,
                                        float scale_log2, const int32_t* counts,
                                        const int32_t* indices, const RowLayout& lay, int nseg,
-                                       int segk, int64_t dense_qoff, float* stats,
+                                       int segk, int64_t dense_qoff, float* stats, int form,
                                        hipStream_t stream) {
 #define VA_ATTN_LAUNCH(DENSE, STATS)                                                           \
   return launch_attn_mfma_k<T, D, QPS, DENSE, STATS>(q, sq, k, sk, v, sv, out, so, B, Hq, Hk,  \
                                                      Sq, Sk, causal, scale_log2, counts,      \
                                                      indices, lay, nseg, segk, dense_qoff,    \
-                                                     stats, stream)
+                                                     stats, form, stream)
   if (dense_qoff >= 0) {
     if constexpr (QPS == 64) {
       if (stats) VA_ATTN_LAUNCH(true, true);
@@ -780,13 +942,13 @@ static hipError_t launch_attn_mfma_t(int64_t D, int64_t qps, const void* q, cons
                                      int64_t Hq, int64_t Hk, int64_t Sq, int64_t Sk, int causal,
                                      float scale_log2, const int32_t* counts,
                                      const int32_t* indices, const RowLayout& lay, int nseg,
-                                     int segk, int64_t dense_qoff, float* stats,
+                                     int segk, int64_t dense_qoff, float* stats, int form,
                                      hipStream_t stream) {
 #define VA_ATTN_CASE(DD, QQ)                                                                   \
   if (D == DD && qps == QQ)                                                                    \
     return launch_attn_mfma_tdq<T, DD, QQ>(q, sq, k, sk, v, sv, out, so, B, Hq, Hk, Sq, Sk,   \
                                            causal, scale_log2, counts, indices, lay, nseg,    \
-                                           segk, dense_qoff, stats, stream);
+                                           segk, dense_qoff, stats, form, stream);
   VA_ATTN_CASE(64, 64)
   VA_ATTN_CASE(128, 64)
   VA_ATTN_CASE(64, 128)
@@ -817,11 +979,11 @@ static hipError_t launch_attn_split_t(int64_t D, const void* q, const int64_t* s
   if (D == 64)
     return launch_attn_mfma_k<T, 64, 64, true, false, true>(
         q, sq, k, sk, v, sv, nullptr, zero, B, H, H, Sq, Sk, 0, scale_log2, nullptr, nullptr, lay,
-        1, 0, span, part, stream);
+        1, 0, span, part, kAttnFormAuto, stream);
   if (D == 128)
     return launch_attn_mfma_k<T, 128, 64, true, false, true>(
         q, sq, k, sk, v, sv, nullptr, zero, B, H, H, Sq, Sk, 0, scale_log2, nullptr, nullptr, lay,
-        1, 0, span, part, stream);
+        1, 0, span, part, kAttnFormAuto, stream);
   return hipErrorInvalidValue;
 }
 
@@ -842,21 +1004,25 @@ bool attn_mfma_supported(int dtype, int64_t D, int64_t qps) {
   return (dtype == kBF16 || dtype == kF16) && (D == 64 || D == 128) && (qps == 64 || qps == 128);
 }
 
+bool attn_mfma_ring_supported(int dtype, int64_t D, int64_t qps) {
+  return (dtype == kBF16 || dtype == kF16) && D == 128 && qps == 64;
+}
+
 hipError_t launch_attn_mfma(int dtype, int64_t D, int64_t qps, const void* q, const int64_t* sq,
                             const void* k, const int64_t* sk, const void* v, const int64_t* sv,
                             void* out, const int64_t* so, int64_t B, int64_t Hq, int64_t Hk,
                             int64_t Sq, int64_t Sk, int causal, float scale_log2,
                             const int32_t* counts, const int32_t* indices, const RowLayout& lay,
-                            int nseg, int segk, int64_t dense_qoff, float* stats,
+                            int nseg, int segk, int64_t dense_qoff, float* stats, int form,
                             hipStream_t stream) {
   if (dtype == kBF16)
     return launch_attn_mfma_t<bf16_t>(D, qps, q, sq, k, sk, v, sv, out, so, B, Hq, Hk, Sq, Sk,
                                       causal, scale_log2, counts, indices, lay, nseg, segk,
-                                      dense_qoff, stats, stream);
+                                      dense_qoff, stats, form, stream);
   if (dtype == kF16)
     return launch_attn_mfma_t<f16_t>(D, qps, q, sq, k, sk, v, sv, out, so, B, Hq, Hk, Sq, Sk,
                                      causal, scale_log2, counts, indices, lay, nseg, segk,
-                                     dense_qoff, stats, stream);
+                                     dense_qoff, stats, form, stream);
   return hipErrorInvalidValue;
 }
 

@@ -16,6 +16,11 @@ enum DType : int { kF32 = 0, kBF16 = 1, kF16 = 2 };
 // sequential walk would hold there.  Plain: one pass, no carried state.
 enum SelectPass : int { kPassPlain = 0, kPassMax = 1, kPassCarry = 2 };
 
+// Forms of the MFMA attention kernel's sparse loop (D = 128, 64-row blocks):
+// staged (two stages of a K and a V tile, two work-groups per CU) or ring
+// (three tile slots, three work-groups per CU); auto picks by shape.
+enum AttnForm : int { kAttnFormAuto = 0, kAttnFormStaged = 1, kAttnFormRing = 2 };
+
 // Raw 16-bit storage types; arithmetic goes through explicit conversions so
 // that every rounding step is visible.
 struct bf16_t { uint16_t bits; };

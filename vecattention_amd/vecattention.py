@@ -157,7 +157,7 @@ def VecAttention_prefill(
         dt, nat.ptr(q), q.stride(0), q.stride(1), q.stride(2), nat.ptr(k), k.stride(0),
         k.stride(1), k.stride(2), nat.ptr(v), v.stride(0), v.stride(1), v.stride(2),
         nat.ptr(attn_output), attn_output.stride(0), attn_output.stride(1), attn_output.stride(2),
-        Sk, D, q_pooling_size, k_local_size, group_k_block)
+        Hq, Hk, Sk, D, q_pooling_size, k_local_size, group_k_block)
     if flags < 0:
         nat.check("va_prefill_kernels", flags)
     _warn_slow_path(flags, q.dtype, D, q_pooling_size, k_local_size)
