@@ -137,6 +137,48 @@ def kernel_source_hash():
     return h.hexdigest()[:16]
 
 
+def profiled_record(workload, kernel):
+    """The record of `kernel` on `workload` in profiles/hbm_traffic.json, or None
+    when not profiled or profiled on other kernel sources than the ones built now."""
+    path = os.path.join(ROOT, "profiles", "hbm_traffic.json")
+    try:
+        with open(path) as f:
+            doc = json.load(f)
+        rec = doc["workloads"][workload][kernel]
+    except (OSError, KeyError, ValueError):
+        return None
+    return rec if doc.get("source_hash") == kernel_source_hash() else None
+
+
+def gather_ceiling(dev, work_groups=256 * 12, steps=512, reps=5):
+    """Rate (TB/s) of the attention kernel's K/V copy instruction on its own
+    (va_probe_gather: 256-byte rows at hashed ids into LDS, 8 copies in flight
+    per wave), from a 2 MiB table (L2 hits) and a 64 MiB one (L2 misses served
+    over the data fabric by the Infinity Cache)."""
+    from vecattention_amd import _native as nat
+    L = nat.lib()
+    sink = torch.empty(work_groups, dtype=torch.int32, device=dev)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    moved = work_groups * 4 * steps * 1024
+    rates = {}
+    for name, mib in (("l2", 2), ("fabric", 64)):
+        rows = (mib << 20) // 256
+        table = torch.ones(rows * 256, dtype=torch.uint8, device=dev)
+        call = lambda: nat.check("va_probe_gather", L.va_probe_gather(
+            nat.ptr(table), rows, work_groups, steps, 0, nat.ptr(sink), stream))
+        call()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(reps):
+            call()
+        b.record()
+        torch.cuda.synchronize()
+        rates[name] = moved / (a.elapsed_time(b) / reps * 1e-3) / 1e12
+        del table
+    return rates
+
+
 def profiled_traffic(workload, kernel):
     """Bytes per launch of `kernel` on `workload` crossing between L2 and the
     data fabric (reads + writes; fabric reads include those the Infinity
@@ -620,6 +662,19 @@ def measure_prefill(args, wl, dev, with_cpu):
     e2e_tflops = F_attn / (ms_per_step * 1e-3) / 1e12
     attn_tflops = F_attn / (t_attn * 1e-3) / 1e12
     traffic, compulsory = profiled_traffic(wl.name, "attn_mfma_kernel")
+    # The attention's K/V gathers against the copy instruction's own rate: K and
+    # V rows of every (q-block, key) pair, F_attn * elem / (2 * qps) bytes.
+    es = q.element_size()
+    gathered = F_attn * es / (2 * wl.q_pooling_size)
+    gather_rate = gathered / (t_attn * 1e-3) / 1e12
+    ceil = gather_ceiling(dev)
+    rec = profiled_record(wl.name, "attn_mfma_kernel")
+    l2_share = None if rec is None or "fabric_over_gathered" not in rec else \
+        max(0.0, 1.0 - rec["fabric_over_gathered"])
+    mix = None if l2_share is None else \
+        1.0 / (l2_share / ceil["l2"] + (1.0 - l2_share) / ceil["fabric"])
+    print(f"[bench] gathers {gather_rate:.2f} TB/s; copy-instruction ceiling {ceil['l2']:.2f} "
+          f"(L2) / {ceil['fabric']:.2f} (fabric) TB/s", file=sys.stderr, flush=True)
     result = {
         "metric": METRIC,
         "value": round(e2e_tflops, 3),
@@ -658,7 +713,16 @@ def measure_prefill(args, wl, dev, with_cpu):
                      "traffic_kind": "L2<->fabric bytes per launch (exact, from the TCC_EA0 "
                                      "request-size counters; Infinity Cache hits included)",
                      "traffic_over_compulsory": (round(traffic / compulsory, 2)
-                                                 if traffic and compulsory else None)},
+                                                 if traffic and compulsory else None),
+                     "gather": {
+                         "achieved_TBps": round(gather_rate, 3),
+                         "ceiling_l2_TBps": round(ceil["l2"], 3),
+                         "ceiling_fabric_TBps": round(ceil["fabric"], 3),
+                         "l2_share_profiled": None if l2_share is None else round(l2_share, 3),
+                         "ceiling_at_l2_share_TBps": None if mix is None else round(mix, 3),
+                         "frac_of_ceiling_at_l2_share": None if mix is None else
+                         round(gather_rate / mix, 3),
+                         "frac_of_l2_ceiling": round(gather_rate / ceil["l2"], 3)}},
         "flops": {"attn_executed": F_attn, "dense": F_dense},
     }
     if with_cpu:

@@ -322,6 +322,19 @@ int va_prefill(int dtype, const void* q, int64_t sqb, int64_t sqh, int64_t sqs,
                int64_t k_local_size, int64_t group_k_block, int causal, int64_t chunk_size,
                int64_t bsq, void* workspace, int64_t workspace_bytes, void* stream);
 
+/*
+ * Measurement probe, no counterpart in the reference: the L2 -> LDS row-gather
+ * rate the sparse attention kernel is bound by.  `work_groups` work-groups of
+ * 4 waves each copy `steps` (a multiple of 16) tiles of four 256-byte rows of
+ * `table` (`rows` rows, at most 2^23) into LDS with the attention kernel's
+ * copy instruction, 8 copies in flight per wave; rows are drawn by an integer
+ * hash (`sequential` 0) or consecutively (1).  Bytes moved:
+ * work_groups * 4 * steps * 1024.  `sink` (work_groups uint32) receives one
+ * value per work-group.  Time it with events on `stream`.
+ */
+int va_probe_gather(const void* table, int64_t rows, int64_t work_groups, int64_t steps,
+                    int sequential, uint32_t* sink, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

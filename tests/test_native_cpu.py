@@ -251,3 +251,13 @@ def test_prefill_kernels_reports_the_slow_paths(L):
     f = _plan(L, align=258)
     assert f & nat.VA_KERNELS_SELECT_EXACT and f & nat.VA_KERNELS_ATTN_ROW
     assert _plan(L, D=0) < 0
+
+
+def test_probe_rejects_bad_sizes(L):
+    # Checked before any launch: fake addresses are never dereferenced.
+    t, sink = 256, 512
+    assert L.va_probe_gather(t, 1024, 8, 15, 0, sink, None) == nat.VA_ERR_ARG   # steps % 16
+    assert L.va_probe_gather(t, 0, 8, 16, 0, sink, None) == nat.VA_ERR_ARG      # no rows
+    assert L.va_probe_gather(t, (1 << 23) + 1, 8, 16, 0, sink, None) == nat.VA_ERR_ARG
+    assert L.va_probe_gather(None, 1024, 8, 16, 0, sink, None) == nat.VA_ERR_ARG
+    assert L.va_probe_gather(t, 1024, 1 << 20, 1 << 12, 0, sink, None) == nat.VA_ERR_ARG  # ids

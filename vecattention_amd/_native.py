@@ -77,6 +77,7 @@ SIGNATURES = {
     "va_prefill": (_int, [_int, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _vp, _i64, _i64,
                           _i64, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _f32,
                           _vp, _i64, _i64, _i64, _int, _i64, _i64, _vp, _i64, _vp]),
+    "va_probe_gather": (_int, [_vp, _i64, _i64, _i64, _int, _vp, _vp]),
 }
 
 
