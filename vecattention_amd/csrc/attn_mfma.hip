@@ -63,7 +63,7 @@ __device__ inline void static_for(F&& f) {
 template <uint32_t V>
 using lds_off = std::integral_constant<uint32_t, V>;
 
-template <int D, int QPS, bool kRing3 = false>
+template <int D, int QPS, bool kRing3 = false, bool kStats = false>
 struct AttnShape {
   static constexpr int kRowHalves = QPS / 32;
   static constexpr int kWaves = 2 * kRowHalves;
@@ -71,10 +71,13 @@ struct AttnShape {
   static constexpr int kRowBytes = 2 * D;
   static constexpr int kChunks = D / 8;                      // 16-byte chunks per row
   static constexpr int kTileBytes = kTileKeys * kRowBytes;   // one K (or V) tile
-  static constexpr int kStageBytes = 2 * kTileBytes;         // K tile, then V tile
+  // K tile, then V tile (the statistics form reads no V: K tile only)
+  static constexpr int kStageBytes = (kStats ? 1 : 2) * kTileBytes;
   static constexpr int kRowsPerCopy = 1024 / kRowBytes;      // rows per 1 KB copy
   static constexpr int kCopiesPerWave = kTileBytes / 1024 / kWaves;  // per operand
-  static constexpr int kMergeBytes = kRowHalves * 64 * (D / 2 + 4) * 4;
+  // Epilogue: half of each row half's partial output and its (m, l) per
+  // wave, or (statistics form) the (m, l) of each row half only.
+  static constexpr int kMergeBytes = kStats ? kRowHalves * 128 * 4 : kRowHalves * 64 * (D / 2 + 4) * 4;
   // Two stages of a K and a V tile, or (kRing3) a ring of three tile slots.
   static constexpr int kRingBytes = kRing3 ? 3 * kTileBytes : 2 * kStageBytes;
   static constexpr int kDataBytes = kRingBytes > kMergeBytes ? kRingBytes : kMergeBytes;
@@ -137,7 +140,7 @@ struct TileInfo {
 // the next multiple of 4 floats, P = ceil(2 * B * Hq * nc * Sq / 4) * 4), at
 // stats + P + ((bh * Sq + i) * nc + J) * D.
 template <typename T, int D, int QPS, bool kDense, bool kStats, bool kSplit, bool kRing3>
-__global__ __launch_bounds__(QPS * 4, kRing3 ? 3 : 2) void attn_mfma_kernel(  // QPS * 4 == kThreads
+__global__ __launch_bounds__(QPS * 4, (kRing3 || D == 64) ? 3 : 2) void attn_mfma_kernel(  // QPS * 4 == kThreads
     const T* __restrict__ q, int64_t sqb, int64_t sqh, int64_t sqs,
     const T* __restrict__ k, int64_t skb, int64_t skh, int64_t sks,
     const T* __restrict__ v, int64_t svb, int64_t svh, int64_t svs,
@@ -145,7 +148,7 @@ __global__ __launch_bounds__(QPS * 4, kRing3 ? 3 : 2) void attn_mfma_kernel(  //
     int64_t Hq, int64_t Hk, int64_t Sq, int64_t Sk, int causal, float scale_log2,
     const int32_t* __restrict__ counts, const int32_t* __restrict__ indices,
     RowLayout lay, int nseg, int segk, int64_t dense_qoff, float* __restrict__ stats) {
-  using S = AttnShape<D, QPS, kRing3>;
+  using S = AttnShape<D, QPS, kRing3, kStats>;
   static_assert(!kRing3 || (!kDense && !kStats && !kSplit), "the ring form is the sparse kernel's");
   using M = Mfma<T>;
   using vec = typename M::vec;
@@ -773,7 +776,7 @@ __global__ __launch_bounds__(QPS * 4, kRing3 ? 3 : 2) void attn_mfma_kernel(  //
 
   // ---- merge the two key halves, normalise, store --------------------------
   vm_lds_barrier();  // every wave is done with the stages, the last copies have landed
-  float* mo = reinterpret_cast<float*>(smem) + rh * 64 * (D / 2 + 4);
+  float* mo = reinterpret_cast<float*>(smem) + rh * (kStats ? 128 : 64 * (D / 2 + 4));
   if constexpr (kStats) {
     const float lrow = sum_halves(lsum);
     if (kc == 1) {
