@@ -77,7 +77,8 @@ struct AttnShape {
   static constexpr int kCopiesPerWave = kTileBytes / 1024 / kWaves;  // per operand
   // Epilogue: half of each row half's partial output and its (m, l) per
   // wave, or (statistics form) the (m, l) of each row half only.
-  static constexpr int kMergeBytes = kStats ? kRowHalves * 128 * 4 : kRowHalves * 64 * (D / 2 + 4) * 4;
+  static constexpr int kMergeBytes =
+      kStats ? kRowHalves * 128 * 4 : kRowHalves * 64 * (D / 2 + 4) * 4;
   // Two stages of a K and a V tile, or (kRing3) a ring of three tile slots.
   static constexpr int kRingBytes = kRing3 ? 3 * kTileBytes : 2 * kStageBytes;
   static constexpr int kDataBytes = kRingBytes > kMergeBytes ? kRingBytes : kMergeBytes;
@@ -139,8 +140,10 @@ struct TileInfo {
 // at stats[((bh * Sq + i) * nc + J) * 2], the output after all of them (from
 // the next multiple of 4 floats, P = ceil(2 * B * Hq * nc * Sq / 4) * 4), at
 // stats + P + ((bh * Sq + i) * nc + J) * D.
+// QPS * 4 threads (kThreads); three waves per SIMD for the ring form and at
+// D = 64, two otherwise.
 template <typename T, int D, int QPS, bool kDense, bool kStats, bool kSplit, bool kRing3>
-__global__ __launch_bounds__(QPS * 4, (kRing3 || D == 64) ? 3 : 2) void attn_mfma_kernel(  // QPS * 4 == kThreads
+__global__ __launch_bounds__(QPS * 4, (kRing3 || D == 64) ? 3 : 2) void attn_mfma_kernel(
     const T* __restrict__ q, int64_t sqb, int64_t sqh, int64_t sqs,
     const T* __restrict__ k, int64_t skb, int64_t skh, int64_t sks,
     const T* __restrict__ v, int64_t svb, int64_t svh, int64_t svs,
@@ -645,134 +648,134 @@ __global__ __launch_bounds__(QPS * 4, (kRing3 || D == 64) ? 3 : 2) void attn_mfm
       if (t + 2 < ntiles) step(t + 2, std::integral_constant<int, 2>{});
     }
   } else {
-  if (ntiles > 0) {
-    stage_ids(wave, wave);  // tiles 0 .. W-1
-    // When tiles 0 and 1 are local blocks (their ids are LDS writes), their
-    // copies need no column ids: the barrier waits for LDS only and the
-    // column-id copies stay in flight next to K(0), K(1), V(0); the barrier
-    // after them (K(0) landed) also covers the older column-id copies, which
-    // copy_pairs(2) reads next.
-    if (t_init + t_diag >= 2)
-      lds_barrier();
-    else
-      vm_lds_barrier();
-    // K(0), K(1), V(0); after QK(0), K(2) into K(0)'s slot.  The loop's
-    // barriers leave the kKeep most recent copies of the wave in flight.
-    uint64_t pr[H], pr1[H];
-    copy_pairs(0, 0, pr);
-    copy_pairs(1, 1, pr1);
-    static_for<H>([&](auto x) { copy_k(lds_off<0>{}, x, pr[x]); });
-    static_for<H>([&](auto x) { copy_k(lds_off<S::kStageBytes>{}, x, pr1[x]); });
-    if constexpr (!kStats)
-      static_for<H>([&](auto x) { copy_v(lds_off<S::kTileBytes>{}, x, pr[x]); });
-    vm_lds_barrier_keep<kKeep>();  // K(0) landed
-    s_cur = qk(smem);
-    mask(0, s_cur);
-    float tmax = -__builtin_inff();
-#pragma unroll
-    for (int e = 0; e < 16; e += 2) tmax = max3_plain(tmax, s_cur[e], s_cur[e + 1]);
-    rescale(max_halves(tmax));
-    lds_barrier();  // every wave is done with K(0)
-    copy_pairs(2, 2, pr);
-    static_for<H>([&](auto x) { copy_k(lds_off<0>{}, x, pr[x]); });
-  }
-  // One iteration; the parity P = t & 1 is a compile-time constant so that
-  // the LDS slot addresses fold into the instructions' offsets and S(t),
-  // S(t+1) alternate between two register sets.
-  auto iteration = [&](int t, auto parity_tag, const f32x16_t& s_cur, f32x16_t& s_next) {
-    constexpr int P = decltype(parity_tag)::value;
-    constexpr uint32_t k_next = uint32_t((P ^ 1) * S::kStageBytes);    // K slot of t+1 and t+3
-    constexpr uint32_t v_this = uint32_t(P * S::kStageBytes + S::kTileBytes);  // V slot of t
-    constexpr uint32_t v_next = k_next + uint32_t(S::kTileBytes);      // V slot of t+1
-    // ---- first half: QK(t+1) next to the softmax of S(t); copies of V(t+1)
-    vm_lds_barrier_keep<kKeep>();  // K(t+1) landed; every wave is done with PV(t-1)
-    if (P == 0 && t % W == 0) {  // every wave stages one of tiles t+W .. t+2W-1
-      const int u = t + W + wave;
-      stage_ids(u, u % S::kIdSlots);
-    }
-    const unsigned char* kb = smem + k_next;
-#pragma unroll
-    for (int e = 0; e < 16; ++e) s_next[e] = 0.f;
-    float pr[16];
-    uint64_t cpr[H];
-    // K operands are read kAhead MFMAs ahead of their use (LDS latency), the
-    // V^T operands of PV(t) kVAhead MFMAs ahead.
-    constexpr int kAhead = 3, kVAhead = 3;
-    const unsigned char* vb = smem + v_this;
-    vec a[NQK], vf[NPV];
-#pragma unroll
-    for (int st = 0; st < kAhead; ++st)
-      a[st] = __builtin_bit_cast(vec, *reinterpret_cast<const uint4*>(kb + koff[st]));
-#pragma unroll
-    for (int st = 0; st < NQK; ++st) {
-      __builtin_amdgcn_sched_barrier(0);
-      if (st + kAhead < NQK)
-        a[st + kAhead] =
-            __builtin_bit_cast(vec, *reinterpret_cast<const uint4*>(kb + koff[st + kAhead]));
-      s_next = M::run(a[st], qreg[st], s_next);  // past the last tile: masked away below
-      if (st == 0) copy_pairs(t + 1, (t + 1) % S::kIdSlots, cpr);
-      static_for<H>([&](auto c) {  // copy c goes out after MFMA c * NQK / H
-        if (!kStats && c * NQK / H == st) copy_v(lds_off<v_next>{}, c, cpr[c]);
-      });
-      // this step's share of the softmax of S(t)
-#pragma unroll
-      for (int e = st * 16 / NQK; e < (st + 1) * 16 / NQK; ++e) {
-        pr[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(s_cur[e], scale_log2, mneg));
-        asm volatile("" : "+v"(pr[e]));  // keeps the exp in this step (not sunk past mask)
-      }
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    mask(t + 1, s_next);
-    if constexpr (kStats) {  // row sums of P(t), maximum of S(t+1), copies of K(t+3)
-      vm_lds_barrier_keep<kKeep>();  // every wave is done with K(t+1)
-      copy_pairs(t + 3, (t + 3) % S::kIdSlots, cpr);
-      static_for<H>([&](auto c) { copy_k(lds_off<k_next>{}, c, cpr[c]); });
-      float ps[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) ps[e] = pr[e] + pr[e + 8];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) ps[e] += ps[e + 4];
-      lsum += (ps[0] + ps[2]) + (ps[1] + ps[3]);
+    if (ntiles > 0) {
+      stage_ids(wave, wave);  // tiles 0 .. W-1
+      // When tiles 0 and 1 are local blocks (their ids are LDS writes), their
+      // copies need no column ids: the barrier waits for LDS only and the
+      // column-id copies stay in flight next to K(0), K(1), V(0); the barrier
+      // after them (K(0) landed) also covers the older column-id copies, which
+      // copy_pairs(2) reads next.
+      if (t_init + t_diag >= 2)
+        lds_barrier();
+      else
+        vm_lds_barrier();
+      // K(0), K(1), V(0); after QK(0), K(2) into K(0)'s slot.  The loop's
+      // barriers leave the kKeep most recent copies of the wave in flight.
+      uint64_t pr[H], pr1[H];
+      copy_pairs(0, 0, pr);
+      copy_pairs(1, 1, pr1);
+      static_for<H>([&](auto x) { copy_k(lds_off<0>{}, x, pr[x]); });
+      static_for<H>([&](auto x) { copy_k(lds_off<S::kStageBytes>{}, x, pr1[x]); });
+      if constexpr (!kStats)
+        static_for<H>([&](auto x) { copy_v(lds_off<S::kTileBytes>{}, x, pr[x]); });
+      vm_lds_barrier_keep<kKeep>();  // K(0) landed
+      s_cur = qk(smem);
+      mask(0, s_cur);
       float tmax = -__builtin_inff();
 #pragma unroll
-      for (int e = 0; e < 16; e += 2) tmax = max3_plain(tmax, s_next[e], s_next[e + 1]);
+      for (int e = 0; e < 16; e += 2) tmax = max3_plain(tmax, s_cur[e], s_cur[e + 1]);
       rescale(max_halves(tmax));
-      return;
+      lds_barrier();  // every wave is done with K(0)
+      copy_pairs(2, 2, pr);
+      static_for<H>([&](auto x) { copy_k(lds_off<0>{}, x, pr[x]); });
     }
-    const vec bfrag[2] = {M::pack(pr), M::pack(pr + 8)};
-    // ---- second half: PV(t), with the row sums of P(t) and the maximum of
-    // S(t+1) spread over its MFMAs (in-order issue: VALU work placed between
-    // the MFMAs runs while they execute); copies of K(t+3) into the slot QK
-    // just read
-    vm_lds_barrier_keep<kKeep>();  // V(t) landed; every wave is done with K(t+1)
+    // One iteration; the parity P = t & 1 is a compile-time constant so that
+    // the LDS slot addresses fold into the instructions' offsets and S(t),
+    // S(t+1) alternate between two register sets.
+    auto iteration = [&](int t, auto parity_tag, const f32x16_t& s_cur, f32x16_t& s_next) {
+      constexpr int P = decltype(parity_tag)::value;
+      constexpr uint32_t k_next = uint32_t((P ^ 1) * S::kStageBytes);    // K slot of t+1 and t+3
+      constexpr uint32_t v_this = uint32_t(P * S::kStageBytes + S::kTileBytes);  // V slot of t
+      constexpr uint32_t v_next = k_next + uint32_t(S::kTileBytes);      // V slot of t+1
+      // ---- first half: QK(t+1) next to the softmax of S(t); copies of V(t+1)
+      vm_lds_barrier_keep<kKeep>();  // K(t+1) landed; every wave is done with PV(t-1)
+      if (P == 0 && t % W == 0) {  // every wave stages one of tiles t+W .. t+2W-1
+        const int u = t + W + wave;
+        stage_ids(u, u % S::kIdSlots);
+      }
+      const unsigned char* kb = smem + k_next;
 #pragma unroll
-    for (int f = 0; f < kVAhead; ++f) vf[f] = read_v(vb, f);
-    copy_pairs(t + 3, (t + 3) % S::kIdSlots, cpr);
-    float tmax = -__builtin_inff();
+      for (int e = 0; e < 16; ++e) s_next[e] = 0.f;
+      float pr[16];
+      uint64_t cpr[H];
+      // K operands are read kAhead MFMAs ahead of their use (LDS latency), the
+      // V^T operands of PV(t) kVAhead MFMAs ahead.
+      constexpr int kAhead = 3, kVAhead = 3;
+      const unsigned char* vb = smem + v_this;
+      vec a[NQK], vf[NPV];
 #pragma unroll
-    for (int f = 0; f < NPV; ++f) {
+      for (int st = 0; st < kAhead; ++st)
+        a[st] = __builtin_bit_cast(vec, *reinterpret_cast<const uint4*>(kb + koff[st]));
+#pragma unroll
+      for (int st = 0; st < NQK; ++st) {
+        __builtin_amdgcn_sched_barrier(0);
+        if (st + kAhead < NQK)
+          a[st + kAhead] =
+              __builtin_bit_cast(vec, *reinterpret_cast<const uint4*>(kb + koff[st + kAhead]));
+        s_next = M::run(a[st], qreg[st], s_next);  // past the last tile: masked away below
+        if (st == 0) copy_pairs(t + 1, (t + 1) % S::kIdSlots, cpr);
+        static_for<H>([&](auto c) {  // copy c goes out after MFMA c * NQK / H
+          if (!kStats && c * NQK / H == st) copy_v(lds_off<v_next>{}, c, cpr[c]);
+        });
+        // this step's share of the softmax of S(t)
+#pragma unroll
+        for (int e = st * 16 / NQK; e < (st + 1) * 16 / NQK; ++e) {
+          pr[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(s_cur[e], scale_log2, mneg));
+          asm volatile("" : "+v"(pr[e]));  // keeps the exp in this step (not sunk past mask)
+        }
+      }
       __builtin_amdgcn_sched_barrier(0);
-      if (f + kVAhead < NPV) vf[f + kVAhead] = read_v(vb, f + kVAhead);
-      pv_mfma(f, vf[f], bfrag);
-      static_for<H>([&](auto c) {  // copy c goes out after MFMA c * NPV / H
-        if (c * NPV / H == f) copy_k(lds_off<k_next>{}, c, cpr[c]);
-      });
+      mask(t + 1, s_next);
+      if constexpr (kStats) {  // row sums of P(t), maximum of S(t+1), copies of K(t+3)
+        vm_lds_barrier_keep<kKeep>();  // every wave is done with K(t+1)
+        copy_pairs(t + 3, (t + 3) % S::kIdSlots, cpr);
+        static_for<H>([&](auto c) { copy_k(lds_off<k_next>{}, c, cpr[c]); });
+        float ps[8];
 #pragma unroll
-      for (int j = f * 8 / NPV; j < (f + 1) * 8 / NPV; ++j)
-        lsum = M::add_pair(bfrag[j / 4], j % 4, lsum);
+        for (int e = 0; e < 8; ++e) ps[e] = pr[e] + pr[e + 8];
 #pragma unroll
-      for (int e = f * 16 / NPV; e < (f + 1) * 16 / NPV; e += 2)
-        tmax = max3_plain(tmax, s_next[e], s_next[e + 1]);
+        for (int e = 0; e < 4; ++e) ps[e] += ps[e + 4];
+        lsum += (ps[0] + ps[2]) + (ps[1] + ps[3]);
+        float tmax = -__builtin_inff();
+#pragma unroll
+        for (int e = 0; e < 16; e += 2) tmax = max3_plain(tmax, s_next[e], s_next[e + 1]);
+        rescale(max_halves(tmax));
+        return;
+      }
+      const vec bfrag[2] = {M::pack(pr), M::pack(pr + 8)};
+      // ---- second half: PV(t), with the row sums of P(t) and the maximum of
+      // S(t+1) spread over its MFMAs (in-order issue: VALU work placed between
+      // the MFMAs runs while they execute); copies of K(t+3) into the slot QK
+      // just read
+      vm_lds_barrier_keep<kKeep>();  // V(t) landed; every wave is done with K(t+1)
+#pragma unroll
+      for (int f = 0; f < kVAhead; ++f) vf[f] = read_v(vb, f);
+      copy_pairs(t + 3, (t + 3) % S::kIdSlots, cpr);
+      float tmax = -__builtin_inff();
+#pragma unroll
+      for (int f = 0; f < NPV; ++f) {
+        __builtin_amdgcn_sched_barrier(0);
+        if (f + kVAhead < NPV) vf[f + kVAhead] = read_v(vb, f + kVAhead);
+        pv_mfma(f, vf[f], bfrag);
+        static_for<H>([&](auto c) {  // copy c goes out after MFMA c * NPV / H
+          if (c * NPV / H == f) copy_k(lds_off<k_next>{}, c, cpr[c]);
+        });
+#pragma unroll
+        for (int j = f * 8 / NPV; j < (f + 1) * 8 / NPV; ++j)
+          lsum = M::add_pair(bfrag[j / 4], j % 4, lsum);
+#pragma unroll
+        for (int e = f * 16 / NPV; e < (f + 1) * 16 / NPV; e += 2)
+          tmax = max3_plain(tmax, s_next[e], s_next[e + 1]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      rescale(max_halves(tmax));
+    };
+    f32x16_t s_alt;  // scores of the odd tiles (s_cur holds the even ones)
+    for (int t = 0; t < ntiles; t += 2) {
+      iteration(t, std::integral_constant<int, 0>{}, s_cur, s_alt);
+      if (t + 1 < ntiles) iteration(t + 1, std::integral_constant<int, 1>{}, s_alt, s_cur);
     }
-    __builtin_amdgcn_sched_barrier(0);
-    rescale(max_halves(tmax));
-  };
-  f32x16_t s_alt;  // scores of the odd tiles (s_cur holds the even ones)
-  for (int t = 0; t < ntiles; t += 2) {
-    iteration(t, std::integral_constant<int, 0>{}, s_cur, s_alt);
-    if (t + 1 < ntiles) iteration(t + 1, std::integral_constant<int, 1>{}, s_alt, s_cur);
   }
-  }  // staged pipeline
 
   // ---- merge the two key halves, normalise, store --------------------------
   vm_lds_barrier();  // every wave is done with the stages, the last copies have landed
