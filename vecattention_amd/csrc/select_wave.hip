@@ -274,7 +274,6 @@ __global__ __launch_bounds__(256, 2) void select_wave_kernel(
   }
   ambk[wave][64 + lane] = 0;  // resolved flags start cleared
 
-  // Append this lane's selected keys of block bb (bits over keys key0 + e).
   auto append = [&](int kb0, int bb, uint32_t bt) {
     const int cnt = __builtin_popcount(bt);
     const int ocnt = int(other_half(uint32_t(cnt)));
@@ -532,35 +531,39 @@ __global__ __launch_bounds__(256, 2) void select_wave_kernel(
       slots(NSL / 4, 3 * NSL / 8);
 
       // ---- decisions ------------------------------------------------------------
-      // d = s^ - (m^ - gap): selected outright when d > band, ambiguous when
-      // |d| <= band; tiles past the causal limit select nothing.
+      // With hi = (m^ - gap) + band and x = hi - s^: selected outright when
+      // x < 0 (the sign of a difference is exact, and hi is never -0), ambiguous
+      // when 0 <= x <= 2*band, rejected above.  The sign bits are shifted into
+      // the lane's mask (v_alignbit), and as unsigned integers the smallest
+      // non-negative x is the smallest bit pattern (negative x and NaN sort
+      // above 2*band), so one unsigned minimum tests ambiguity.  Tiles past the
+      // causal limit select nothing (hi = +inf).
       uint32_t bits[2];
-      float mid[2];
-      bool amb_lane = false;
+      float hi[2];
+      uint32_t xmin = 0xffffffffu;
 #pragma unroll
       for (int bb = 0; bb < 2; ++bb) {
         const int koff = BK == 16 ? kb0 + 32 * bb + 16 * hh : (BK == 32 ? kb0 + 32 * bb : kb0);
-        const bool ok = valid && koff < lim;
-        mid[bb] = ok ? mt[bb] - gap : __builtin_inff();
+        const bool ok = valid && koff < lim && mode != kPassMax;  // maxima pass: select nothing
+        hi[bb] = ok ? (mt[bb] - gap) + band : __builtin_inff();
         uint32_t bt = 0;
-        float dmin = __builtin_inff();
-        if (mode == kPassMax) mid[bb] = __builtin_inff();  // maxima only: select nothing
 #pragma unroll
         for (int half = 0; half < 2; ++half) {
           if (mode != kPassMax) {
 #pragma unroll
-            for (int e = 8 * half; e < 8 * half + 8; ++e) {
-              const float d = acc[bb][e] - mid[bb];
-              bt |= uint32_t(d > band) << e;
-              dmin = __builtin_fminf(dmin, __builtin_fabsf(d));
+            for (int e = 15 - 8 * half; e >= 8 - 8 * half; --e) {
+              const uint32_t x = __builtin_bit_cast(uint32_t, hi[bb] - acc[bb][e]);
+              bt = __builtin_amdgcn_alignbit(bt, x, 31u);  // (bt << 1) | sign(x)
+              xmin = x < xmin ? x : xmin;
             }
           }
           const int sl = 3 * NSL / 8 + (2 * bb + half) * NSL / 8;
           slots(sl, sl + NSL / 8);
         }
         bits[bb] = bt;
-        amb_lane = amb_lane || (dmin <= band);
       }
+      const uint32_t band2 = __builtin_bit_cast(uint32_t, 2.f * band);
+      const bool amb_lane = xmin <= band2;
       if (__builtin_amdgcn_ballot_w64(amb_lane || listcnt > kWList - 4) != 0) {
         // ---- rare path: exact resolution, one row at a time ----------------------
         // Row r's jobs: every key of its listed tiles, then its ambiguous keys;
@@ -570,7 +573,8 @@ __global__ __launch_bounds__(256, 2) void select_wave_kernel(
         for (int bb = 0; bb < 2; ++bb) {
           uint32_t x = 0;
 #pragma unroll
-          for (int e = 0; e < 16; ++e) x |= uint32_t(__builtin_fabsf(acc[bb][e] - mid[bb]) <= band) << e;
+          for (int e = 0; e < 16; ++e)
+            x |= uint32_t(__builtin_bit_cast(uint32_t, hi[bb] - acc[bb][e]) <= band2) << e;
           ambm[wave][l32][2 * bb + hh] = x;
         }
         // (no short-circuit: the lane exchange must run with the whole wave active)
