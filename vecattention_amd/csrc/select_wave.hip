@@ -467,6 +467,7 @@ __global__ __launch_bounds__(256, 2) void select_wave_kernel(
       }
       const float tm0 = max16(acc[0]), tm1 = max16(acc[1]);
       const float om0 = other_half(tm0), om1 = other_half(tm1);
+      const float m_prev = m;  // running maximum before this chunk's tiles
       float mt[2];  // running max at this lane's tile of each block
       int rec[2];   // this lane lists the tile as near-max
       int nrec;     // tiles the row lists in this chunk
@@ -580,6 +581,30 @@ __global__ __launch_bounds__(256, 2) void select_wave_kernel(
         // (no short-circuit: the lane exchange must run with the whole wave active)
         const bool row_amb = (uint32_t(amb_lane) | other_half(uint32_t(amb_lane))) != 0u;
         uint64_t need = __builtin_amdgcn_ballot_w64(hh == 0 && (row_amb || listcnt > kWList - 4));
+        // The rows found here first drop the listed tiles that cannot hold the
+        // exact running maximum: a tile whose MFMA maximum is below
+        // m_prev - win, m_prev the running maximum before this chunk's tiles,
+        // since the tile that set m_prev (listed, or folded into exr) is
+        // exactly above it (win >= 2*delta plus rounding).  Rows whose list is
+        // then short enough and that hold no ambiguous key need no exact work.
+        if ((need >> lane) & 1u) {
+          const float cut = m_prev - win;
+          int keep = 0;
+          for (int i = 0; i < listcnt; ++i) {
+            const float x = nmx[wave][l32][i];
+            if (x >= cut) {
+              nml[wave][l32][keep] = nml[wave][l32][i];
+              nmx[wave][l32][keep] = x;
+              ++keep;
+            }
+          }
+          listcnt = keep;
+        }
+        {
+          const uint32_t lc = other_half(uint32_t(listcnt));  // the high half mirrors the count
+          if (hh) listcnt = int(lc);
+        }
+        need = __builtin_amdgcn_ballot_w64(hh == 0 && (row_amb || listcnt > kWList - 4));
         uint32_t ovr[2] = {0u, 0u};
         resolve(need, kb0, ovr);
         bits[0] |= ovr[0];
