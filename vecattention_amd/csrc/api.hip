@@ -248,6 +248,15 @@ static bool select_wave_ok(int dtype, const void* qs, int64_t sqb, int64_t sqh, 
          Sk < (int64_t(1) << 24) && (Sk + 64) * sks * esize(dtype) < (int64_t(1) << 31);
 }
 
+// The wave kernel starts a row's scan at the 64-key chunk holding its first
+// selectable key (smin) and keeps the running maximum of the keys below smin at
+// -inf; its sign-bit decisions assume that no visited chunk starts with such
+// keys, i.e. smin is a multiple of 64 (always so for q_pooling_size 64 or 128).
+static bool first_key_aligned(int64_t qps, int64_t Sk, int causal, int wo_init) {
+  const int64_t smin = !wo_init ? 0 : (causal ? qps : (qps < Sk ? qps : Sk));
+  return smin % 64 == 0;
+}
+
 int va_select(int dtype, const void* qs, int64_t sqb, int64_t sqh, int64_t sqn,
               const void* k, int64_t skb, int64_t skh, int64_t sks, int64_t B, int64_t Hq,
               int64_t Hk, int64_t Sk, int64_t D, int64_t qps, int64_t bk, int64_t group,
@@ -265,7 +274,8 @@ int va_select(int dtype, const void* qs, int64_t sqb, int64_t sqh, int64_t sqn,
                             scratch_floats >= va::key_norm_scratch_floats(B, Hk);
   const bool mfma_ok = select_mfma_ok(dtype, qs, sqb, sqh, sqn, k, skb, skh, sks, D, bk);
   const bool wave_ok =
-      select_wave_ok(dtype, qs, sqb, sqh, sqn, k, skb, skh, sks, Sk, D, bk, group);
+      select_wave_ok(dtype, qs, sqb, sqh, sqn, k, skb, skh, sks, Sk, D, bk, group) &&
+      first_key_aligned(qps, Sk, causal, wo_init);
   SelKernel which;
   if (kernel == VA_SEL_EXACT) {
     which = kSelExact;
@@ -278,7 +288,8 @@ int va_select(int dtype, const void* qs, int64_t sqb, int64_t sqh, int64_t sqn,
       return fail(VA_ERR_UNSUPPORTED,
                   "wave selection needs bf16/fp16, D in {64,128}, k_local_size in {16,32,64}, "
                   "k_local_size * group_k_block a multiple of 64, 16-byte aligned rows, "
-                  "Sk < 2^24 and < 2 GiB of key rows per kv head");
+                  "Sk < 2^24, < 2 GiB of key rows per kv head and a first selectable key "
+                  "at a multiple of 64");
     if (!have_scratch) return fail(VA_ERR_ARG, "MFMA selection needs scratch");
     which = kernel == VA_SEL_WAVE ? kSelWave : kSelMfma;
   } else if (kernel == VA_SEL_AUTO) {
@@ -349,7 +360,9 @@ int va_select_segments(int dtype, const void* qs, int64_t sqb, int64_t sqh, int6
   // The wave kernel takes every split; the 64-row MFMA kernel (tiles of 128
   // and 256 keys) takes segments of whole 256-key chunks that start groups.
   const SelKernel which =
-      select_wave_ok(dtype, qs, sqb, sqh, sqn, k, skb, skh, sks, Sk, D, bk, group) ? kSelWave
+      (select_wave_ok(dtype, qs, sqb, sqh, sqn, k, skb, skh, sks, Sk, D, bk, group) &&
+       first_key_aligned(qps, Sk, causal, wo_init))
+          ? kSelWave
       : (!two_pass && segment_keys % 256 == 0 &&
          select_mfma_ok(dtype, qs, sqb, sqh, sqn, k, skb, skh, sks, D, bk))
           ? kSelMfma

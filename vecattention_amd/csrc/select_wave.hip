@@ -533,12 +533,16 @@ __global__ __launch_bounds__(256, 2) void select_wave_kernel(
 
       // ---- decisions ------------------------------------------------------------
       // With hi = (m^ - gap) + band and x = hi - s^: selected outright when
-      // x < 0 (the sign of a difference is exact, and hi is never -0), ambiguous
-      // when 0 <= x <= 2*band, rejected above.  The sign bits are shifted into
-      // the lane's mask (v_alignbit), and as unsigned integers the smallest
-      // non-negative x is the smallest bit pattern (negative x and NaN sort
-      // above 2*band), so one unsigned minimum tests ambiguity.  Tiles past the
-      // causal limit select nothing (hi = +inf).
+      // x < 0 (the sign of a difference is exact, and hi is never -0: a sum of
+      // opposite equal values rounds to +0), ambiguous when 0 <= x <= 2*band,
+      // rejected above.  The sign bits are shifted into the lane's mask
+      // (v_alignbit), and as unsigned integers the smallest non-negative x is
+      // the smallest bit pattern (negative x sort above 2*band), so one
+      // unsigned minimum tests ambiguity.  Tiles past the causal limit select
+      // nothing (hi = +inf).  x is never NaN: s^ is -inf only for keys past Sk,
+      // which follow a finite running maximum, since the host runs this
+      // kernel only when the first selectable key starts a 64-key chunk (keys
+      // below it are never visited).
       uint32_t bits[2];
       float hi[2];
       uint32_t xmin = 0xffffffffu;
