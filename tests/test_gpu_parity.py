@@ -158,6 +158,28 @@ def test_select_bit_exact(device, case, kernel):
     _select_case(device, case, kernel)
 
 
+# A q_pooling_size that is not a multiple of 64 (the tuner API takes any):
+# with the initial block excluded the first selectable key does not start a
+# 64-key chunk, so the wave kernel refuses it and AUTO takes another kernel.
+UNALIGNED_CASE = ("bf16-causal-qps96-bk16-G4", 1, 4, 2, 1536, 128, torch.bfloat16, True, 96,
+                  16, 4, 0.10, None)
+
+
+@pytest.mark.parametrize("kernel", [nat.VA_SEL_AUTO, nat.VA_SEL_MFMA], ids=["auto", "mfma"])
+def test_select_unaligned_first_key(device, kernel):
+    _select_case(device, UNALIGNED_CASE, kernel)
+
+
+def test_select_unaligned_first_key_refuses_wave_kernel(device):
+    name, B, Hq, Hk, S, D, dtype, causal, qps, bk, G, _, _ = UNALIGNED_CASE
+    note("select refuses wave", name)
+    q, k, _ = make_inputs(B, Hq, Hk, S, D, dtype, seed=1)
+    qs, _ = stages.pool_scaled(q.to(device), qps)
+    with pytest.raises(NotImplementedError):
+        stages.select_rows(qs, k.to(device), 0, 0.2, None, causal, qps, bk, G, causal,
+                           kernel=nat.VA_SEL_WAVE)
+
+
 # Tiles of 128 and 256 keys (the reference signature's default k_local_size is
 # 128): the 64-row MFMA kernel takes them (a tile is 8 or 16 of its 16-key
 # segments, one or two per 256-key chunk); the wave kernel does not.
