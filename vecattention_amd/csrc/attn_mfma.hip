@@ -585,7 +585,7 @@ __global__ __launch_bounds__(QPS * 4, (kRing3 || D == 64) ? 3 : 2) void attn_mfm
       }
       uint32_t kx = k0, cx = c0;
       asm volatile("" : "+v"(kx), "+v"(cx));
-      uint64_t cpr[H];
+      uint64_t cpr[H];  // tile t+1's copy pairs: K(t+1) here, V(t+1) at the V step
       copy_pairs3(t + 1, (t + 1) % S::kIdSlots, cx, cpr);
       const unsigned char* kb = smem + k_this;
       constexpr int kAhead = 2, kVAhead = 2;
@@ -627,9 +627,8 @@ __global__ __launch_bounds__(QPS * 4, (kRing3 || D == 64) ? 3 : 2) void attn_mfm
       const vec bfrag[2] = {M::pack(pr), M::pack(pr + 8)};
       // ---- V(t): PV(t) with the row sums of P(t); copies of V(t+1)
       vm_lds_barrier_keep<H>();  // V(t) landed; every wave is done with K(t)
-      uint32_t va = v00, vb1 = v01, cy = c0;
-      asm volatile("" : "+v"(va), "+v"(vb1), "+v"(cy));
-      copy_pairs3(t + 1, (t + 1) % S::kIdSlots, cy, cpr);
+      uint32_t va = v00, vb1 = v01;
+      asm volatile("" : "+v"(va), "+v"(vb1));
       const unsigned char* vb = smem + v_this;
       vec vf[NPV];
 #pragma unroll
