@@ -451,8 +451,11 @@ __global__ __launch_bounds__(QPS * 4, (kRing3 || D == 64) ? 3 : 2) void attn_mfm
   // than the slack (rare): rescale O and the row sums.  The test compares raw
   // scores with thr = (mc + slack) / scale; its rounding only moves the
   // bound on the kept probabilities by a few ulps of 2^8.
+  // tmax is this lane's maximum over its 16 keys: a row moves when either of
+  // its two lanes exceeds thr, and only then is the row's maximum formed.
   auto rescale = [&](float tmax) {
     if (__builtin_amdgcn_ballot_w64(tmax > thr)) {
+      tmax = max_halves(tmax);
       const float mnew = __builtin_fmaxf(mc, tmax * scale_log2);
       const float alpha = (mnew == mc) ? 1.f : __builtin_amdgcn_exp2f(mc - mnew);
 #pragma unroll
@@ -619,7 +622,7 @@ __global__ __launch_bounds__(QPS * 4, (kRing3 || D == 64) ? 3 : 2) void attn_mfm
       float tmax = -__builtin_inff();
 #pragma unroll
       for (int e = 0; e < 16; e += 2) tmax = max3_plain(tmax, sc[e], sc[e + 1]);
-      rescale(max_halves(tmax));
+      rescale(tmax);
       float pr[16];
 #pragma unroll
       for (int e = 0; e < 16; ++e)
@@ -681,7 +684,7 @@ __global__ __launch_bounds__(QPS * 4, (kRing3 || D == 64) ? 3 : 2) void attn_mfm
       float tmax = -__builtin_inff();
 #pragma unroll
       for (int e = 0; e < 16; e += 2) tmax = max3_plain(tmax, s_cur[e], s_cur[e + 1]);
-      rescale(max_halves(tmax));
+      rescale(tmax);
       lds_barrier();  // every wave is done with K(0)
       copy_pairs(2, 2, pr);
       static_for<H>([&](auto x) { copy_k(lds_off<0>{}, x, pr[x]); });
@@ -746,7 +749,7 @@ __global__ __launch_bounds__(QPS * 4, (kRing3 || D == 64) ? 3 : 2) void attn_mfm
         float tmax = -__builtin_inff();
 #pragma unroll
         for (int e = 0; e < 16; e += 2) tmax = max3_plain(tmax, s_next[e], s_next[e + 1]);
-        rescale(max_halves(tmax));
+        rescale(tmax);
         return;
       }
       const vec bfrag[2] = {M::pack(pr), M::pack(pr + 8)};
@@ -775,7 +778,7 @@ __global__ __launch_bounds__(QPS * 4, (kRing3 || D == 64) ? 3 : 2) void attn_mfm
           tmax = max3_plain(tmax, s_next[e], s_next[e + 1]);
       }
       __builtin_amdgcn_sched_barrier(0);
-      rescale(max_halves(tmax));
+      rescale(tmax);
     };
     f32x16_t s_alt;  // scores of the odd tiles (s_cur holds the even ones)
     for (int t = 0; t < ntiles; t += 2) {
