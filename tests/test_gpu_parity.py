@@ -6,6 +6,7 @@ inputs), 1e-4 / 1e-5 for fp32 inputs.  Every call goes through the C ABI of
 libvecattn.so.
 """
 import math
+import os
 
 import numpy as np
 import pytest
@@ -703,6 +704,34 @@ def test_full_size_rows_match_oracle(config_b, th):
                                  nc=1)
             err = np.abs(out_cpu[0, h, J * qps:(J + 1) * qps] - want[0, 0])
             assert err.max() <= ATOL_MAX and err.mean() <= ATOL_MEAN, (h, J, err.max())
+
+
+def test_full_size_every_row_matches_oracle(config_b):
+    # Every row of every head of the 32K config at the benchmark's calibrated
+    # threshold: the split selection's lists (16 segments of 2048 keys, as the
+    # prefill runs them) equal the CPU oracle's bit for bit.  The oracle runs
+    # per head in threads (its C loop releases the interpreter lock).
+    from concurrent.futures import ThreadPoolExecutor
+    q, k, _, qd, kd, _ = config_b
+    qps, nqb, th = 64, 512, 0.7550760976531293
+    note("full-size every row, threshold", th)
+    qs_gpu, _ = stages.pool_scaled(qd, qps)
+    gpu = select_chunk(qs_gpu, kd, 0, nqb, -math.log(th + 1e-9), True, qps, 16, 16)
+    gaps = orc.gap_from_threshold(th, 1, 1)
+
+    def head(h):
+        _, qs = orc.pool(q[:, h:h + 1], qps, "bfloat16")
+        cnt, lists = orc.select(qs, k[:, h // 7:h // 7 + 1], 0, nqb, gaps, qps, 16, 16, True,
+                                True, 64)
+        bad = [J for J in range(nqb) if not np.array_equal(gpu.row(0, h, J), lists[0][0][J])]
+        return h, int(cnt.sum()), bad
+
+    with ThreadPoolExecutor(max_workers=min(16, os.cpu_count() or 1)) as ex:
+        results = list(ex.map(head, range(28)))
+    total = sum(n for _, n, _ in results)
+    assert total > 0
+    for h, _, bad in results:
+        assert not bad, (h, bad[:8])
 
 
 def test_full_size_chunking_invariant(config_b):
