@@ -12,11 +12,14 @@ of C, two heads of D and of E).  Run on an MI355X.
   rows is within the north-star tolerance of the oracle;
 - the two-pass split selection equals the exact fp64 kernel on every row of a
   chunk;
+- every row of one chunk (all heads of the subset) equals the oracle's list;
 - chunk-size invariance where the reference's rule makes it hold;
 - with all 28 heads of C, the prefill's causal row groups (the index buffer
   holds one group of a chunk at a time) give the same output as whole chunks.
 """
 import math
+import os
+from concurrent.futures import ThreadPoolExecutor
 
 import numpy as np
 import pytest
@@ -79,6 +82,29 @@ def check_rows(q, k, v, qs_dev, kd, out_cpu, heads, rows, th, causal, G, chunk_r
                     assert err.max() <= ATOL_MAX and err.mean() <= ATOL_MEAN, (h, J, err.max())
 
 
+def check_every_row(q, k, qs_dev, kd, J0, nc, th, causal, G, heads, rep=1, qps=64, bk=16):
+    """Every row J0..J0+nc-1 of every head in `heads`: the split selection's
+    list equals the oracle's bit for bit (heads in parallel threads; the
+    oracle's C selection releases the interpreter lock)."""
+    gap = -math.log(th + 1e-9)
+    gaps = orc.gap_from_threshold(th, 1, 1)
+    gpu = select_chunk(qs_dev, kd, J0, nc, gap, causal, qps, bk, G)
+
+    def head(h):
+        qs = pooled_oracle(q[:, h:h + 1], qps)
+        cnt, lists = orc.select(qs, k[:, h // rep:h // rep + 1], J0, nc, gaps, qps, bk, G,
+                                causal, causal, 64)
+        bad = [J for J in range(nc) if not np.array_equal(gpu.row(0, h, J), lists[0][0][J])]
+        return h, int(cnt.sum()), bad
+
+    with ThreadPoolExecutor(max_workers=min(16, os.cpu_count() or 1)) as ex:
+        results = list(ex.map(head, heads))
+    for h, total, bad in results:
+        assert total > 0, h
+        assert not bad, f"h={h}: rows {[J0 + J for J in bad[:10]]} differ"
+    return sum(t for _, t, _ in results)
+
+
 # ------------------------------------------------------------------ config C --
 
 @pytest.fixture(scope="module")
@@ -119,6 +145,13 @@ def test_c_sampled_rows_match_oracle(config_c, th):
     # program (the causal first-row rule), 2047 is the longest row
     rows = [1, 64] + sorted(rng.choice(np.arange(1536, 2048), 3, replace=False).tolist()) + [2047]
     check_rows(q, k, v, qs, kd, out_cpu, (0, 6), rows, th, True, 16, rep=7)
+
+
+def test_c_last_chunk_every_row_matches_oracle(config_c):
+    # the longest rows (96K..128K keys), all 7 heads of the kv group
+    q, k, _, _, kd, _, qs = config_c
+    note("C every row of the last chunk")
+    check_every_row(q, k, qs, kd, 1536, 512, 0.84, True, 16, range(7), rep=7)
 
 
 def test_c_chunking_invariant(config_c):
@@ -196,6 +229,12 @@ def test_d_sampled_rows_match_oracle(config_d, th):
     rng = np.random.default_rng(2)
     rows = [0] + sorted(rng.choice(np.arange(1, 511), 5, replace=False).tolist()) + [511]
     check_rows(q, k, v, qs, kd, out_cpu, (0, 1), rows, th, False, 8192)
+
+
+def test_d_every_row_matches_oracle(config_d):
+    q, k, _, _, kd, _, qs = config_d
+    note("D every row")
+    check_every_row(q, k, qs, kd, 0, 512, 0.3, False, 8192, range(2))
 
 
 def test_d_split_selection_equals_exact_kernel(config_d):
@@ -283,3 +322,10 @@ def test_e_sampled_rows_match_oracle(config_e, th):
     out_cpu = out.float().cpu().numpy()
     nqb = qs.shape[2]
     check_rows(q, k, v, qs, kd, out_cpu, (0, 1), [0, 700, 1537, nqb - 1], th, False, 8192)
+
+
+def test_e_last_chunk_every_row_matches_oracle(config_e):
+    q, k, _, _, kd, _, qs = config_e
+    note("E every row of the last chunk")
+    nqb = qs.shape[2]
+    check_every_row(q, k, qs, kd, 1536, nqb - 1536, 0.43, False, 8192, range(2))
