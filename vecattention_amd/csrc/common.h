@@ -160,6 +160,25 @@ struct WorkOrder {
     bh = i % BH;
     return true;
   }
+  // Position of item (J, bh) in its XCD's dispatch sequence, modulo `period`
+  // and up to a constant, from the absolute q-block J (items are walked in
+  // descending J), so that every launch holding the row gives it the same
+  // value.  Only (back mod period * span) matters for the result, which keeps
+  // every product in 32 bits.
+  __device__ uint32_t xcd_rank(uint32_t J, uint32_t bh, uint32_t period) const {
+    const uint32_t hq = uint32_t(Hq), g = uint32_t(B) * uint32_t(Hk), r = hq / uint32_t(Hk);
+    const uint32_t back = (1u << 24) - J;  // J < 2^24 (the host bounds Sk, hence Sq / qps)
+    uint32_t rank;
+    if (kXcd % g == 0) {
+      const uint32_t copies = kXcd / g, bk = back % (period * copies);
+      rank = (bk * r + bh % r) / copies;
+    } else if (g % kXcd == 0 || equal_rows) {
+      rank = (back % (period * kTeam)) / kTeam;
+    } else {
+      rank = ((back % (period * kXcd)) * (uint32_t(B) * hq) + bh) / kXcd;
+    }
+    return rank % period;
+  }
   // map_item in 32-bit arithmetic, for kernels: every quantity is below 2^31
   // (the host bounds nrows * B * Hq by the grid limit), and a 64-bit division
   // costs a few hundred dependent scalar instructions at every work-group start.
