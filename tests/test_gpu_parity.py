@@ -508,6 +508,34 @@ def test_mfma_all_keys_equals_dense_sdpa(device):
     assert err.max().item() <= ATOL_MAX and err.mean().item() <= ATOL_MEAN
 
 
+@pytest.mark.parametrize("kernel", [nat.VA_ATTN_MFMA_STAGED, nat.VA_ATTN_MFMA_RING],
+                         ids=["staged", "ring"])
+def test_attention_scores_far_below_zero(device, kernel):
+    # Every score is about -150 (q = -c, k = +c, every key selected): the
+    # softmax is uniform and each output row is the mean of V.  A walk step
+    # past the end of a row's list (zero K rows, score 0) that escaped its
+    # mask would move the running maximum to 0 and underflow the row's sums.
+    # 1000 keys: every row ends in a partial tile, and rows start their walk
+    # at different tiles.
+    note("attn scores far below zero", kernel)
+    B, H, S, D = 1, 2, 1000, 128
+    c = 3.65  # q.k / sqrt(D) = -sqrt(128) * c^2 = -150.7
+    q = torch.full((B, H, S, D), -c, dtype=torch.bfloat16)
+    k = torch.full((B, H, S, D), c, dtype=torch.bfloat16)
+    v = torch.randn(B, H, S, D, generator=torch.Generator().manual_seed(5)).to(torch.bfloat16)
+    nqb = -(-S // 64)
+    cnt = torch.full((B, H, nqb), S, dtype=torch.int32, device=device)
+    idx = torch.arange(S, dtype=torch.int32, device=device).repeat(B * H * nqb)
+    out = torch.empty(B, H, S, D, dtype=torch.bfloat16, device=device)
+    stages.sparse_attention(q.to(device), k.to(device), v.to(device), out, 0, nqb, cnt, idx, False,
+                            64, kernel=kernel)
+    got = out.float().cpu()
+    assert torch.isfinite(got).all()
+    want = v.float().mean(dim=2, keepdim=True).expand(B, H, S, D)
+    err = (got - want).abs()
+    assert err.max().item() <= ATOL_MAX and err.mean().item() <= ATOL_MEAN
+
+
 # -------------------------------------------------------------- end to end --
 
 E2E_CASES = [

@@ -370,13 +370,16 @@ __global__ __launch_bounds__(QPS * 4, (kRing3 || D == 64) ? 3 : 2) void attn_mfm
   // [0, Sk) read zeros.  In the partial column tile (one per list, a uniform
   // test), rows past the list's end get key 2^32 - 1.
   const int p_col = n_col % kTileKeys != 0 ? ntiles - 1 : -1;
+  // Walk step of the partial column tile (-1: none) and its key count, so
+  // that the per-tile tests compare walk steps without mapping them.
+  const int u_pcol = __builtin_amdgcn_readfirstlane(p_col < 0 ? -1 : ntiles - 1 - c_rot);
+  const int lim_pcol = __builtin_amdgcn_readfirstlane(n_col - (t_col - 1) * kTileKeys);
   auto copy_pairs = [&](int u, int idslot, uint64_t (&pr)[H]) {
     uint32_t key[H];
 #pragma unroll
     for (int x = 0; x < H; ++x) key[x] = uint32_t(ids[idslot * kTileKeys + id_pos + x]);
-    const int lt = list_tile(u);
-    if (lt == p_col) {
-      const int lim = n_col - (lt - tc0) * kTileKeys;
+    if (u == u_pcol) {
+      const int lim = lim_pcol;
 #pragma unroll
       for (int x = 0; x < H; ++x)  // row (wave*H + x)*RPC + qr holds a key below lim
         if (qr >= lim - (wave * H + x) * RPC) key[x] = 0xffffffffu;
@@ -454,19 +457,19 @@ __global__ __launch_bounds__(QPS * 4, (kRing3 || D == 64) ? 3 : 2) void attn_mfm
     }
     return s;
   };
-  // Mask tile u's scores: empty slots, the causal diagonal, every slot of a
-  // tile past the end of the list.  Slot of s[e]: 32kc + 8(e/4) + 4hh + e%4.
-  // Tiles that may need masking, found with two comparisons: [m_lo, m_hi)
-  // holds the partial last tile of the initial blocks and the diagonal tiles,
-  // and every tile from m_col on is the partial last column tile or lies past
-  // the end of the list.
-  const int m_lo = t_init - (n_init % kTileKeys != 0 ? 1 : 0);
-  const uint32_t m_span = uint32_t(t_init + t_diag - m_lo);
-  const int m_col = ntiles - (n_col % kTileKeys != 0 ? 1 : 0);
+  // Mask the scores of walk step u: empty slots, the causal diagonal, every
+  // slot of a step past the end of the list.  Slot of s[e]: 32kc + 8(e/4) +
+  // 4hh + e%4.  Steps that may need masking, found with three comparisons:
+  // [m_lo, m_lo + m_span) holds the partial last tile of the initial blocks
+  // and the diagonal tiles, u_pcol is the partial column tile, and steps from
+  // ntiles on lie past the end of the list.
+  const int m_lo = __builtin_amdgcn_readfirstlane(t_init - (n_init % kTileKeys != 0 ? 1 : 0));
+  const uint32_t m_span = uint32_t(__builtin_amdgcn_readfirstlane(t_init + t_diag - m_lo));
   auto mask = [&](int u, f32x16_t& s) {
-    const int lt = list_tile(u);
-    if (uint32_t(lt - m_lo) >= m_span && lt < m_col) return;  // uniform: a full column tile
-    const TileInfo ti = tile_info(lt);
+    // uniform: a full column tile (the staged pipeline also scores the step
+    // past the last tile, whose slots are all masked)
+    if (uint32_t(u - m_lo) >= m_span && u != u_pcol && u < ntiles) return;
+    const TileInfo ti = tile_info(u < ntiles ? list_tile(u) : u);
     if (ti.diag || ti.lim < kTileKeys) {  // rare: partial, diagonal or empty tiles
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
@@ -570,9 +573,8 @@ __global__ __launch_bounds__(QPS * 4, (kRing3 || D == 64) ? 3 : 2) void attn_mfm
       uint32_t key[H];
 #pragma unroll
       for (int x = 0; x < H; ++x) key[x] = uint32_t(ids[idslot * kTileKeys + id_pos + x]);
-      const int lt = list_tile(u);
-      if (lt == p_col) {
-        const int lim = n_col - (lt - tc0) * kTileKeys;
+      if (u == u_pcol) {
+        const int lim = lim_pcol;
 #pragma unroll
         for (int x = 0; x < H; ++x)
           if (qr >= lim - (wave * H + x) * RPC) key[x] = 0xffffffffu;
