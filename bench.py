@@ -155,8 +155,9 @@ def gather_ceiling(dev, work_groups=256 * 12, steps=512, reps=5):
     (va_probe_gather: 256-byte rows at hashed ids into LDS, 8 copies in flight
     per wave), from a 2 MiB table (L2 hits) and a 64 MiB one (L2 misses served
     over the data fabric by the Infinity Cache)."""
+    sys.path.insert(0, os.path.join(ROOT, "tests", "numerics"))
+    import gather_probe
     from vecattention_amd import _native as nat
-    L = nat.lib()
     sink = torch.empty(work_groups, dtype=torch.int32, device=dev)
     stream = torch.cuda.current_stream(dev).cuda_stream
     moved = work_groups * 4 * steps * 1024
@@ -164,8 +165,8 @@ def gather_ceiling(dev, work_groups=256 * 12, steps=512, reps=5):
     for name, mib in (("l2", 2), ("fabric", 64)):
         rows = (mib << 20) // 256
         table = torch.ones(rows * 256, dtype=torch.uint8, device=dev)
-        call = lambda: nat.check("va_probe_gather", L.va_probe_gather(
-            nat.ptr(table), rows, work_groups, steps, 0, nat.ptr(sink), stream))
+        call = lambda: gather_probe.gather(nat.ptr(table), rows, work_groups, steps, 0,
+                                           nat.ptr(sink), stream)
         call()
         torch.cuda.synchronize()
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)

@@ -274,10 +274,14 @@ int va_sparse_attn_segments(int dtype, const void* q, int64_t sqb, int64_t sqh, 
                             int64_t dense_stride, int64_t segment_keys, const int32_t* counts,
                             const int32_t* indices, float softmax_scale, void* stream);
 
-/* Bytes of device workspace va_prefill needs (256-byte aligned segments). */
+/*
+ * Bytes of device workspace va_prefill needs for the same sizes and bsq
+ * (256-byte aligned segments; -1 on invalid sizes).  bsq matters for causal
+ * prefills only: their row groups start at multiples of bsq rows.
+ */
 int64_t va_prefill_workspace_size(int dtype, int64_t B, int64_t Hq, int64_t Sq, int64_t Sk,
                                   int64_t D, int64_t q_pooling_size, int causal,
-                                  int64_t chunk_size);
+                                  int64_t chunk_size, int64_t bsq);
 
 /*
  * Kernels va_prefill runs for these tensors and parameters, as a bit set
@@ -321,19 +325,6 @@ int va_prefill(int dtype, const void* q, int64_t sqb, int64_t sqh, int64_t sqs,
                int64_t D, float gap, const float* gaps, int64_t q_pooling_size,
                int64_t k_local_size, int64_t group_k_block, int causal, int64_t chunk_size,
                int64_t bsq, void* workspace, int64_t workspace_bytes, void* stream);
-
-/*
- * Measurement probe, no counterpart in the reference: the L2 -> LDS row-gather
- * rate the sparse attention kernel is bound by.  `work_groups` work-groups of
- * 4 waves each copy `steps` (a multiple of 16) tiles of four 256-byte rows of
- * `table` (`rows` rows, at most 2^23) into LDS with the attention kernel's
- * copy instruction, 8 copies in flight per wave; rows are drawn by an integer
- * hash (`sequential` 0) or consecutively (1).  Bytes moved:
- * work_groups * 4 * steps * 1024.  `sink` (work_groups uint32) receives one
- * value per work-group.  Time it with events on `stream`.
- */
-int va_probe_gather(const void* table, int64_t rows, int64_t work_groups, int64_t steps,
-                    int sequential, uint32_t* sink, void* stream);
 
 #ifdef __cplusplus
 }

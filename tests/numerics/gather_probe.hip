@@ -1,4 +1,6 @@
-// Row-gather probe: va_probe_gather.
+// Row-gather probe: va_probe_gather (measurement helper, built into
+// tests/numerics/libgatherprobe.so by __graft_entry__.build(); not part of
+// libvecattn.so).
 //
 // The sparse attention kernel moves every selected key's K and V rows from L2
 // (or, on an L2 miss, from the data fabric) into LDS with buffer_load_dwordx4
@@ -11,13 +13,13 @@
 // (tens of MiB, served by the Infinity Cache) bounds what any kernel built on
 // these gathers can reach; bench.py reports the attention's gather rate
 // against it.
+#include <cstdio>
+
 #include "../../include/vecattn.h"
-#include "common.h"
-#include "lanes.h"
+#include "../../vecattention_amd/csrc/common.h"
+#include "../../vecattention_amd/csrc/lanes.h"
 
 namespace va {
-int api_error(int code, const char* fmt, ...);
-
 namespace {
 
 constexpr int kProbeWaves = 4;
@@ -61,12 +63,15 @@ extern "C" int va_probe_gather(const void* table, int64_t rows, int64_t work_gro
   if (table == nullptr || sink == nullptr || rows <= 0 || rows > (int64_t(1) << 31) / 256 ||
       work_groups <= 0 || work_groups > (int64_t(1) << 20) || steps <= 0 || steps % 16 != 0 ||
       work_groups * va::kProbeWaves * steps * 4 > (int64_t(1) << 32))
-    return va::api_error(VA_ERR_ARG, "probe: rows in (0, 2^23], work_groups in (0, 2^20], "
-                                     "steps a positive multiple of 16, ids below 2^32");
+    return VA_ERR_ARG;  // rows in (0, 2^23], work_groups in (0, 2^20], steps % 16 == 0,
+                        // ids below 2^32
   hipLaunchKernelGGL(va::gather_probe_kernel, dim3(unsigned(work_groups)),
                      dim3(64 * va::kProbeWaves), 0, static_cast<hipStream_t>(stream), table,
                      uint32_t(rows), sequential, int(steps), sink);
   const hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return va::api_error(VA_ERR_HIP, "probe launch: %s", hipGetErrorString(e));
+  if (e != hipSuccess) {
+    std::fprintf(stderr, "va_probe_gather: launch failed: %s\n", hipGetErrorString(e));
+    return VA_ERR_HIP;
+  }
   return VA_OK;
 }

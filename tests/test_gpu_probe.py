@@ -1,9 +1,16 @@
-"""The row-gather probe (va_probe_gather) behind bench.py's gather ceiling:
-its copies land in LDS and every work-group reports the first byte it read."""
+"""The row-gather probe (va_probe_gather, tests/numerics/gather_probe.hip)
+behind bench.py's gather ceiling: its copies land in LDS and every work-group
+reports the first byte it read."""
+import os
+import sys
+
 import pytest
 import torch
 
-from vecattention_amd import _native as nat
+sys.path.insert(0, os.path.join(os.path.dirname(os.path.abspath(__file__)), "numerics"))
+import gather_probe  # noqa: E402
+
+from vecattention_amd import _native as nat  # noqa: E402
 
 pytestmark = pytest.mark.gpu
 
@@ -13,8 +20,7 @@ def test_probe_copies_rows_into_lds(device, sequential):
     rows, wgs, steps = 4096, 16, 32
     table = torch.full((rows * 256,), 3, dtype=torch.uint8, device=device)
     sink = torch.zeros(wgs, dtype=torch.int32, device=device)
-    rc = nat.lib().va_probe_gather(nat.ptr(table), rows, wgs, steps, sequential, nat.ptr(sink),
-                                   torch.cuda.current_stream(device).cuda_stream)
-    nat.check("va_probe_gather", rc)
+    gather_probe.gather(nat.ptr(table), rows, wgs, steps, sequential, nat.ptr(sink),
+                        torch.cuda.current_stream(device).cuda_stream)
     torch.cuda.synchronize()
     assert torch.equal(sink.cpu(), torch.full((wgs,), 3, dtype=torch.int32))

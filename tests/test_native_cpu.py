@@ -4,6 +4,7 @@ arguments into error codes before any device work."""
 import ctypes
 import os
 import re
+import sys
 
 import numpy as np
 import pytest
@@ -111,7 +112,7 @@ def test_workspace_size_covers_largest_row_group(L):
     # slots or one group), not the whole 32K chunk.
     B, Hq, S, D, qps, chunk = 1, 28, 131072, 128, 64, 32768
     qs_bytes = B * Hq * (S // qps) * D * 2
-    ws = L.va_prefill_workspace_size(nat.VA_BF16, B, Hq, S, S, D, qps, 1, chunk)
+    ws = L.va_prefill_workspace_size(nat.VA_BF16, B, Hq, S, S, D, qps, 1, chunk, 64)
     whole = L.va_select_index_capacity(B, Hq, S, qps, 1, 1, (S - chunk) // qps, chunk // qps, 0)
     group = L.va_select_index_capacity(B, Hq, S, qps, 1, 1, S // qps - 128, 128, 0)
     assert group * 4 <= 2 << 30
@@ -120,9 +121,24 @@ def test_workspace_size_covers_largest_row_group(L):
     assert ws < 2 * 2 ** 30 + qs_bytes + (64 << 20)
     # non-causal chunks are not split: every row sees every key
     S2, H2 = 119056, 24
-    ws2 = L.va_prefill_workspace_size(nat.VA_BF16, B, H2, S2, S2, D, qps, 0, chunk)
+    ws2 = L.va_prefill_workspace_size(nat.VA_BF16, B, H2, S2, S2, D, qps, 0, chunk, 64)
     full = L.va_select_index_capacity(B, H2, S2, qps, 0, 0, 0, chunk // qps, 0)
     assert ws2 >= full * 4 + B * H2 * (-(-S2 // qps)) * D * 2
+
+
+def test_workspace_size_follows_bsq(L):
+    # Causal row groups are runs of units of ceil(128 / bsq) * bsq rows from the
+    # chunk origin: the query sizes them for the bsq va_prefill is given.
+    B, Hq, S, D, qps, chunk = 1, 28, 131072, 128, 64, 32768
+    for bsq in (3, 5, 64, 100, 256):
+        unit = -(-128 // bsq) * bsq
+        ws = L.va_prefill_workspace_size(nat.VA_BF16, B, Hq, S, S, D, qps, 1, chunk, bsq)
+        # the last unit of the last chunk, the one with the longest rows, fits
+        nqb, J0 = S // qps, (S - chunk) // qps
+        last = J0 + (chunk // qps - 1) // unit * unit
+        cap = L.va_select_index_capacity(B, Hq, S, qps, 1, 1, last, nqb - last, 0)
+        assert ws >= cap * 4
+    assert L.va_prefill_workspace_size(nat.VA_BF16, B, Hq, S, S, D, qps, 1, chunk, 0) == -1
 
 
 def _dense(L, **over):
@@ -225,6 +241,8 @@ def test_prefill_kernels_reports_the_mfma_path(L):
     # the ring form exists for D = 128 and 64-row blocks only
     assert not _plan(L, D=64) & ring and not _plan(L, qps=128) & ring
     assert _plan(L, Hq=6, Hk=4) == nat.VA_ERR_ARG             # q heads not a multiple
+    # va_prefill takes q_pooling_size 64 or 128 only, and so does its plan
+    assert _plan(L, qps=96) == nat.VA_ERR_ARG
 
 
 def test_prefill_kernels_reports_the_slow_paths(L):
@@ -253,11 +271,20 @@ def test_prefill_kernels_reports_the_slow_paths(L):
     assert _plan(L, D=0) < 0
 
 
-def test_probe_rejects_bad_sizes(L):
-    # Checked before any launch: fake addresses are never dereferenced.
+def test_probe_rejects_bad_sizes():
+    # The helper library (not the product): checked before any launch, so fake
+    # addresses are never dereferenced.
+    sys.path.insert(0, os.path.join(os.path.dirname(os.path.abspath(__file__)), "numerics"))
+    import gather_probe
+    P = gather_probe.lib()
     t, sink = 256, 512
-    assert L.va_probe_gather(t, 1024, 8, 15, 0, sink, None) == nat.VA_ERR_ARG   # steps % 16
-    assert L.va_probe_gather(t, 0, 8, 16, 0, sink, None) == nat.VA_ERR_ARG      # no rows
-    assert L.va_probe_gather(t, (1 << 23) + 1, 8, 16, 0, sink, None) == nat.VA_ERR_ARG
-    assert L.va_probe_gather(None, 1024, 8, 16, 0, sink, None) == nat.VA_ERR_ARG
-    assert L.va_probe_gather(t, 1024, 1 << 20, 1 << 12, 0, sink, None) == nat.VA_ERR_ARG  # ids
+    assert P.va_probe_gather(t, 1024, 8, 15, 0, sink, None) == nat.VA_ERR_ARG   # steps % 16
+    assert P.va_probe_gather(t, 0, 8, 16, 0, sink, None) == nat.VA_ERR_ARG      # no rows
+    assert P.va_probe_gather(t, (1 << 23) + 1, 8, 16, 0, sink, None) == nat.VA_ERR_ARG
+    assert P.va_probe_gather(None, 1024, 8, 16, 0, sink, None) == nat.VA_ERR_ARG
+    assert P.va_probe_gather(t, 1024, 1 << 20, 1 << 12, 0, sink, None) == nat.VA_ERR_ARG  # ids
+
+
+def test_product_exports_no_probe():
+    L = nat.lib()
+    assert not hasattr(L, "va_probe_gather")

@@ -70,12 +70,15 @@ def test_noalloc_decode_equals_workspace_decode_twice(device):
 
 def test_noalloc_decode_rejects_sizes_beyond_its_array(device):
     # 64 q heads over one kv head and a long cache need more partial states
-    # than the array holds: rejected before any launch, nothing written.
+    # than the array holds: rejected before any launch, nothing written.  K/V
+    # have their full size (256 MiB each), so that if the size check ever
+    # regressed the launch would read in bounds and fail the assertions below
+    # instead of reading past the allocation.
     Hq, Hk, L, D = 64, 1, 1 << 20, 128
     need = int(nat.lib().va_decode_workspace_size(Hq, Hk, L, D))
     assert need > int(nat.lib().va_decode_noalloc_scratch_bytes())
     q = torch.zeros(Hq, D, dtype=torch.bfloat16, device=device)
-    kv = torch.zeros(1, Hk, D, dtype=torch.bfloat16, device=device)  # never read
+    kv = torch.zeros(L, Hk, D, dtype=torch.bfloat16, device=device)  # NHD, never read
     out = torch.full((Hq, D), 7.0, dtype=torch.bfloat16, device=device)
     rc = nat.lib().va_decode_attn_noalloc(
         nat.VA_BF16, nat.ptr(q), q.stride(0), nat.ptr(kv), kv.stride(1), kv.stride(0),

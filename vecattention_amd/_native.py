@@ -70,14 +70,14 @@ SIGNATURES = {
     "va_decode_noalloc_scratch_bytes": (_i64, []),
     "va_decode_attn_noalloc": (_int, [_int, _vp, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _vp,
                                       _i64, _i64, _i64, _i64, _i64, _f32, _int, _vp]),
-    "va_prefill_workspace_size": (_i64, [_int, _i64, _i64, _i64, _i64, _i64, _i64, _int, _i64]),
+    "va_prefill_workspace_size": (_i64, [_int, _i64, _i64, _i64, _i64, _i64, _i64, _int, _i64,
+                                         _i64]),
     "va_prefill_kernels": (_int, [_int, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _vp, _i64,
                                   _i64, _i64, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                                   _i64, _i64, _i64]),
     "va_prefill": (_int, [_int, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _vp, _i64, _i64,
                           _i64, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _f32,
                           _vp, _i64, _i64, _i64, _int, _i64, _i64, _vp, _i64, _vp]),
-    "va_probe_gather": (_int, [_vp, _i64, _i64, _i64, _int, _vp, _vp]),
 }
 
 

@@ -97,10 +97,6 @@ bool pow2(int64_t x) { return x > 0 && (x & (x - 1)) == 0; }
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
 constexpr int64_t kMaxSegments = 64;  // key segments of a split selection
-// BLOCK_SIZE_Q the workspace query assumes (every configuration of the
-// reference's shipped launch caches uses 64); va_prefill checks the workspace
-// against the bsq it is given.
-constexpr int64_t kPrefillBsq = 64;
 
 va::RowLayout make_layout(int64_t J0, int64_t nc, int64_t qps, int64_t Sk, int causal,
                           int wo_init, int64_t dense_stride) {
@@ -787,13 +783,13 @@ static void prefill_segments(int dtype, int64_t B, int64_t Hq, int64_t Sq, int64
 }
 
 int64_t va_prefill_workspace_size(int dtype, int64_t B, int64_t Hq, int64_t Sq, int64_t Sk,
-                                  int64_t D, int64_t qps, int causal, int64_t chunk_size) {
+                                  int64_t D, int64_t qps, int causal, int64_t chunk_size,
+                                  int64_t bsq) {
   if (!dtype_ok(dtype) || B <= 0 || Hq <= 0 || Sq <= 0 || Sk <= 0 || D <= 0 || qps <= 0 ||
-      chunk_size <= 0 || chunk_size % qps)
+      chunk_size <= 0 || chunk_size % qps || bsq <= 0)
     return -1;
   int64_t a, b, c, d, e;
-  prefill_segments(dtype, B, Hq, Sq, Sk, D, qps, causal, chunk_size, kPrefillBsq, &a, &b, &c, &d,
-                   &e);
+  prefill_segments(dtype, B, Hq, Sq, Sk, D, qps, causal, chunk_size, bsq, &a, &b, &c, &d, &e);
   return a + b + c + d + e;
 }
 
@@ -805,6 +801,10 @@ int va_prefill_kernels(int dtype, const void* q, int64_t sqb, int64_t sqh, int64
   if (!dtype_ok(dtype) || Hq <= 0 || Hk <= 0 || Hq % Hk != 0 || Sk <= 0 || D <= 0 || qps <= 0 ||
       bk <= 0 || group <= 0)
     return fail(VA_ERR_ARG, "invalid prefill sizes");
+  // va_prefill's own precondition; with q_pooling_size 64 or 128 the first
+  // selectable key (0, or q_pooling_size for causal rows) is 64-aligned, as
+  // the wave selection kernel needs, so the plan below is the one it runs.
+  if (qps != 64 && qps != 128) return fail(VA_ERR_ARG, "q_pooling_size must be 64 or 128");
   // The pooled queries live in the 256-byte aligned workspace with element
   // strides that are multiples of D: any aligned address and D strides stand
   // for them.
@@ -846,21 +846,17 @@ int va_prefill(int dtype, const void* q, int64_t sqb, int64_t sqh, int64_t sqs, 
   if (qps != 64 && qps != 128) return fail(VA_ERR_ARG, "q_pooling_size must be 64 or 128");
   if (!q || !k || !v || !out) return fail(VA_ERR_ARG, "null tensor pointer");
   if (causal && Sq != Sk) return fail(VA_ERR_UNSUPPORTED, "causal prefill needs Sq == Sk");
-  const int64_t need = va_prefill_workspace_size(dtype, B, Hq, Sq, Sk, D, qps, causal, chunk_size);
+  if (bsq <= 0) return fail(VA_ERR_ARG, "bsq must be positive");
+  const int64_t need =
+      va_prefill_workspace_size(dtype, B, Hq, Sq, Sk, D, qps, causal, chunk_size, bsq);
   if (need < 0) return fail(VA_ERR_ARG, "invalid prefill sizes");
   if (!workspace || workspace_bytes < need)
-    return fail(VA_ERR_WORKSPACE, "workspace %lld bytes < required %lld",
-                (long long)workspace_bytes, (long long)need);
+    return fail(VA_ERR_WORKSPACE, "workspace %lld bytes < required %lld (bsq %lld)",
+                (long long)workspace_bytes, (long long)need, (long long)bsq);
   const int64_t nqb = cdiv(Sq, qps);
-  if (bsq <= 0) return fail(VA_ERR_ARG, "bsq must be positive");
   int64_t qs_bytes, cnt_bytes, idx_bytes, kn_bytes, carry_bytes;
   prefill_segments(dtype, B, Hq, Sq, Sk, D, qps, causal, chunk_size, bsq, &qs_bytes, &cnt_bytes,
                    &idx_bytes, &kn_bytes, &carry_bytes);
-  if (qs_bytes + cnt_bytes + idx_bytes + kn_bytes + carry_bytes > workspace_bytes)
-    return fail(VA_ERR_WORKSPACE, "workspace %lld bytes < required %lld (bsq %lld)",
-                (long long)workspace_bytes,
-                (long long)(qs_bytes + cnt_bytes + idx_bytes + kn_bytes + carry_bytes),
-                (long long)bsq);
   char* ws = static_cast<char*>(workspace);
   void* qs = ws;
   int32_t* counts = reinterpret_cast<int32_t*>(ws + qs_bytes);

@@ -43,12 +43,13 @@ __device__ inline uint32_t lds_addr(const void* p) {
 // assembly so that the compiler's memory-counter bookkeeping does not make
 // LDS reads of the other stage wait for these copies; completion is awaited
 // explicitly with vm_lds_barrier().  M0 (the LDS base) is set in the same
-// statement; nothing else in these kernels uses M0.
+// statement, and every such statement lists M0 (and SCC, where a scalar add
+// sets it) as clobbered, so the compiler keeps no value of its own there.
 __device__ inline void copy16_to_lds(__amdgpu_buffer_rsrc_t r, uint32_t lds, uint32_t voffset) {
   asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
                :
                : "s"(__builtin_amdgcn_readfirstlane(int(lds))), "v"(voffset), "s"(r)
-               : "memory");
+               : "memory", "m0");
 }
 // The same through a row resource (make_rsrc_rows): the lane's address is
 // row index * stride + byte offset, the pair packed as index | offset << 32.
@@ -61,7 +62,7 @@ __device__ inline void copy16_row_to_lds(__amdgpu_buffer_rsrc_t r, uint32_t lds,
   asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 idxen offen sc1 lds"
                :
                : "s"(__builtin_amdgcn_readfirstlane(int(lds))), "v"(index_offset), "s"(r)
-               : "memory");
+               : "memory", "m0");
 }
 // The same with the LDS address given as a wave-uniform base plus a
 // compile-time offset, so that setting M0 costs one scalar add.
@@ -71,14 +72,14 @@ __device__ inline void copy16_row_to_lds_at(__amdgpu_buffer_rsrc_t r, uint32_t l
   asm volatile("s_add_u32 m0, %0, %3\n\tbuffer_load_dwordx4 %1, %2, 0 idxen offen sc1 lds"
                :
                : "s"(lds_base), "v"(index_offset), "s"(r), "n"(kOffset)
-               : "memory");
+               : "memory", "m0", "scc");
 }
 // One dword per lane, device scope (read once, as copy16_row_to_lds).
 __device__ inline void copy4_to_lds(__amdgpu_buffer_rsrc_t r, uint32_t lds, uint32_t voffset) {
   asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen sc1 lds"
                :
                : "s"(__builtin_amdgcn_readfirstlane(int(lds))), "v"(voffset), "s"(r)
-               : "memory");
+               : "memory", "m0");
 }
 
 // Max of x over lanes l and l ^ 32.  x must not be a signaling NaN (it is an

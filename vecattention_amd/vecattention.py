@@ -161,12 +161,12 @@ def VecAttention_prefill(
     if flags < 0:
         nat.check("va_prefill_kernels", flags)
     _warn_slow_path(flags, q.dtype, D, q_pooling_size, k_local_size)
+    bsq = reference_block_size_q(q_pooling_size, k_local_size, group_k_block, D, causal)
     ws_bytes = L.va_prefill_workspace_size(dt, B, Hq, S, Sk, D, q_pooling_size, int(causal),
-                                           chunk_size)
+                                           chunk_size, bsq)
     if ws_bytes < 0:
         raise AssertionError("invalid VecAttention_prefill sizes")
     workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
-    bsq = reference_block_size_q(q_pooling_size, k_local_size, group_k_block, D, causal)
     with torch.cuda.device(q.device):
         rc = L.va_prefill(
             dt, nat.ptr(q), q.stride(0), q.stride(1), q.stride(2),
