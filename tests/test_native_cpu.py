@@ -4,6 +4,7 @@ arguments into error codes before any device work."""
 import ctypes
 import os
 import re
+import subprocess
 import sys
 
 import numpy as np
@@ -288,3 +289,29 @@ def test_probe_rejects_bad_sizes():
 def test_product_exports_no_probe():
     L = nat.lib()
     assert not hasattr(L, "va_probe_gather")
+
+
+@pytest.mark.parametrize("src", ["attn_mfma.hip", "select_wave.hip"])
+def test_m0_is_only_set_by_the_lds_copies(src, tmp_path):
+    # The LDS-DMA copies set M0 inside inline assembly (lanes.h).  M0 is
+    # reserved to the compiler, which ignores it as a clobber, so the copies
+    # are only safe while no compiler-generated instruction reads or writes
+    # M0: check the device assembly outside the inline-asm blocks.
+    from vecattention_amd import build as vbuild
+    out = tmp_path / (src + ".s")
+    subprocess.run([vbuild.hipcc(), *vbuild.FLAGS, "--cuda-device-only", "-S",
+                    os.path.join(vbuild.CSRC, src), "-o", str(out)],
+                   check=True, capture_output=True)
+    inside, outside, sets = False, [], 0
+    for line in out.read_text().splitlines():
+        if "ASMSTART" in line:
+            inside = True
+        elif "ASMEND" in line:
+            inside = False
+        elif not line.lstrip().startswith(";") and re.search(r"\bm0\b", line):
+            if inside:
+                sets += 1
+            else:
+                outside.append(line.strip())
+    assert sets > 0
+    assert outside == []

@@ -43,13 +43,16 @@ __device__ inline uint32_t lds_addr(const void* p) {
 // assembly so that the compiler's memory-counter bookkeeping does not make
 // LDS reads of the other stage wait for these copies; completion is awaited
 // explicitly with vm_lds_barrier().  M0 (the LDS base) is set in the same
-// statement, and every such statement lists M0 (and SCC, where a scalar add
-// sets it) as clobbered, so the compiler keeps no value of its own there.
+// statement.  M0 is a reserved register to the compiler, which ignores it in
+// a clobber list; these kernels issue no instruction of their own that reads
+// M0 (no LDS-DMA builtins, no indirect register indexing), which
+// tests/test_native_cpu.py checks on the generated assembly.  A statement that
+// sets M0 with a scalar add lists SCC as clobbered.
 __device__ inline void copy16_to_lds(__amdgpu_buffer_rsrc_t r, uint32_t lds, uint32_t voffset) {
   asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
                :
                : "s"(__builtin_amdgcn_readfirstlane(int(lds))), "v"(voffset), "s"(r)
-               : "memory", "m0");
+               : "memory");
 }
 // The same through a row resource (make_rsrc_rows): the lane's address is
 // row index * stride + byte offset, the pair packed as index | offset << 32.
@@ -62,7 +65,7 @@ __device__ inline void copy16_row_to_lds(__amdgpu_buffer_rsrc_t r, uint32_t lds,
   asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 idxen offen sc1 lds"
                :
                : "s"(__builtin_amdgcn_readfirstlane(int(lds))), "v"(index_offset), "s"(r)
-               : "memory", "m0");
+               : "memory");
 }
 // The same with the LDS address given as a wave-uniform base plus a
 // compile-time offset, so that setting M0 costs one scalar add.
@@ -72,14 +75,14 @@ __device__ inline void copy16_row_to_lds_at(__amdgpu_buffer_rsrc_t r, uint32_t l
   asm volatile("s_add_u32 m0, %0, %3\n\tbuffer_load_dwordx4 %1, %2, 0 idxen offen sc1 lds"
                :
                : "s"(lds_base), "v"(index_offset), "s"(r), "n"(kOffset)
-               : "memory", "m0", "scc");
+               : "memory", "scc");
 }
 // One dword per lane, device scope (read once, as copy16_row_to_lds).
 __device__ inline void copy4_to_lds(__amdgpu_buffer_rsrc_t r, uint32_t lds, uint32_t voffset) {
   asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen sc1 lds"
                :
                : "s"(__builtin_amdgcn_readfirstlane(int(lds))), "v"(voffset), "s"(r)
-               : "memory", "m0");
+               : "memory");
 }
 
 // Max of x over lanes l and l ^ 32.  x must not be a signaling NaN (it is an
