@@ -143,30 +143,6 @@ int va_select_segments(int dtype, const void* qs, int64_t sqb, int64_t sqh, int6
                        int64_t dense_stride, int64_t segment_keys, int32_t* counts,
                        int32_t* indices, float* scratch, int64_t scratch_floats, void* stream);
 
-/*
- * va_select_segments writing the lists of chunk-row pairs (rows 2i and 2i+1
- * of [J0, J0+nc), "A" and "B"), the form va_prefill uses internally: within
- * each segment s, row A's slots hold the keys both rows selected (ascending
- * from the segment's first slot, max(s*segment_keys, smin) - smin) and the
- * keys only A selected (descending from the segment's last slot: the row's
- * capacity, or the next segment's first slot), row B's slots the keys only B
- * selected (ascending from the segment's first slot), and
- * pair_common[((b*Hq + h)*ceil(nc/2) + i)*nseg + s] the number of common keys.
- * counts are per row, as in va_select_segments, so each row's list is exactly
- * recoverable: A = common + A-only, B = common + B-only.  Needs the
- * VA_SEL_WAVE kernel.  No counterpart in the reference: the layout lets the
- * attention gather every shared key once for both rows
- * (va_sparse_attn_segments_paired).
- */
-int va_select_segments_paired(int dtype, const void* qs, int64_t sqb, int64_t sqh, int64_t sqn,
-                              const void* k, int64_t skb, int64_t skh, int64_t sks, int64_t B,
-                              int64_t Hq, int64_t Hk, int64_t Sk, int64_t D, int64_t qps,
-                              int64_t bk, int64_t group, int causal, int wo_init, int64_t J0,
-                              int64_t nc, int64_t bsq, float gap, const float* gaps,
-                              int64_t dense_stride, int64_t segment_keys, int32_t* counts,
-                              int32_t* indices, int32_t* pair_common, float* scratch,
-                              int64_t scratch_floats, void* stream);
-
 /* fp32 scratch floats va_select's MFMA kernel needs (B*Hk key-norm slots). */
 int64_t va_select_scratch_floats(int64_t B, int64_t Hk);
 
@@ -297,25 +273,6 @@ int va_sparse_attn_segments(int dtype, const void* q, int64_t sqb, int64_t sqh, 
                             int causal, int wo_init, int64_t J0, int64_t nc,
                             int64_t dense_stride, int64_t segment_keys, const int32_t* counts,
                             const int32_t* indices, float softmax_scale, void* stream);
-
-/*
- * va_sparse_attn_segments on the paired lists of va_select_segments_paired:
- * one work-group per row pair gathers the local blocks, the common keys once
- * for both rows, then each row's own keys (the pair form of the MFMA kernel:
- * bf16/fp16, D = 128, q_pooling_size 64).  Same result as the per-row form
- * within rounding (the key order differs).  Replaces the reference's
- * sparse_attn_func call (spattn/src/VecAttention.py:110-121) in va_prefill.
- */
-int va_sparse_attn_segments_paired(int dtype, const void* q, int64_t sqb, int64_t sqh,
-                                   int64_t sqs, const void* k, int64_t skb, int64_t skh,
-                                   int64_t sks, const void* v, int64_t svb, int64_t svh,
-                                   int64_t svs, void* out, int64_t sob, int64_t soh, int64_t sos,
-                                   int64_t B, int64_t Hq, int64_t Hk, int64_t Sq, int64_t Sk,
-                                   int64_t D, int64_t qps, int causal, int wo_init, int64_t J0,
-                                   int64_t nc, int64_t dense_stride, int64_t segment_keys,
-                                   const int32_t* counts, const int32_t* indices,
-                                   const int32_t* pair_common, float softmax_scale,
-                                   void* stream);
 
 /*
  * Bytes of device workspace va_prefill needs for the same sizes and bsq

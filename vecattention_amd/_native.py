@@ -45,10 +45,6 @@ SIGNATURES = {
     "va_select_segments": (_int, [_int, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _i64, _i64,
                                   _i64, _i64, _i64, _i64, _i64, _i64, _int, _int, _i64, _i64, _i64,
                                   _f32, _vp, _i64, _i64, _vp, _vp, _vp, _i64, _vp]),
-    "va_select_segments_paired": (_int, [_int, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64,
-                                         _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _int,
-                                         _int, _i64, _i64, _i64, _f32, _vp, _i64, _i64, _vp,
-                                         _vp, _vp, _vp, _i64, _vp]),
     "va_select_scratch_floats": (_i64, [_i64, _i64]),
     "va_select_segments_scratch_floats": (_i64, [_i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64]),
     "va_select_index_capacity": (_i64, [_i64, _i64, _i64, _i64, _int, _int, _i64, _i64, _i64]),
@@ -63,10 +59,6 @@ SIGNATURES = {
                                        _i64, _i64, _i64, _vp, _i64, _i64, _i64, _i64, _i64, _i64,
                                        _i64, _i64, _i64, _i64, _int, _int, _i64, _i64, _i64, _i64,
                                        _vp, _vp, _f32, _vp]),
-    "va_sparse_attn_segments_paired": (_int, [_int, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64,
-                                              _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _i64,
-                                              _i64, _i64, _i64, _i64, _i64, _i64, _int, _int,
-                                              _i64, _i64, _i64, _i64, _vp, _vp, _vp, _f32, _vp]),
     "va_sparse_row_stats": (_int, [_int, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _i64, _i64,
                                    _i64, _i64, _i64, _i64, _i64, _int, _int, _i64, _i64, _i64, _vp,
                                    _vp, _f32, _int, _vp, _vp]),

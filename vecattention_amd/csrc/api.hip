@@ -41,7 +41,7 @@ hipError_t launch_select_wave(int dtype, const void* qs, int64_t sqb, int64_t sq
                               int64_t bk, int64_t group, int causal, int64_t bsq, float gap,
                               const float* gaps, const float* kmax, const RowLayout& lay,
                               int32_t* counts, int32_t* indices, int64_t segk, void* carry,
-                              int mode, int32_t* pcommon, hipStream_t stream);
+                              int mode, hipStream_t stream);
 constexpr int64_t kSegCarryBytes = 32;  // per (row, segment) record of the two-pass selection
 int64_t select_wave_segment_keys(int64_t Sk, int64_t bk, int64_t group);
 int64_t select_wave_carry_segment_keys(int64_t Sk, int64_t bk, int64_t group);
@@ -49,13 +49,6 @@ int64_t key_norm_scratch_floats(int64_t B, int64_t Hk);
 hipError_t launch_key_norm(int dtype, const void* k, int64_t skb, int64_t skh, int64_t sks,
                            int64_t B, int64_t Hk, int64_t Sk, int64_t D, float* scratch,
                            hipStream_t stream);
-bool attn_pair_supported(int dtype, int64_t D, int64_t qps);
-hipError_t launch_attn_pair(int dtype, const void* q, const int64_t* sq, const void* k,
-                            const int64_t* sk, const void* v, const int64_t* sv, void* out,
-                            const int64_t* so, int64_t B, int64_t Hq, int64_t Hk, int64_t Sq,
-                            int64_t Sk, int causal, float scale_log2, const int32_t* counts,
-                            const int32_t* pcommon, const int32_t* indices, const RowLayout& lay,
-                            int nseg, int segk, hipStream_t stream);
 hipError_t launch_attn_mfma(int dtype, int64_t D, int64_t qps, const void* q, const int64_t* sq,
                             const void* k, const int64_t* sk, const void* v, const int64_t* sv,
                             void* out, const int64_t* so, int64_t B, int64_t Hq, int64_t Hk,
@@ -212,14 +205,14 @@ static int select_impl(int dtype, const void* qs, int64_t sqb, int64_t sqh, int6
                        int64_t bsq, float gap, const float* gaps, int64_t dense_stride,
                        int32_t* counts, int32_t* indices, SelKernel which, const float* kmax,
                        int64_t segk, hipStream_t stream, void* carry = nullptr,
-                       int mode = 0, int32_t* pcommon = nullptr) {
+                       int mode = 0) {
   const va::RowLayout lay = make_layout(J0, nc, qps, Sk, causal, wo_init, dense_stride);
   group = effective_group(group, Sk, bk);
   hipError_t e;
   if (which == kSelWave)
     e = va::launch_select_wave(dtype, qs, sqb, sqh, sqn, k, skb, skh, sks, B, Hq, Hk, Sk, D, qps,
                                bk, group, causal, bsq, gap, gaps, kmax, lay, counts, indices,
-                               segk, carry, mode, pcommon, stream);
+                               segk, carry, mode, stream);
   else if (which == kSelMfma)
     e = va::launch_select_mfma(dtype, qs, sqb, sqh, sqn, k, skb, skh, sks, B, Hq, Hk, Sk, D, qps,
                                bk, group, causal, bsq, gap, gaps, kmax, lay, counts, indices,
@@ -340,14 +333,13 @@ int64_t va_select_segments_scratch_floats(int64_t B, int64_t Hq, int64_t Hk, int
   return kn + va::kSegCarryBytes / 4 * B * Hq * nc * cdiv(Sk, segment_keys);  // carry records
 }
 
-static int select_segments_impl(int dtype, const void* qs, int64_t sqb, int64_t sqh,
-                                int64_t sqn, const void* k, int64_t skb, int64_t skh, int64_t sks,
-                                int64_t B, int64_t Hq, int64_t Hk, int64_t Sk, int64_t D,
-                                int64_t qps, int64_t bk, int64_t group, int causal, int wo_init,
-                                int64_t J0, int64_t nc, int64_t bsq, float gap, const float* gaps,
-                                int64_t dense_stride, int64_t segment_keys, int32_t* counts,
-                                int32_t* indices, float* scratch, int64_t scratch_floats,
-                                int32_t* pcommon, void* stream) {
+int va_select_segments(int dtype, const void* qs, int64_t sqb, int64_t sqh, int64_t sqn,
+                       const void* k, int64_t skb, int64_t skh, int64_t sks, int64_t B,
+                       int64_t Hq, int64_t Hk, int64_t Sk, int64_t D, int64_t qps, int64_t bk,
+                       int64_t group, int causal, int wo_init, int64_t J0, int64_t nc, int64_t bsq,
+                       float gap, const float* gaps, int64_t dense_stride, int64_t segment_keys,
+                       int32_t* counts, int32_t* indices, float* scratch, int64_t scratch_floats,
+                       void* stream) {
   int rc = check_select_args(dtype, qs, k, B, Hq, Hk, Sk, D, qps, bk, group, causal, wo_init, J0,
                              nc, bsq);
   if (rc) return rc;
@@ -374,9 +366,6 @@ static int select_segments_impl(int dtype, const void* qs, int64_t sqb, int64_t 
   if (which == kSelExact)
     return fail(VA_ERR_UNSUPPORTED, "segmented selection needs the wave selection kernel, or "
                                     "the MFMA kernel with segments of whole 256-key chunks");
-  if (pcommon && which != kSelWave)
-    return fail(VA_ERR_UNSUPPORTED, "paired lists need the wave selection kernel (bf16/fp16, "
-                                    "D in {64,128}, k_local_size in {16,32,64})");
   const int64_t need = va_select_segments_scratch_floats(B, Hq, Hk, Sk, nc, segment_keys, bk, group);
   if (!scratch || scratch_floats < need)
     return fail(VA_ERR_ARG, "segmented selection needs %lld scratch floats", (long long)need);
@@ -394,36 +383,8 @@ static int select_segments_impl(int dtype, const void* qs, int64_t sqb, int64_t 
   rc = select_impl(dtype, qs, sqb, sqh, sqn, k, skb, skh, sks, B, Hq, Hk, Sk, D, qps, bk, group,
                    causal, wo_init, J0, nc, bsq, gap, gaps, dense_stride, counts, indices,
                    which, scratch, segment_keys, st, carry,
-                   two_pass ? va::kPassCarry : va::kPassPlain, pcommon);
+                   two_pass ? va::kPassCarry : va::kPassPlain);
   return rc ? rc : ok();
-}
-
-int va_select_segments(int dtype, const void* qs, int64_t sqb, int64_t sqh, int64_t sqn,
-                       const void* k, int64_t skb, int64_t skh, int64_t sks, int64_t B,
-                       int64_t Hq, int64_t Hk, int64_t Sk, int64_t D, int64_t qps, int64_t bk,
-                       int64_t group, int causal, int wo_init, int64_t J0, int64_t nc, int64_t bsq,
-                       float gap, const float* gaps, int64_t dense_stride, int64_t segment_keys,
-                       int32_t* counts, int32_t* indices, float* scratch, int64_t scratch_floats,
-                       void* stream) {
-  return select_segments_impl(dtype, qs, sqb, sqh, sqn, k, skb, skh, sks, B, Hq, Hk, Sk, D, qps,
-                              bk, group, causal, wo_init, J0, nc, bsq, gap, gaps, dense_stride,
-                              segment_keys, counts, indices, scratch, scratch_floats, nullptr,
-                              stream);
-}
-
-int va_select_segments_paired(int dtype, const void* qs, int64_t sqb, int64_t sqh, int64_t sqn,
-                              const void* k, int64_t skb, int64_t skh, int64_t sks, int64_t B,
-                              int64_t Hq, int64_t Hk, int64_t Sk, int64_t D, int64_t qps,
-                              int64_t bk, int64_t group, int causal, int wo_init, int64_t J0,
-                              int64_t nc, int64_t bsq, float gap, const float* gaps,
-                              int64_t dense_stride, int64_t segment_keys, int32_t* counts,
-                              int32_t* indices, int32_t* pair_common, float* scratch,
-                              int64_t scratch_floats, void* stream) {
-  if (!pair_common) return fail(VA_ERR_ARG, "null pair_common");
-  return select_segments_impl(dtype, qs, sqb, sqh, sqn, k, skb, skh, sks, B, Hq, Hk, Sk, D, qps,
-                              bk, group, causal, wo_init, J0, nc, bsq, gap, gaps, dense_stride,
-                              segment_keys, counts, indices, scratch, scratch_floats, pair_common,
-                              stream);
 }
 
 // Whether the MFMA attention kernel can run these operands: bf16/fp16, D in
@@ -463,22 +424,8 @@ static int attn_dispatch(int dtype, const void* q, const int64_t* sq, const void
                          int64_t Sk, int64_t D, int64_t qps, int causal,
                          const va::RowLayout& lay, const int32_t* counts,
                          const int32_t* indices, float softmax_scale, int kernel, int nseg,
-                         int64_t segk, hipStream_t stream, float* stats = nullptr,
-                         const int32_t* pcommon = nullptr) {
+                         int64_t segk, hipStream_t stream, float* stats = nullptr) {
   const float scale_log2 = softmax_scale * 1.4426950408889634f;
-  if (pcommon) {  // paired lists: the pair form of the MFMA kernel
-    const AttnMfmaCheck chk = attn_mfma_check(dtype, q, sq, k, sk, v, sv, out, so, Sk, D, qps);
-    if (stats || !va::attn_pair_supported(dtype, D, qps) || !chk.shape || !chk.align ||
-        !chk.span || !(softmax_scale > 0.f) || !counts ||
-        (kernel != VA_ATTN_AUTO && kernel != VA_ATTN_MFMA))
-      return fail(VA_ERR_UNSUPPORTED, "paired lists need the MFMA attention's pair form: "
-                                      "bf16/fp16, D = 128, qps = 64, 16-byte aligned rows, "
-                                      "K/V row strides < 16 KiB and a positive scale");
-    return hip_check(va::launch_attn_pair(dtype, q, sq, k, sk, v, sv, out, so, B, Hq, Hk, Sq, Sk,
-                                          causal, scale_log2, counts, pcommon, indices, lay,
-                                          nseg, int(segk), stream),
-                     "attention launch");
-  }
   // Row statistics read no V and write no output: only q and k are checked.
   const AttnMfmaCheck chk = stats ? attn_mfma_check(dtype, q, sq, k, sk, k, sk, q, sq, Sk, D, qps)
                                   : attn_mfma_check(dtype, q, sq, k, sk, v, sv, out, so, Sk, D, qps);
@@ -528,7 +475,7 @@ static int sparse_attn_impl(int dtype, const void* q, int64_t sqb, int64_t sqh, 
                             int wo_init, int64_t J0, int64_t nc, int64_t dense_stride,
                             const int32_t* counts, const int32_t* indices, float softmax_scale,
                             int kernel, int nseg, int64_t segk, void* stream,
-                            float* stats = nullptr, const int32_t* pcommon = nullptr) {
+                            float* stats = nullptr) {
   if (!dtype_ok(dtype)) return fail(VA_ERR_ARG, "unknown dtype %d", dtype);
   if (!q || !k || (!stats && (!v || !out))) return fail(VA_ERR_ARG, "null tensor pointer");
   if ((counts == nullptr) != (indices == nullptr))
@@ -543,10 +490,9 @@ static int sparse_attn_impl(int dtype, const void* q, int64_t sqb, int64_t sqh, 
   const int64_t sq[3] = {sqb, sqh, sqs}, sk[3] = {skb, skh, sks}, sv[3] = {svb, svh, svs},
                 so[3] = {sob, soh, sos};
   const va::RowLayout lay = make_layout(J0, nc, qps, Sk, causal, wo_init, dense_stride);
-  if (pcommon && (nc + 1) / 2 * B * Hq > kMaxGrid) return fail(VA_ERR_UNSUPPORTED, "grid too large");
   int rc = attn_dispatch(dtype, q, sq, k, sk, v, sv, out, so, B, Hq, Hk, Sq, Sk, D, qps, causal,
                          lay, counts, indices, softmax_scale, kernel, nseg, segk,
-                         static_cast<hipStream_t>(stream), stats, pcommon);
+                         static_cast<hipStream_t>(stream), stats);
   return rc ? rc : ok();
 }
 
@@ -669,27 +615,6 @@ int va_sparse_attn_segments(int dtype, const void* q, int64_t sqb, int64_t sqh, 
                           soh, sos, B, Hq, Hk, Sq, Sk, D, qps, causal, wo_init, J0, nc,
                           dense_stride, counts, indices, softmax_scale, VA_ATTN_MFMA,
                           int(cdiv(Sk, segment_keys)), segment_keys, stream);
-}
-
-int va_sparse_attn_segments_paired(int dtype, const void* q, int64_t sqb, int64_t sqh,
-                                   int64_t sqs, const void* k, int64_t skb, int64_t skh,
-                                   int64_t sks, const void* v, int64_t svb, int64_t svh,
-                                   int64_t svs, void* out, int64_t sob, int64_t soh, int64_t sos,
-                                   int64_t B, int64_t Hq, int64_t Hk, int64_t Sq, int64_t Sk,
-                                   int64_t D, int64_t qps, int causal, int wo_init, int64_t J0,
-                                   int64_t nc, int64_t dense_stride, int64_t segment_keys,
-                                   const int32_t* counts, const int32_t* indices,
-                                   const int32_t* pair_common, float softmax_scale,
-                                   void* stream) {
-  if (!counts || !indices || !pair_common) return fail(VA_ERR_ARG, "null counts / indices");
-  if (segment_keys <= 0 || segment_keys % 64 || cdiv(Sk, segment_keys) > kMaxSegments)
-    return fail(VA_ERR_ARG, "segment_keys %lld: need a positive multiple of 64, at most %lld "
-                            "segments", (long long)segment_keys, (long long)kMaxSegments);
-  return sparse_attn_impl(dtype, q, sqb, sqh, sqs, k, skb, skh, sks, v, svb, svh, svs, out, sob,
-                          soh, sos, B, Hq, Hk, Sq, Sk, D, qps, causal, wo_init, J0, nc,
-                          dense_stride, counts, indices, softmax_scale, VA_ATTN_MFMA,
-                          int(cdiv(Sk, segment_keys)), segment_keys, stream, nullptr,
-                          pair_common);
 }
 
 // Decode: the kv cache of each kv head is cut into nsplit ranges of `span`
@@ -831,18 +756,17 @@ static int64_t group_end(int64_t B, int64_t Hq, int64_t Sk, int64_t qps, int cau
 }
 
 // Workspace of va_prefill: [scaled pooled q][counts][indices][key norms]
-// [segment maxima][common counts of row pairs], 256-byte aligned.
+// [segment maxima], 256-byte aligned.
 static void prefill_segments(int dtype, int64_t B, int64_t Hq, int64_t Sq, int64_t Sk, int64_t D,
                              int64_t qps, int causal, int64_t chunk, int64_t bsq,
                              int64_t* qs_bytes, int64_t* cnt_bytes, int64_t* idx_bytes,
-                             int64_t* kn_bytes, int64_t* carry_bytes, int64_t* pc_bytes) {
+                             int64_t* kn_bytes, int64_t* carry_bytes = nullptr) {
   *kn_bytes = align256(va::key_norm_scratch_floats(B, Hq) * 4);  // Hk <= Hq
   const int64_t nqb = cdiv(Sq, qps);
   *qs_bytes = align256(B * Hq * nqb * D * esize(dtype));
   const int64_t nc_max = cdiv(chunk < Sq ? chunk : Sq, qps);
   *cnt_bytes = align256(B * Hq * nc_max * 4 * kMaxSegments);  // per-segment counts
-  *carry_bytes = align256(B * Hq * nc_max * va::kSegCarryBytes * kMaxSegments);
-  *pc_bytes = align256(B * Hq * cdiv(nc_max, 2) * 4 * kMaxSegments);
+  if (carry_bytes) *carry_bytes = align256(B * Hq * nc_max * va::kSegCarryBytes * kMaxSegments);
   int64_t idx_max = 0;
   const int64_t unit = group_unit(bsq);
   for (int64_t i = 0; i < Sq; i += chunk) {
@@ -864,9 +788,9 @@ int64_t va_prefill_workspace_size(int dtype, int64_t B, int64_t Hq, int64_t Sq, 
   if (!dtype_ok(dtype) || B <= 0 || Hq <= 0 || Sq <= 0 || Sk <= 0 || D <= 0 || qps <= 0 ||
       chunk_size <= 0 || chunk_size % qps || bsq <= 0)
     return -1;
-  int64_t a, b, c, d, e, f;
-  prefill_segments(dtype, B, Hq, Sq, Sk, D, qps, causal, chunk_size, bsq, &a, &b, &c, &d, &e, &f);
-  return a + b + c + d + e + f;
+  int64_t a, b, c, d, e;
+  prefill_segments(dtype, B, Hq, Sq, Sk, D, qps, causal, chunk_size, bsq, &a, &b, &c, &d, &e);
+  return a + b + c + d + e;
 }
 
 int va_prefill_kernels(int dtype, const void* q, int64_t sqb, int64_t sqh, int64_t sqs,
@@ -930,17 +854,15 @@ int va_prefill(int dtype, const void* q, int64_t sqb, int64_t sqh, int64_t sqs, 
     return fail(VA_ERR_WORKSPACE, "workspace %lld bytes < required %lld (bsq %lld)",
                 (long long)workspace_bytes, (long long)need, (long long)bsq);
   const int64_t nqb = cdiv(Sq, qps);
-  int64_t qs_bytes, cnt_bytes, idx_bytes, kn_bytes, carry_bytes, pc_bytes;
+  int64_t qs_bytes, cnt_bytes, idx_bytes, kn_bytes, carry_bytes;
   prefill_segments(dtype, B, Hq, Sq, Sk, D, qps, causal, chunk_size, bsq, &qs_bytes, &cnt_bytes,
-                   &idx_bytes, &kn_bytes, &carry_bytes, &pc_bytes);
+                   &idx_bytes, &kn_bytes, &carry_bytes);
   char* ws = static_cast<char*>(workspace);
   void* qs = ws;
   int32_t* counts = reinterpret_cast<int32_t*>(ws + qs_bytes);
   int32_t* indices = reinterpret_cast<int32_t*>(ws + qs_bytes + cnt_bytes);
   float* knorm = reinterpret_cast<float*>(ws + qs_bytes + cnt_bytes + idx_bytes);
   void* carry = ws + qs_bytes + cnt_bytes + idx_bytes + kn_bytes;
-  int32_t* pcommon =
-      reinterpret_cast<int32_t*>(ws + qs_bytes + cnt_bytes + idx_bytes + kn_bytes + carry_bytes);
   hipStream_t st = static_cast<hipStream_t>(stream);
 
   int rc = va_pool(dtype, q, B, Hq, Sq, D, sqb, sqh, sqs, qps, nullptr, qs, stream);
@@ -964,14 +886,11 @@ int va_prefill(int dtype, const void* q, int64_t sqb, int64_t sqh, int64_t sqs, 
   // start a group when the groups are short, otherwise (one group per row) a
   // maxima pass followed by a carry pass.
   int64_t segk = 0;
-  bool two_pass = false, paired = false;
+  bool two_pass = false;
   {
     const int64_t sq[3] = {sqb, sqh, sqs}, sk[3] = {skb, skh, sks}, sv[3] = {svb, svh, svs},
                   so[3] = {sob, soh, sos};
     const bool attn = attn_mfma_check(dtype, q, sq, k, sk, v, sv, out, so, Sk, D, qps).ok();
-    // Row pairs: the wave selection writes each pair's shared keys once and
-    // the attention's pair form gathers them once for both rows.
-    paired = which == kSelWave && attn && va::attn_pair_supported(dtype, D, qps);
     const int64_t g = effective_group(group, Sk, bk);
     if (which == kSelWave && attn) {
       segk = va::select_wave_segment_keys(Sk, bk, g);
@@ -1027,12 +946,11 @@ int va_prefill(int dtype, const void* q, int64_t sqb, int64_t sqh, int64_t sqs, 
       rc = select_impl(dtype, qs_chunk, Hq * nqb * D, nqb * D, D, k, skb, skh, sks, B, Hq, Hk,
                        Sk, D, qps, bk, group, causal, causal, J0, nc, bsq, gap, gaps, 0, counts,
                        indices, which, knorm, segk_g, st, carry,
-                       two_pass ? va::kPassCarry : va::kPassPlain, paired ? pcommon : nullptr);
+                       two_pass ? va::kPassCarry : va::kPassPlain);
       if (rc) return rc;
       rc = sparse_attn_impl(dtype, q, sqb, sqh, sqs, k, skb, skh, sks, v, svb, svh, svs, out, sob,
                             soh, sos, B, Hq, Hk, Sq, Sk, D, qps, causal, causal, J0, nc, 0, counts,
-                            indices, scale, VA_ATTN_AUTO, nseg, segk_g, st, nullptr,
-                            paired ? pcommon : nullptr);
+                            indices, scale, VA_ATTN_AUTO, nseg, segk_g, st);
       if (rc) return rc;
     }
   }

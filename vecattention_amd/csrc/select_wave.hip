@@ -38,17 +38,7 @@
 // rare path of the wave that needs it.
 //
 // Output.  Each lane writes its selected keys straight to the row's index
-// list (ascending: the low half's tile before the high half's).  Pair mode
-// (pcommon != null, the prefill's own lists): chunk rows 2i and 2i+1 of the
-// launch form a pair (A, B) whose lanes are adjacent, so one DPP lane swap
-// gives each lane its partner's decisions; within each key segment, row A's
-// slots receive the keys both rows selected (ascending from the segment's
-// first slot) and the keys only A selected (descending from the segment's
-// last slot), row B's slots the keys only B selected (ascending), and
-// pcommon[(bh * npairs + i) * nseg + seg] the number of common keys.  The
-// counts stay per row (|A| and |B|), so each row's list is still exactly
-// recoverable; the attention kernel's pair form gathers every common key once
-// for both rows.
+// list (ascending: the low half's tile before the high half's).
 #include "lanes.h"
 #include "mfma.h"
 
@@ -112,7 +102,7 @@ __global__ __launch_bounds__(256, 2) void select_wave_kernel(
     int64_t qps, uint32_t gspan, int causal, int64_t bsq, float gap_scalar,
     const float* __restrict__ gaps, const float* __restrict__ kmax, RowLayout lay,
     int32_t* __restrict__ counts, int32_t* __restrict__ indices, int64_t nrowsets, int segk,
-    int nseg, SegCarry* __restrict__ carry, int mode, int32_t* __restrict__ pcommon) {
+    int nseg, SegCarry* __restrict__ carry, int mode) {
   using M = Mfma<T>;
   using vec = typename M::vec;
   constexpr int NS = D / 16;                    // MFMA steps over the features
@@ -219,18 +209,6 @@ __global__ __launch_bounds__(256, 2) void select_wave_kernel(
   int32_t* const orow = indices + (valid ? lay.row_offset(bh, jr) + seg_slot : 0);
   const int cap = valid ? int(lay.capacity(J0 + jr)) - seg_slot : 0;
   int rowcnt = 0;   // keys selected so far for this row
-  // Pair mode: keys written so far to the common run (A rows) and to the
-  // row's own run (A: descending from a_end, the end of the segment's slots;
-  // B: ascending from the segment's first slot).
-  const bool pair = pcommon != nullptr;
-  const bool row_a = (l32 & 1) == 0;  // jr_wave is even: lane parity = row parity
-  int posc = 0, poso = 0;
-  int a_end = cap;
-  if (nseg > 1) {
-    const int nxt = seg_lo + segk;
-    const int nslot = (nxt > smin ? nxt : smin) - smin - seg_slot;
-    a_end = nslot < cap ? nslot : cap;
-  }
   int listcnt = 0;  // near-max tiles listed for this row
   float m = -__builtin_inff();  // MFMA running maximum of the row
 
@@ -299,39 +277,13 @@ __global__ __launch_bounds__(256, 2) void select_wave_kernel(
   auto append = [&](int kb0, int bb, uint32_t bt) {
     const int cnt = __builtin_popcount(bt);
     const int ocnt = int(other_half(uint32_t(cnt)));
+    int pos = rowcnt + (hh ? ocnt : 0);
     const int key0 = kb0 + 32 * bb + 16 * hh;
-    if (!pair) {
-      int pos = rowcnt + (hh ? ocnt : 0);
-      while (bt) {
-        const int e = __builtin_ctz(bt);
-        bt &= bt - 1;
-        if (pos < cap) orow[pos] = key0 + e;
-        ++pos;
-      }
-    } else {
-      // partner row's decisions on the same 16 keys (quad_perm [1,0,3,2])
-      const uint32_t pt = uint32_t(__builtin_amdgcn_mov_dpp(int(bt), 0xb1, 0xf, 0xf, false));
-      const uint32_t cm = row_a ? (bt & pt) : 0u;  // common keys, written by row A
-      const uint32_t own = bt & ~pt;
-      const int nc_ = __builtin_popcount(cm), no_ = __builtin_popcount(own);
-      const uint32_t oth = other_half(uint32_t(nc_) | (uint32_t(no_) << 16));
-      int pc = posc + (hh ? int(oth & 0xffffu) : 0);
-      int po = poso + (hh ? int(oth >> 16) : 0);
-      uint32_t w = cm | own;
-      while (w) {
-        const int e = __builtin_ctz(w);
-        w &= w - 1;
-        int slot;
-        if ((cm >> e) & 1u) {
-          slot = pc++;
-        } else {
-          slot = row_a ? a_end - 1 - po : po;
-          ++po;
-        }
-        if (slot >= 0 && slot < a_end) orow[slot] = key0 + e;
-      }
-      posc += nc_ + int(oth & 0xffffu);
-      poso += no_ + int(oth >> 16);
+    while (bt) {
+      const int e = __builtin_ctz(bt);
+      bt &= bt - 1;
+      if (pos < cap) orow[pos] = key0 + e;
+      ++pos;
     }
     rowcnt += cnt + ocnt;
   };
@@ -699,8 +651,6 @@ __global__ __launch_bounds__(256, 2) void select_wave_kernel(
   }
 
   if (valid && hh == 0) counts[(bh * nc + jr) * nseg + seg] = rowcnt < cap ? rowcnt : (cap > 0 ? cap : 0);
-  if (pair && valid && hh == 0 && row_a)
-    pcommon[(bh * ((nc + 1) / 2) + jr / 2) * nseg + seg] = posc < a_end ? posc : (a_end > 0 ? a_end : 0);
 }
 
 // Segment length the splits aim for: Sk / 16 keys, within [2048, 4096].  Short
@@ -754,7 +704,7 @@ static hipError_t launch_select_wave_tdb(const void* qs, int64_t sqb, int64_t sq
                                          float gap, const float* gaps, const float* kmax,
                                          const RowLayout& lay, int32_t* counts, int32_t* indices,
                                          int64_t segk, SegCarry* carry, int mode,
-                                         int32_t* pcommon, hipStream_t stream) {
+                                         hipStream_t stream) {
   const int64_t nrowsets = (lay.nc + kWWaves * kWRows - 1) / (kWWaves * kWRows);
   const int64_t nseg = segk > 0 ? (Sk + segk - 1) / segk : 1;
   // Group span in keys, capped at 2^31 (key offsets are below 2^24, so a span
@@ -765,7 +715,7 @@ static hipError_t launch_select_wave_tdb(const void* qs, int64_t sqb, int64_t sq
                      stream, static_cast<const T*>(qs), sqb, sqh, sqn, static_cast<const T*>(k),
                      skb, skh, sks, B, Hq, Hk, Sk, qps, uint32_t(gs), causal, bsq, gap, gaps, kmax,
                      lay, counts, indices, nrowsets, int(segk > 0 ? segk : 0), int(nseg), carry,
-                     mode, pcommon);
+                     mode);
   return hipGetLastError();
 }
 
@@ -777,12 +727,12 @@ static hipError_t launch_select_wave_td(int64_t bk, const void* qs, int64_t sqb,
                                         float gap, const float* gaps, const float* kmax,
                                         const RowLayout& lay, int32_t* counts, int32_t* indices,
                                         int64_t segk, SegCarry* carry, int mode,
-                                        int32_t* pcommon, hipStream_t stream) {
+                                        hipStream_t stream) {
 #define VA_SELW_BK(BB)                                                                          \
   if (bk == BB)                                                                                 \
     return launch_select_wave_tdb<T, D, BB>(qs, sqb, sqh, sqn, k, skb, skh, sks, B, Hq, Hk, Sk, \
                                             qps, group, causal, bsq, gap, gaps, kmax, lay,      \
-                                            counts, indices, segk, carry, mode, pcommon, stream);
+                                            counts, indices, segk, carry, mode, stream);
   VA_SELW_BK(16)
   VA_SELW_BK(32)
   VA_SELW_BK(64)
@@ -796,12 +746,11 @@ hipError_t launch_select_wave(int dtype, const void* qs, int64_t sqb, int64_t sq
                               int64_t bk, int64_t group, int causal, int64_t bsq, float gap,
                               const float* gaps, const float* kmax, const RowLayout& lay,
                               int32_t* counts, int32_t* indices, int64_t segk, void* carry,
-                              int mode, int32_t* pcommon, hipStream_t stream) {
+                              int mode, hipStream_t stream) {
 #define VA_SELW_CASE(TT, DD)                                                                 \
   return launch_select_wave_td<TT, DD>(bk, qs, sqb, sqh, sqn, k, skb, skh, sks, B, Hq, Hk, \
                                        Sk, qps, group, causal, bsq, gap, gaps, kmax, lay,    \
-                                       counts, indices, segk, static_cast<SegCarry*>(carry), mode, \
-                                       pcommon, stream);
+                                       counts, indices, segk, static_cast<SegCarry*>(carry), mode, stream);
   if (dtype == kBF16 && D == 128) { VA_SELW_CASE(bf16_t, 128) }
   if (dtype == kBF16 && D == 64) { VA_SELW_CASE(bf16_t, 64) }
   if (dtype == kF16 && D == 128) { VA_SELW_CASE(f16_t, 128) }

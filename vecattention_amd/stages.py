@@ -109,15 +109,13 @@ def segment_keys(Sk, k_local_size, group_k_block):
 
 def select_segments(qs_chunk, k, J0, gap, gaps, causal, q_pooling_size, k_local_size,
                     group_k_block, wo_init, segk, bsq=None, dense_stride=0, indices=None,
-                    scratch=None, paired=False):
+                    scratch=None):
     """Split TilingSelect (the form VecAttention_prefill runs): keys cut into
     segments of `segk` keys selected in parallel.  Returns (counts
     (B, Hq, nc, nseg) int32, indices int32): segment s of a row writes from slot
     max(s*segk, smin) - smin of the row in the index layout.  `indices` and
     `scratch` may be passed in (int32 / fp32 device buffers at least as large as
     the index layout and va_select_segments_scratch_floats) to reuse them.
-    paired=True: the lists of chunk-row pairs (va_select_segments_paired), and
-    a third result, pair_common (B, Hq, ceil(nc/2), nseg) int32.
     """
     if qs_chunk.stride(-1) != 1:
         qs_chunk = qs_chunk.contiguous()
@@ -144,17 +142,6 @@ def select_segments(qs_chunk, k, J0, gap, gaps, causal, q_pooling_size, k_local_
         raise AssertionError(f"scratch: need {nscr} fp32 slots")
     else:
         nscr = scratch.numel()
-    if paired:
-        pair_common = torch.empty(B, Hq, (nc + 1) // 2, nseg, dtype=torch.int32, device=k.device)
-        with torch.cuda.device(k.device):
-            rc = nat.lib().va_select_segments_paired(
-                nat.dtype_code(k), nat.ptr(qs_chunk), qs_chunk.stride(0), qs_chunk.stride(1),
-                qs_chunk.stride(2), nat.ptr(k), k.stride(0), k.stride(1), k.stride(2), B, Hq, Hk,
-                Sk, D, q_pooling_size, k_local_size, group_k_block, int(causal), int(wo_init), J0,
-                nc, bsq, float(gap), nat.ptr(gaps), dense_stride, segk, nat.ptr(counts),
-                nat.ptr(indices), nat.ptr(pair_common), nat.ptr(scratch), nscr, _stream(k))
-        nat.check("va_select_segments_paired", rc)
-        return counts, indices, pair_common
     with torch.cuda.device(k.device):
         rc = nat.lib().va_select_segments(
             nat.dtype_code(k), nat.ptr(qs_chunk), qs_chunk.stride(0), qs_chunk.stride(1),
@@ -167,12 +154,9 @@ def select_segments(qs_chunk, k, J0, gap, gaps, causal, q_pooling_size, k_local_
 
 
 def sparse_attention(q, k, v, out, J0, nc, counts, indices, causal, q_pooling_size, wo_init=None,
-                     dense_stride=0, softmax_scale=None, kernel=nat.VA_ATTN_AUTO, segk=0,
-                     pair_common=None):
+                     dense_stride=0, softmax_scale=None, kernel=nat.VA_ATTN_AUTO, segk=0):
     """Vector-sparse attention of q-block rows [J0, J0+nc) into `out` (B, Hq, Sq, D).
-    With segk > 0, (counts, indices) are the segmented lists of select_segments;
-    with pair_common as well, its paired lists (select_segments(paired=True)),
-    run by the pair form of the MFMA kernel."""
+    With segk > 0, (counts, indices) are the segmented lists of select_segments."""
     q = q if q.stride(-1) == 1 else q.contiguous()
     k = k if k.stride(-1) == 1 else k.contiguous()
     v = v if v.stride(-1) == 1 else v.contiguous()
@@ -182,17 +166,6 @@ def sparse_attention(q, k, v, out, J0, nc, counts, indices, causal, q_pooling_si
         wo_init = causal
     if softmax_scale is None:
         softmax_scale = 1.0 / math.sqrt(D)
-    if segk and pair_common is not None:
-        with torch.cuda.device(q.device):
-            rc = nat.lib().va_sparse_attn_segments_paired(
-                nat.dtype_code(q), nat.ptr(q), q.stride(0), q.stride(1), q.stride(2), nat.ptr(k),
-                k.stride(0), k.stride(1), k.stride(2), nat.ptr(v), v.stride(0), v.stride(1),
-                v.stride(2), nat.ptr(out), out.stride(0), out.stride(1), out.stride(2), B, Hq, Hk,
-                Sq, Sk, D, q_pooling_size, int(causal), int(wo_init), J0, nc, dense_stride, segk,
-                nat.ptr(counts), nat.ptr(indices), nat.ptr(pair_common), float(softmax_scale),
-                _stream(q))
-        nat.check("va_sparse_attn_segments_paired", rc)
-        return out
     if segk:
         with torch.cuda.device(q.device):
             rc = nat.lib().va_sparse_attn_segments(
