@@ -35,6 +35,8 @@ import torch  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
+FP32_PEAK_TFLOPS = 157.3  # MI355X vector fp32 (the fp32 workload's per-row attention kernel)
+FP64_PEAK_TFLOPS = 78.6   # MI355X fp64 (the exact selection kernel)
 METRIC = "prefill attn latency (ms) + effective TFLOPS at 32k/128k; speedup vs dense"
 
 
@@ -46,8 +48,8 @@ def parse():
     ap.add_argument("--config", default="C", help="workload key A..E")
     ap.add_argument("--extra", default=None,
                     help="comma-separated workload keys measured after the headline and "
-                         "reported under extra_workloads (default: B when the headline is C; "
-                         "'none' for none)")
+                         "reported under extra_workloads (default: B,D,E,A when the headline "
+                         "is C; 'none' for none)")
     ap.add_argument("--no-dense", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
@@ -202,12 +204,25 @@ def profiled_traffic(workload, kernel):
 
 # ------------------------------------------------------------------- stages --
 
+def prefill_plan(wl, q, k, v, out):
+    """va_prefill_kernels' bit set for these tensors: the kernels the prefill runs."""
+    from vecattention_amd import _native as nat
+    return nat.check_flags("va_prefill_kernels", nat.lib().va_prefill_kernels(
+        nat.dtype_code(q), nat.ptr(q), q.stride(0), q.stride(1), q.stride(2), nat.ptr(k),
+        k.stride(0), k.stride(1), k.stride(2), nat.ptr(v), v.stride(0), v.stride(1), v.stride(2),
+        nat.ptr(out), out.stride(0), out.stride(1), out.stride(2), q.shape[1], k.shape[1],
+        k.shape[2], q.shape[3], wl.q_pooling_size, wl.k_local_size, wl.group_k_block))
+
+
 def run_stages(wl, q, k, v, gap, out, events=None):
     """Pool + per-chunk select/attention through the stage API (same kernels
     as VecAttention_prefill).  Returns per-chunk counts; records events."""
+    from vecattention_amd import _native as nat
     from vecattention_amd import stages
     qps, S = wl.q_pooling_size, q.shape[2]
-    segk = stages.segment_keys(k.shape[2], wl.k_local_size, wl.group_k_block)  # as the prefill
+    # the key segments the prefill uses, when its plan splits the selection
+    split = prefill_plan(wl, q, k, v, out) & nat.VA_KERNELS_SPLIT
+    segk = stages.segment_keys(k.shape[2], wl.k_local_size, wl.group_k_block) if split else 0
     ev = events
     if ev is not None:
         ev["p0"].record()
@@ -412,6 +427,34 @@ def cpu_baseline(wl, q_cpu, k_cpu, v_cpu, threshold, seconds, workers=None):
             "attention_s_per_qblock": round(t_attn / max(blocks, 1), 5),
             "host_cpu": host_cpu_model(),
             "host_threads_available": len(os.sched_getaffinity(0))}
+
+
+def cpu_full_run(wl, q_cpu, k_cpu, v_cpu, threshold, F_attn, reps=3):
+    """The whole prefill on the CPU oracle (oracle.prefill: C selection, numpy
+    attention) in fp32 arithmetic for the attention, on the host cores of this
+    box: 1 warmup + `reps` timed runs, median.  The C selection is single
+    threaded; numpy's BLAS uses the threads its environment allows."""
+    import numpy as np
+
+    from oracle import oracle as orc
+    dt = {torch.bfloat16: "bfloat16", torch.float16: "float16", torch.float32: "float32"}[wl.dtype]
+    run = lambda: orc.prefill(q_cpu, k_cpu, v_cpu, threshold, wl.q_pooling_size,
+                              wl.k_local_size, wl.group_k_block, wl.causal, wl.chunk_size, 64, dt,
+                              acc=np.float32)
+    run()
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    return {"ms": round(med * 1e3, 2), "value": F_attn / med / 1e12, "unit": "TFLOP/s",
+            "reps": reps, "warmup": 1, "kind": "port",
+            "threads": {"blas": os.environ.get("OMP_NUM_THREADS", "unset"), "selection": 1},
+            "host_cpu": host_cpu_model(),
+            "host_threads_available": len(os.sched_getaffinity(0)),
+            "sample": f"whole workload {wl.name}: oracle.prefill (fp32 attention), median of "
+                      f"{reps} runs after 1 warmup"}
 
 
 # -------------------------------------------------------------------- tuner --
@@ -662,13 +705,28 @@ def measure_prefill(args, wl, dev, with_cpu):
     # value: the whole VecAttention_prefill step, as timed above
     e2e_tflops = F_attn / (ms_per_step * 1e-3) / 1e12
     attn_tflops = F_attn / (t_attn * 1e-3) / 1e12
+    from vecattention_amd import _native as nat
+    plan = prefill_plan(wl, q, k, v, out)
+    attn_mfma = bool(plan & nat.VA_KERNELS_ATTN_MFMA)
+    attn_kernel = "attn_mfma_kernel" if attn_mfma else "attn_simple_kernel"
+    attn_peak = BF16_PEAK_TFLOPS if attn_mfma else FP32_PEAK_TFLOPS
+    # Selection (pooling + TilingSelect) against max(Bytes_sel / HBM peak,
+    # F_sel / the scoring kernel's peak): F_sel = 2*D per selectable (row, key).
+    F_sel = 2.0 * wl.D * selectable(wl, S)
+    sel_peak = FP64_PEAK_TFLOPS if plan & nat.VA_KERNELS_SELECT_EXACT else BF16_PEAK_TFLOPS
+    t_bytes = sel_bytes / (HBM_PEAK_GBS * 1e9) * 1e3
+    t_flops = F_sel / (sel_peak * 1e12) * 1e3
+    sel_roof = {"bound": "hbm" if t_bytes >= t_flops else "mfma" if sel_peak == BF16_PEAK_TFLOPS
+                else "fp64", "bytes": sel_bytes, "flops": F_sel,
+                "t_bound_ms": round(max(t_bytes, t_flops), 4), "t_ms": round(t_sel_total, 4),
+                "frac": round(max(t_bytes, t_flops) / t_sel_total, 4)}
     traffic, compulsory = profiled_traffic(wl.name, "attn_mfma_kernel")
     # The attention's K/V gathers against the copy instruction's own rate: K and
     # V rows of every (q-block, key) pair, F_attn * elem / (2 * qps) bytes.
     es = q.element_size()
     gathered = F_attn * es / (2 * wl.q_pooling_size)
     gather_rate = gathered / (t_attn * 1e-3) / 1e12
-    ceil = gather_ceiling(dev)
+    ceil = gather_ceiling(dev) if attn_mfma else {"l2": float("nan"), "fabric": float("nan")}
     rec = profiled_record(wl.name, "attn_mfma_kernel")
     l2_share = None if rec is None or "fabric_over_gathered" not in rec else \
         max(0.0, 1.0 - rec["fabric_over_gathered"])
@@ -700,22 +758,22 @@ def measure_prefill(args, wl, dev, with_cpu):
         "sparse_attn_tflops": round(attn_tflops, 3),
         "selection_gbs": round(sel_bytes / (t_sel_total * 1e-3) / 1e9, 1),
         "selection_hbm_frac": round(sel_bytes / (t_sel_total * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "selection_roofline": sel_roof,
         "dense_ms": None if dense_ms is None else round(dense_ms, 4),
         "dense_backend": dense_backend,
         "speedup_vs_dense": None if dense_ms is None else round(dense_ms / ms_per_step, 3),
         "dense_va_ms": None if dense_va_ms is None else round(dense_va_ms, 4),
         "dense_va_tflops": None if dense_va_ms is None else round(F_dense / (dense_va_ms * 1e-3) / 1e12, 1),
         "speedup_vs_dense_va": None if dense_va_ms is None else round(dense_va_ms / ms_per_step, 3),
-        "dense_equiv_tflops": round(F_dense / (ms_per_step * 1e-3) / 1e12, 3),
-        "roofline": {"bound": "mfma", "kernel": "attn_mfma_kernel",
-                     "achieved": round(attn_tflops, 3), "peak": BF16_PEAK_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(attn_tflops / BF16_PEAK_TFLOPS, 4),
+        "roofline": {"bound": "mfma" if attn_mfma else "valu-fp32", "kernel": attn_kernel,
+                     "achieved": round(attn_tflops, 3), "peak": attn_peak,
+                     "unit": "TFLOP/s", "frac": round(attn_tflops / attn_peak, 4),
                      "traffic": traffic,
                      "traffic_kind": "L2<->fabric bytes per launch (exact, from the TCC_EA0 "
                                      "request-size counters; Infinity Cache hits included)",
                      "traffic_over_compulsory": (round(traffic / compulsory, 2)
                                                  if traffic and compulsory else None),
-                     "gather": {
+                     "gather": None if not attn_mfma else {
                          "achieved_TBps": round(gather_rate, 3),
                          "ceiling_l2_TBps": round(ceil["l2"], 3),
                          "ceiling_fabric_TBps": round(ceil["fabric"], 3),
@@ -729,14 +787,19 @@ def measure_prefill(args, wl, dev, with_cpu):
     if with_cpu:
         result["cpu_baseline"] = cpu_baseline(wl, q_cpu, k_cpu, v_cpu, th, args.cpu_seconds,
                                               args.cpu_workers)
+    if wl.dtype == torch.float32 and not args.no_cpu:
+        # the workload small enough for the whole CPU path (the fp32 CPU
+        # reference configuration): 1 warmup + 3 reps, median
+        result["cpu_full"] = cpu_full_run(wl, q_cpu, k_cpu, v_cpu, th, F_attn)
     del q, k, v, out
     torch.cuda.empty_cache()
     return result
 
 
 EXTRA_KEYS = ("ms_per_step", "value", "config", "latency_ms", "sparse_attn_tflops", "selection_gbs",
-              "selection_hbm_frac", "dense_ms", "dense_backend", "speedup_vs_dense", "dense_va_ms",
-              "dense_va_tflops", "speedup_vs_dense_va", "roofline", "flops")
+              "selection_hbm_frac", "selection_roofline", "dense_ms", "dense_backend",
+              "speedup_vs_dense", "dense_va_ms", "dense_va_tflops", "speedup_vs_dense_va",
+              "roofline", "flops", "cpu_full")
 
 
 def main():
@@ -756,7 +819,7 @@ def main():
     if args.decode:
         bench_decode(args, wl, dev)
         return
-    extra = args.extra if args.extra is not None else ("B" if args.config == "C" else "none")
+    extra = args.extra if args.extra is not None else ("B,D,E,A" if args.config == "C" else "none")
     extra = [] if extra.lower() == "none" else [x for x in extra.split(",") if x]
     result = measure_prefill(args, wl, dev, with_cpu=not args.no_cpu)
     if extra:
@@ -765,7 +828,8 @@ def main():
         result["extra_workloads"] = {}
         for key in extra:
             r = measure_prefill(args, WORKLOADS[key], dev, with_cpu=False)
-            result["extra_workloads"][r["config"]["workload"]] = {k: r[k] for k in EXTRA_KEYS}
+            result["extra_workloads"][r["config"]["workload"]] = {k: r[k] for k in EXTRA_KEYS
+                                                                  if k in r}
         args.threshold = saved_th
     line = json.dumps(result)
     print(line, flush=True)

@@ -118,6 +118,13 @@ def check(fn, code):
     return code
 
 
+def check_flags(fn, flags):
+    """A bit-set result (va_prefill_kernels): raise on a negative error code."""
+    if flags < 0:
+        check(fn, flags)
+    return flags
+
+
 def dtype_code(t):
     try:
         return _DTYPES[t.dtype]

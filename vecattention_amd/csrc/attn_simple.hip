@@ -1,4 +1,4 @@
-// Vector-sparse attention, one thread per query row (any element type).
+// Vector-sparse attention, four lanes per query row (any element type).
 //
 // Semantics of the reference call vllm_flash_attn.sparse_attn_func at
 // spattn/src/VecAttention.py:110-121 as restated by the dense-mask code of
@@ -8,8 +8,13 @@
 // no key gets 0.
 //
 // This kernel serves fp32 inputs (which the MFMA kernel does not take) and is
-// an independent GPU cross-check of the MFMA kernel.  Every key row is read
-// by all threads of the work-group at once, so loads broadcast through L1.
+// an independent GPU cross-check of the MFMA kernel.  Four lanes (a quad)
+// serve one query row, lane j holding features [j*DQ, (j+1)*DQ) of the row and
+// of its output accumulator in registers (DQ = ceil(D/4) rounded up to 16, 32
+// or 64): each score is the quad's four partial dot products added with two
+// lane swaps, so the four lanes hold the same score and run the same online
+// softmax.  A work-group covers 64 rows of a q-block; every key row is read by
+// all quads of the work-group at once, so loads broadcast through L1.
 //
 // dense_qoff >= 0: every key instead (KeyList::dense, causal rows aligned at
 // offset dense_qoff).  stats != nullptr: no V; row i of head bh writes
@@ -21,9 +26,21 @@
 namespace va {
 
 constexpr int kSimpleMaxD = 256;
+constexpr int kSimpleRows = 64;  // query rows per work-group (4 lanes each)
 
-template <typename T>
-__global__ __launch_bounds__(128) void attn_simple_kernel(
+// x summed over the four lanes of each quad (the same value in all four).
+__device__ inline float quad_sum(float x) {
+  const float a = x + __builtin_bit_cast(
+                          float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0xb1, 0xf,
+                                                          0xf, false));  // quad_perm [1,0,3,2]
+  return a + __builtin_bit_cast(
+                 float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, a), 0x4e, 0xf, 0xf,
+                                                 false));  // quad_perm [2,3,0,1]
+}
+
+// kFull: D == 4 * DQ (every lane's features exist; no per-feature guards).
+template <typename T, int DQ, bool kFull>
+__global__ __launch_bounds__(4 * kSimpleRows) void attn_simple_kernel(
     const T* __restrict__ q, int64_t sqb, int64_t sqh, int64_t sqs,
     const T* __restrict__ k, int64_t skb, int64_t skh, int64_t sks,
     const T* __restrict__ v, int64_t svb, int64_t svh, int64_t svs,
@@ -33,13 +50,19 @@ __global__ __launch_bounds__(128) void attn_simple_kernel(
     const int32_t* __restrict__ indices, RowLayout lay, int64_t dense_qoff,
     float* __restrict__ stats) {
   const int64_t BH = B * Hq;
-  const int64_t jr = lay.nc - 1 - int64_t(blockIdx.x) / BH;
-  const int64_t bh = int64_t(blockIdx.x) % BH;
+  const int64_t parts = (qps + kSimpleRows - 1) / kSimpleRows;  // work-groups per q-block
+  const int64_t item = int64_t(blockIdx.x) / parts, part = int64_t(blockIdx.x) % parts;
+  const int64_t jr = lay.nc - 1 - item / BH;
+  const int64_t bh = item % BH;
   const int64_t b = bh / Hq, h = bh % Hq, hk = h / (Hq / Hk);
   const int64_t J = lay.J0 + jr;
-  const int64_t row = threadIdx.x;
+  const int64_t row = part * kSimpleRows + threadIdx.x / 4;
+  const int qlane = threadIdx.x % 4;
   const int64_t qpos = J * qps + row;
-  if (row >= qps || qpos >= Sq) return;
+  // Rows past the q-block or past Sq compute row 0 of the block (whole quads,
+  // so that the lane swaps see live lanes) and write nothing.
+  const bool live = row < qps && qpos < Sq;
+  const int64_t qrow = live ? qpos : J * qps;
 
   int64_t cnt = counts ? counts[bh * lay.nc + jr] : 0;
   const int64_t cap = lay.capacity(J);
@@ -47,43 +70,51 @@ __global__ __launch_bounds__(128) void attn_simple_kernel(
   const int32_t* cols = indices ? indices + lay.row_offset(bh, jr) : nullptr;
   const KeyList kl = dense_qoff >= 0 ? KeyList::dense(J, qps, Sk, causal, dense_qoff)
                                      : KeyList::make(J, qps, Sk, causal, cnt, cols);
-  const int64_t qkey = qpos + (dense_qoff > 0 ? dense_qoff : 0);  // last visible diagonal key
+  const int64_t qkey = qrow + (dense_qoff > 0 ? dense_qoff : 0);  // last visible diagonal key
 
-  float qv[kSimpleMaxD];
-  float acc[kSimpleMaxD];
-  const T* qr = q + b * sqb + h * sqh + qpos * sqs;
-  for (int64_t d = 0; d < D; ++d) {
-    qv[d] = to_f32(qr[d]);
-    acc[d] = 0.f;
+  // this lane's features: d0 + i for i < DQ with d0 + i < D
+  const int64_t d0 = int64_t(qlane) * DQ;
+  float qv[DQ], acc[DQ];
+  const T* qr = q + b * sqb + h * sqh + qrow * sqs;
+#pragma unroll
+  for (int i = 0; i < DQ; ++i) {
+    qv[i] = (kFull || d0 + i < D) ? to_f32(qr[d0 + i]) : 0.f;
+    acc[i] = 0.f;
   }
   const T* kh = k + b * skb + hk * skh;
   const T* vh = v + b * svb + hk * svh;
   float m = -__builtin_inff(), l = 0.f;
   const int64_t n = kl.total();
   for (int64_t p = 0; p < n; ++p) {
-    const int64_t key = kl.key(p);
+    const int64_t key = kl.key(p);  // the same key in every lane of the work-group
     if (key < 0 || key >= Sk) continue;  // never read outside K / V
-    if (causal && kl.is_diag(p) && key > qkey) continue;
-    const T* kr = kh + key * sks;
+    const T* kr = kh + key * sks + d0;
     float s = 0.f;
-    for (int64_t d = 0; d < D; ++d) s += qv[d] * to_f32(kr[d]);
-    s *= scale_log2;
+#pragma unroll
+    for (int i = 0; i < DQ; ++i) s += (kFull || d0 + i < D) ? qv[i] * to_f32(kr[i]) : 0.f;
+    s = quad_sum(s) * scale_log2;
+    if (causal && kl.is_diag(p) && key > qkey) continue;  // (after the swaps: whole quads)
     const float m_new = __builtin_fmaxf(m, s);
     const float alpha = __builtin_amdgcn_exp2f(m - m_new);
     const float pe = __builtin_amdgcn_exp2f(s - m_new);
     l = l * alpha + pe;
     m = m_new;
     if (stats) continue;
-    const T* vr = vh + key * svs;
-    for (int64_t d = 0; d < D; ++d) acc[d] = acc[d] * alpha + pe * to_f32(vr[d]);
+    const T* vr = vh + key * svs + d0;
+#pragma unroll
+    for (int i = 0; i < DQ; ++i)
+      if (kFull || d0 + i < D) acc[i] = acc[i] * alpha + pe * to_f32(vr[i]);
   }
+  if (!live) return;
   if (stats) {
-    *reinterpret_cast<float2*>(stats + (bh * Sq + qpos) * 2) = make_float2(m, l);
+    if (qlane == 0) *reinterpret_cast<float2*>(stats + (bh * Sq + qpos) * 2) = make_float2(m, l);
     return;
   }
   const float inv = l > 0.f ? 1.f / l : 0.f;
-  T* orow = out + b * sob + h * soh + qpos * sos;
-  for (int64_t d = 0; d < D; ++d) orow[d] = Round<T>::store(acc[d] * inv);
+  T* orow = out + b * sob + h * soh + qpos * sos + d0;
+#pragma unroll
+  for (int i = 0; i < DQ; ++i)
+    if (kFull || d0 + i < D) orow[i] = Round<T>::store(acc[i] * inv);
 }
 
 template <typename T>
@@ -95,13 +126,22 @@ static hipError_t launch_attn_simple_t(const void* q, const int64_t* sq, const v
                                        const int32_t* counts, const int32_t* indices,
                                        const RowLayout& lay, int64_t dense_qoff, float* stats,
                                        hipStream_t stream) {
-  const int64_t nblocks = lay.nc * B * Hq;
-  hipLaunchKernelGGL((attn_simple_kernel<T>), dim3(unsigned(nblocks)), dim3(unsigned(qps)), 0,
-                     stream, static_cast<const T*>(q), sq[0], sq[1], sq[2],
-                     static_cast<const T*>(k), sk[0], sk[1], sk[2], static_cast<const T*>(v),
-                     sv[0], sv[1], sv[2], static_cast<T*>(out), so[0], so[1], so[2], B, Hq, Hk,
-                     Sq, Sk, D, qps, causal, scale_log2, counts, indices, lay, dense_qoff, stats);
-  return hipGetLastError();
+  const int64_t parts = (qps + kSimpleRows - 1) / kSimpleRows;
+  const int64_t nblocks = lay.nc * B * Hq * parts;
+  auto go = [&](auto kernel) {
+    hipLaunchKernelGGL(kernel, dim3(unsigned(nblocks)), dim3(4 * kSimpleRows), 0, stream,
+                       static_cast<const T*>(q), sq[0], sq[1], sq[2], static_cast<const T*>(k),
+                       sk[0], sk[1], sk[2], static_cast<const T*>(v), sv[0], sv[1], sv[2],
+                       static_cast<T*>(out), so[0], so[1], so[2], B, Hq, Hk, Sq, Sk, D, qps,
+                       causal, scale_log2, counts, indices, lay, dense_qoff, stats);
+    return hipGetLastError();
+  };
+  if (D == 64) return go(attn_simple_kernel<T, 16, true>);
+  if (D == 128) return go(attn_simple_kernel<T, 32, true>);
+  if (D < 64) return go(attn_simple_kernel<T, 16, false>);
+  if (D < 128) return go(attn_simple_kernel<T, 32, false>);
+  if (D <= kSimpleMaxD) return go(attn_simple_kernel<T, 64, false>);
+  return hipErrorInvalidValue;
 }
 
 hipError_t launch_attn_simple(int dtype, const void* q, const int64_t* sq, const void* k,
