@@ -26,7 +26,7 @@ import pytest
 import torch
 
 from oracle import oracle as orc
-from seglists import calibrate_threshold, pooled_oracle, select_chunk
+from seglists import calibrate_threshold, check_rows, pooled_oracle, select_chunk
 from vecattention_amd import VecAttention_prefill
 from vecattention_amd import _native as nat
 from vecattention_amd import stages
@@ -44,42 +44,6 @@ def note(*a):
 
 def segment_totals(counts):
     return counts.sum(dim=-1)
-
-
-def check_rows(q, k, v, qs_dev, kd, out_cpu, heads, rows, th, causal, G, chunk_rows=512,
-               qps=64, bk=16, rep=1):
-    """For each sampled (head, q-block J): the split selection's list equals
-    the oracle's, and the prefill output rows are within tolerance."""
-    S, Sk = q.shape[2], k.shape[2]
-    nqb = -(-S // qps)
-    gap = -math.log(th + 1e-9)
-    gaps = orc.gap_from_threshold(th, 1, 1)
-    bc, bi = orc.local_blocks(1, 1, S, qps, causal)
-    by_chunk = {}
-    for J in rows:
-        by_chunk.setdefault(J // chunk_rows * chunk_rows, []).append(J)
-    for J0, Js in sorted(by_chunk.items()):
-        nc = min(chunk_rows, nqb - J0)
-        gpu = select_chunk(qs_dev, kd, J0, nc, gap, causal, qps, bk, G)
-        for h in heads:
-            hk = h // rep
-            qh, kh, vh = q[:, h:h + 1], k[:, hk:hk + 1], v[:, hk:hk + 1]
-            qs = pooled_oracle(qh, qps)
-            for J in Js:
-                _, lists = orc.select(qs, kh, J0, nc, gaps, qps, bk, G, causal, causal, 64,
-                                      rows=(J - J0, J - J0 + 1))
-                want_list = lists[0][0][J - J0]
-                got_list = gpu.row(0, h, J - J0)
-                if not np.array_equal(got_list, want_list):
-                    diff = sorted(set(got_list.tolist()) ^ set(want_list.tolist()))[:10]
-                    raise AssertionError(f"h={h} J={J}: {len(got_list)} vs {len(want_list)} "
-                                         f"keys, differ at {diff}")
-                if out_cpu is not None:
-                    want = orc.attention(qh, kh, vh, qps, causal, bc, bi, [[[want_list]]], J0=J,
-                                         nc=1)
-                    r0, r1 = J * qps, min(S, (J + 1) * qps)
-                    err = np.abs(out_cpu[0, h, r0:r1] - want[0, 0])
-                    assert err.max() <= ATOL_MAX and err.mean() <= ATOL_MEAN, (h, J, err.max())
 
 
 def check_every_row(q, k, qs_dev, kd, J0, nc, th, causal, G, heads, rep=1, qps=64, bk=16):
