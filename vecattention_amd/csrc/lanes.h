@@ -95,6 +95,13 @@ __device__ inline float max_halves(float x) {
   asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"((uint32_t)p[0]), "v"((uint32_t)p[1]));
   return r;
 }
+// max(a, b) for values that are not signaling NaNs (as max_halves): the
+// plain v_max_f32, without the quieting fmaxf adds in front of it.
+__device__ inline float max_plain(float a, float b) {
+  float r;
+  asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
 // max(a, b, c) for values that are not signaling NaNs (as max_halves).
 __device__ inline float max3_plain(float a, float b, float c) {
   float r;

@@ -88,11 +88,15 @@ __device__ inline float exact_dot_global(const T* __restrict__ q, const T* __res
   return float(acc);
 }
 
+// Maximum of the 16 scores of a lane: a depth-3 tree of plain v_max3_f32
+// (scores are MFMA results or -inf, never signaling NaNs, so the quieting
+// that fmaxf puts in front of each operand is not needed; on quiet NaNs
+// v_max3_f32 returns the maximum of the other operands, as fmaxf does).
 __device__ inline float max16(const f32x16_t& a) {
-  float m = __builtin_fmaxf(a[0], a[1]);
-#pragma unroll
-  for (int e = 2; e < 16; ++e) m = __builtin_fmaxf(m, a[e]);
-  return m;
+  const float t0 = max3_plain(a[0], a[1], a[2]), t1 = max3_plain(a[3], a[4], a[5]);
+  const float t2 = max3_plain(a[6], a[7], a[8]), t3 = max3_plain(a[9], a[10], a[11]);
+  const float t4 = max3_plain(a[12], a[13], a[14]);
+  return max_plain(max3_plain(t0, t1, t2), max3_plain(t3, t4, a[15]));
 }
 
 template <typename T, int D, int BK>
@@ -206,8 +210,19 @@ __global__ __launch_bounds__(256, 2) void select_wave_kernel(
   // Segment seg writes its keys from slot max(seg_lo, smin) - smin of the row,
   // the slot of its first selectable key: segments never overlap.
   const int seg_slot = (seg_lo > smin ? seg_lo : smin) - smin;
-  int32_t* const orow = indices + (valid ? lay.row_offset(bh, jr) + seg_slot : 0);
   const int cap = valid ? int(lay.capacity(J0 + jr)) - seg_slot : 0;
+  // The keys are stored through a buffer resource over this wave's rows (the
+  // rows of one (b, h) are contiguous, at most 32 * 2^24 slots: the byte
+  // offsets fit 32 bits).  A lane's offset starts at its row's first slot of
+  // the segment and is clamped to the row's last slot, so that no store
+  // leaves its row and the loop needs no bounds branch.
+  const int64_t wrow0 = lay.row_offset(bh, jr_wave);
+  const int64_t wrow_end = lay.row_offset(bh, jr_wave + (nvalid_wave > 0 ? nvalid_wave : 0));
+  const __amdgpu_buffer_rsrc_t ors =
+      make_rsrc(indices + wrow0, uint32_t(nvalid_wave > 0 ? (wrow_end - wrow0) * 4 : 0));
+  const uint32_t ofirst =
+      valid ? uint32_t(lay.row_offset(bh, jr) - wrow0 + seg_slot) * 4u : 0xfffffff0u;
+  const uint32_t olast = valid && cap > 0 ? ofirst + uint32_t(cap - 1) * 4u : 0xfffffff0u;
   int rowcnt = 0;   // keys selected so far for this row
   int listcnt = 0;  // near-max tiles listed for this row
   float m = -__builtin_inff();  // MFMA running maximum of the row
@@ -277,13 +292,13 @@ __global__ __launch_bounds__(256, 2) void select_wave_kernel(
   auto append = [&](int kb0, int bb, uint32_t bt) {
     const int cnt = __builtin_popcount(bt);
     const int ocnt = int(other_half(uint32_t(cnt)));
-    int pos = rowcnt + (hh ? ocnt : 0);
+    uint32_t off = ofirst + uint32_t(rowcnt + (hh ? ocnt : 0)) * 4u;
     const int key0 = kb0 + 32 * bb + 16 * hh;
     while (bt) {
       const int e = __builtin_ctz(bt);
       bt &= bt - 1;
-      if (pos < cap) orow[pos] = key0 + e;
-      ++pos;
+      __builtin_amdgcn_raw_buffer_store_b32(key0 + e, ors, off < olast ? off : olast, 0, 0);
+      off += 4u;
     }
     rowcnt += cnt + ocnt;
   };
@@ -477,8 +492,8 @@ __global__ __launch_bounds__(256, 2) void select_wave_kernel(
         const float t00 = hh ? om0 : tm0, t01 = hh ? tm0 : om0;
         const float t10 = hh ? om1 : tm1, t11 = hh ? tm1 : om1;
         if (BK == 16) {
-          const float r00 = __builtin_fmaxf(m, t00), r01 = __builtin_fmaxf(r00, t01);
-          const float r10 = __builtin_fmaxf(r01, t10), r11 = __builtin_fmaxf(r10, t11);
+          const float r00 = max_plain(m, t00), r01 = max_plain(r00, t01);
+          const float r10 = max_plain(r01, t10), r11 = max_plain(r10, t11);
           mt[0] = hh ? r01 : r00;
           mt[1] = hh ? r11 : r10;
           m = r11;
@@ -493,8 +508,8 @@ __global__ __launch_bounds__(256, 2) void select_wave_kernel(
           rmax[0] = tm0;
           rmax[1] = tm1;
         } else if (BK == 32) {
-          const float bm0 = __builtin_fmaxf(t00, t01), bm1 = __builtin_fmaxf(t10, t11);
-          const float r0 = __builtin_fmaxf(m, bm0), r1 = __builtin_fmaxf(r0, bm1);
+          const float bm0 = max_plain(t00, t01), bm1 = max_plain(t10, t11);
+          const float r0 = max_plain(m, bm0), r1 = max_plain(r0, bm1);
           mt[0] = r0;
           mt[1] = r1;
           m = r1;
@@ -508,8 +523,8 @@ __global__ __launch_bounds__(256, 2) void select_wave_kernel(
           rmax[0] = bm0;
           rmax[1] = bm1;
         } else {
-          const float cm = __builtin_fmaxf(__builtin_fmaxf(t00, t01), __builtin_fmaxf(t10, t11));
-          const float r = __builtin_fmaxf(m, cm);
+          const float cm = max_plain(max_plain(t00, t01), max_plain(t10, t11));
+          const float r = max_plain(m, cm);
           mt[0] = mt[1] = r;
           m = r;
           const int g = (live[0] && cm >= r - win) ? 1 : 0;
