@@ -122,11 +122,15 @@ int va_select(int dtype, const void* qs, int64_t sqb, int64_t sqh, int64_t sqn,
  * Segment s of row J writes its keys in ascending order from slot
  * max(s*segment_keys, smin) - smin of the row's index layout and its count to
  * counts[((b*Hq + h)*nc + (J - J0))*nseg + s], nseg = ceil(Sk / segment_keys);
- * a row's list is the concatenation of its segments.  Needs the VA_SEL_WAVE
- * kernel's conditions.  No counterpart in the reference (its single launch
- * writes dense rows); the selected sets are the reference rule's, as for
- * va_select.
- * va_select_segment_keys returns the segment length va_prefill uses, 0 when
+ * a row's list is the concatenation of its segments.  Runs on the VA_SEL_WAVE
+ * kernel where its conditions hold, else on the 64-row MFMA kernel (VA_SEL_MFMA
+ * conditions, one pass, segment_keys a multiple of 256).  No counterpart in
+ * the reference (its single launch writes dense rows); the selected sets are
+ * the reference rule's, as for va_select.
+ * va_select_segment_keys returns the segment length va_prefill uses for
+ * bf16/fp16 inputs with head_dim 64 or 128: the wave kernel's (tiles of 16 to
+ * 64 keys, group span a multiple of 64 keys), else the 64-row MFMA kernel's
+ * (whole 256-key chunks that each start a group, e.g. group_k_block 1); 0 when
  * the keys are not split, or -1 on invalid sizes.
  */
 int64_t va_select_segment_keys(int64_t Sk, int64_t k_local_size, int64_t group_k_block);

@@ -328,6 +328,12 @@ MFMA_SPLIT_CASES = [
      2, 0.10, 1024, 9),
     ("noncausal-bk256-G2-seg512-gap0", 2, 2, 2300, 64, torch.float16, False, 64, 256, 2, None,
      512, None),
+    # groups shorter than the wave kernel's 64-key chunk (the reference models'
+    # default group_k_block 1 with k_local_size 16): this kernel's split
+    ("causal-bk16-G1-seg512-chunked", 4, 2, 3000, 128, torch.bfloat16, True, 64, 16, 1, 0.10,
+     512, 20),
+    ("noncausal-bk16-G3-seg768-gap0", 2, 2, 2500, 128, torch.bfloat16, False, 64, 16, 3, None,
+     768, None),
 ]
 
 

@@ -44,6 +44,7 @@ hipError_t launch_select_wave(int dtype, const void* qs, int64_t sqb, int64_t sq
                               int mode, hipStream_t stream);
 constexpr int64_t kSegCarryBytes = 32;  // per (row, segment) record of the two-pass selection
 int64_t select_wave_segment_keys(int64_t Sk, int64_t bk, int64_t group);
+int64_t select_mfma_segment_keys(int64_t Sk, int64_t bk, int64_t group);
 int64_t select_wave_carry_segment_keys(int64_t Sk, int64_t bk, int64_t group);
 int64_t key_norm_scratch_floats(int64_t B, int64_t Hk);
 hipError_t launch_key_norm(int dtype, const void* k, int64_t skb, int64_t skh, int64_t sks,
@@ -312,7 +313,12 @@ int64_t va_select_segment_keys(int64_t Sk, int64_t k_local_size, int64_t group_k
   if (Sk <= 0 || k_local_size <= 0 || group_k_block <= 0) return -1;
   const int64_t g = effective_group(group_k_block, Sk, k_local_size);
   const int64_t segk = va::select_wave_segment_keys(Sk, k_local_size, g);
-  return segk > 0 ? segk : va::select_wave_carry_segment_keys(Sk, k_local_size, g);
+  if (segk > 0) return segk;
+  // tiles and groups the wave kernel takes (bf16/fp16, D 64 or 128): its
+  // two-pass split; others run on the 64-row MFMA kernel's split
+  if (va::select_wave_supported(VA_BF16, 128, k_local_size, g))
+    return va::select_wave_carry_segment_keys(Sk, k_local_size, g);
+  return va::select_mfma_segment_keys(Sk, k_local_size, g);
 }
 
 // The two-pass form: the groups cover every key of a row and the segments do
@@ -825,9 +831,9 @@ int va_prefill_kernels(int dtype, const void* q, int64_t sqb, int64_t sqh, int64
     flags |= VA_KERNELS_ATTN_RING;
   if (attn && (flags & (VA_KERNELS_SELECT_WAVE | VA_KERNELS_SELECT_MFMA))) {
     const int64_t g = effective_group(group, Sk, bk);
-    const int64_t sg = va::select_wave_segment_keys(Sk, bk, g);
-    if (wave ? (sg > 0 || va::select_wave_carry_segment_keys(Sk, bk, g) > 0)
-             : (sg > 0 && sg % 256 == 0))
+    if (wave ? (va::select_wave_segment_keys(Sk, bk, g) > 0 ||
+                va::select_wave_carry_segment_keys(Sk, bk, g) > 0)
+             : va::select_mfma_segment_keys(Sk, bk, g) > 0)
       flags |= VA_KERNELS_SPLIT;
   }
   ok();
@@ -900,8 +906,7 @@ int va_prefill(int dtype, const void* q, int64_t sqb, int64_t sqh, int64_t sqs, 
       }
     } else if (which == kSelMfma && attn) {
       // the 64-row MFMA kernel splits at whole 256-key chunks (no carry pass)
-      const int64_t sg = va::select_wave_segment_keys(Sk, bk, g);
-      if (sg > 0 && sg % 256 == 0) segk = sg;
+      segk = va::select_mfma_segment_keys(Sk, bk, g);
     }
   }
   const float scale = float(1.0 / std::sqrt(double(D)));

@@ -557,6 +557,31 @@ __global__ __launch_bounds__(256) void select_mfma_kernel(
   }
 }
 
+// Key segments of this kernel's split selection: whole 256-key chunks that
+// each start a group, i.e. a multiple of lcm(256, group span), about Sk / 16
+// keys within [2048, 4096] and at most 64 segments (the wave kernel's rule);
+// 0 when one group covers a row (this kernel has no carry pass) or nothing is
+// left to split.  Groups shorter than 64 keys (the reference models' default
+// group_k_block of 1 with k_local_size 16) run on this kernel, and unsplit
+// their long causal rows each take one work-group through every key.
+int64_t select_mfma_segment_keys(int64_t Sk, int64_t bk, int64_t group) {
+  constexpr int64_t kMaxSeg = 64, kChunk = 256;
+  const int64_t gs = bk * group;
+  if (gs <= 0 || gs >= Sk) return 0;
+  int64_t a = kChunk, b = gs;  // lcm(kChunk, gs)
+  while (b) {
+    const int64_t t = a % b;
+    a = b;
+    b = t;
+  }
+  const int64_t unit = kChunk / a * gs;
+  const int64_t target = Sk / 16 < 2048 ? 2048 : (Sk / 16 > 4096 ? 4096 : Sk / 16);
+  int64_t want = (Sk + kMaxSeg - 1) / kMaxSeg;
+  if (want < target) want = target;
+  const int64_t segk = (want + unit - 1) / unit * unit;
+  return segk < Sk ? segk : 0;
+}
+
 bool select_mfma_supported(int dtype, int64_t D, int64_t bk) {
   return (dtype == kBF16 || dtype == kF16) && (D == 64 || D == 128) &&
          (bk == 16 || bk == 32 || bk == 64 || bk == 128 || bk == 256);
