@@ -94,9 +94,9 @@ int va_pool(int dtype, const void* q, int64_t B, int64_t H, int64_t S, int64_t D
  *                  fp64 recomputation inside the band (D in {64,128},
  *                  k_local_size in {16,32,64}); needs `scratch`;
  *   VA_SEL_WAVE  : the same certified scheme organised one wave per 32 rows
- *                  (additionally k_local_size * group_k_block a multiple of
- *                  64, Sk < 2^24, < 2 GiB of key rows per kv head); needs
- *                  `scratch`;
+ *                  (additionally k_local_size * group_k_block 16, 32 or a
+ *                  multiple of 64, Sk < 2^24, < 2 GiB of key rows per kv
+ *                  head); needs `scratch`;
  *   VA_SEL_AUTO  : WAVE, else MFMA, when supported and scratch is given, else
  *                  exact.
  * scratch: device fp32 buffer of va_select_scratch_floats(B, Hk) floats (key
@@ -129,9 +129,10 @@ int va_select(int dtype, const void* qs, int64_t sqb, int64_t sqh, int64_t sqn,
  * the reference rule's, as for va_select.
  * va_select_segment_keys returns the segment length va_prefill uses for
  * bf16/fp16 inputs with head_dim 64 or 128: the wave kernel's (tiles of 16 to
- * 64 keys, group span a multiple of 64 keys), else the 64-row MFMA kernel's
- * (whole 256-key chunks that each start a group, e.g. group_k_block 1); 0 when
- * the keys are not split, or -1 on invalid sizes.
+ * 64 keys, group span of 16 or 32 keys or a multiple of 64), else the 64-row
+ * MFMA kernel's (whole 256-key chunks that each start a group, e.g.
+ * k_local_size 128 or a group span of 48 keys); 0 when the keys are not split,
+ * or -1 on invalid sizes.
  */
 int64_t va_select_segment_keys(int64_t Sk, int64_t k_local_size, int64_t group_k_block);
 /* fp32 scratch floats va_select_segments needs: the key norms, plus two floats

@@ -137,6 +137,13 @@ SELECT_CASES = [
     ("bf16-noncausal-G8192-tail", 1, 4, 4, 3000, 128, torch.bfloat16, False, 64, 16, 8192, 0.15, None),
     ("fp16-causal-qps128-bk32", 2, 4, 2, 1536, 64, torch.float16, True, 128, 32, 4, 0.10, None),
     ("bf16-noncausal-G1-bk64", 1, 2, 1, 1100, 128, torch.bfloat16, False, 64, 64, 1, 0.2, None),
+    # groups of 16 and 32 keys (the reference models' group_k_block 1): the
+    # wave kernel restarts the running maximum inside its 64-key chunks
+    ("bf16-causal-bk16-G1", 1, 4, 2, 2048, 128, torch.bfloat16, True, 64, 16, 1, 0.10, None),
+    ("fp16-noncausal-bk16-G2-tail", 1, 4, 2, 1500, 64, torch.float16, False, 64, 16, 2, 0.15,
+     None),
+    ("bf16-causal-qps128-bk32-G1-chunked", 2, 4, 1, 1800, 128, torch.bfloat16, True, 128, 32, 1,
+     0.10, 6),
 ]
 
 
@@ -243,6 +250,11 @@ SEGMENT_CASES = [
      None),
     ("noncausal-2pass-gap0-seg1024", 2, 2, 4100, 128, torch.bfloat16, False, 16, 8192, None,
      1024, None),
+    # groups of 16 and 32 keys: segments of whole 64-key chunks
+    ("causal-bk16-G1-seg512-chunked", 4, 2, 3000, 128, torch.bfloat16, True, 16, 1, 0.10, 512,
+     20),
+    ("noncausal-bk16-G2-seg192-gap0", 2, 2, 2000, 64, torch.float16, False, 16, 2, None, 192,
+     None),
 ]
 
 
@@ -314,6 +326,10 @@ MFMA_STRESS = [
     ("noncausal-G8192-bk32", 2, 1, 2500, 128, False, 32, 8192, 0.12),
     ("noncausal-G3-bk64-gap0", 2, 2, 1500, 64, False, 64, 3, 0.0),
     ("causal-G5-bk16", 2, 2, 2048, 64, True, 16, 5, 0.05),
+    # groups of 16 and 32 keys: every tile's maximum key is ambiguous at gap 0
+    ("causal-G1-bk16-gap0", 2, 1, 2048, 128, True, 16, 1, 0.0),
+    ("noncausal-G2-bk16-gap0-tail", 2, 2, 1500, 64, False, 16, 2, 0.0),
+    ("noncausal-G1-bk32-gap0", 2, 1, 1300, 128, False, 32, 1, 0.0),
     # tiles of 128 / 256 keys (MFMA kernel only): exact ties, groups over chunks
     ("noncausal-G2-bk128-gap0", 2, 2, 1500, 128, False, 128, 2, 0.0),
     ("noncausal-G3-bk256-gap0", 2, 1, 1300, 64, False, 256, 3, 0.0),
@@ -328,10 +344,11 @@ MFMA_SPLIT_CASES = [
      2, 0.10, 1024, 9),
     ("noncausal-bk256-G2-seg512-gap0", 2, 2, 2300, 64, torch.float16, False, 64, 256, 2, None,
      512, None),
-    # groups shorter than the wave kernel's 64-key chunk (the reference models'
-    # default group_k_block 1 with k_local_size 16): this kernel's split
-    ("causal-bk16-G1-seg512-chunked", 4, 2, 3000, 128, torch.bfloat16, True, 64, 16, 1, 0.10,
-     512, 20),
+    # groups of 16 keys with a first selectable key (q_pooling_size 32) that
+    # does not start a 64-key chunk, and groups of 48 keys: spans the wave
+    # kernel does not take
+    ("causal-qps32-bk16-G1-seg512-chunked", 4, 2, 3000, 128, torch.bfloat16, True, 32, 16, 1,
+     0.10, 512, 40),
     ("noncausal-bk16-G3-seg768-gap0", 2, 2, 2500, 128, torch.bfloat16, False, 64, 16, 3, None,
      768, None),
 ]
@@ -391,7 +408,7 @@ def test_select_mfma_exact_fallback(device, case, kernel):
     assert_lists_equal(got, want, name)
 
 
-@pytest.mark.parametrize("G", [2, 4, 64])
+@pytest.mark.parametrize("G", [1, 2, 4, 64])
 @pytest.mark.parametrize("kernel", SEL_KERNELS, ids=SEL_IDS)
 def test_select_ties_from_duplicate_keys(device, kernel, G):
     # Repeated key rows give exactly equal scores: selection at equality.
@@ -551,6 +568,8 @@ E2E_CASES = [
     # long enough for the two-pass split selection (segments of 2048 keys)
     ("dit-like-2pass", 1, 2, 2, 9000, 128, torch.bfloat16, False, 64, 16, 8192, 4608, 0.3),
     ("causal-qps128-bk16", 1, 4, 4, 1300, 64, torch.bfloat16, True, 128, 16, 4, 512, 0.6),
+    # the reference models' defaults (k_local_size 16, group_k_block 1)
+    ("model-defaults-causal-G1", 1, 4, 2, 3000, 128, torch.bfloat16, True, 64, 16, 1, 1024, 0.9),
     ("A-fp32-noncausal", 1, 4, 4, 4096, 64, torch.float32, False, 64, 16, 16, 4096, 0.35),
     # batches: every (b, h) work item, strides over the batch dimension
     ("batch2-causal-gqa", 2, 8, 2, 1536, 128, torch.bfloat16, True, 64, 16, 16, 1024, 0.5),

@@ -244,13 +244,19 @@ def test_prefill_kernels_reports_the_mfma_path(L):
     assert _plan(L, Hq=6, Hk=4) == nat.VA_ERR_ARG             # q heads not a multiple
     # va_prefill takes q_pooling_size 64 or 128 only, and so does its plan
     assert _plan(L, qps=96) == nat.VA_ERR_ARG
-    # the reference models' default group_k_block 1 (16-key groups, shorter
-    # than the wave kernel's chunk): the 64-row MFMA kernel, split into key
-    # segments of whole 256-key chunks
-    split_mfma = nat.VA_KERNELS_SELECT_MFMA | nat.VA_KERNELS_ATTN_MFMA | nat.VA_KERNELS_SPLIT
-    assert _plan(L, G=1) == split_mfma | ring
-    assert _plan(L, G=1, Sk=131072) == split_mfma | ring
+    # the reference models' default group_k_block 1: groups of 16 or 32 keys
+    # divide the wave kernel's 64-key chunk, so it takes them, in segments of
+    # whole chunks
+    assert _plan(L, G=1) == fast | ring
+    assert _plan(L, G=1, Sk=131072) == fast | ring
+    assert _plan(L, G=2) == fast | ring and _plan(L, bk=32, G=1) == fast | ring
     assert L.va_select_segment_keys(131072, 16, 1) == 4096
+    assert L.va_select_segment_keys(32768, 16, 1) == 2048
+    assert L.va_select_segment_keys(3000, 32, 1) % 64 == 0
+    # a 48-key span neither divides nor is a multiple of the chunk: the 64-row
+    # MFMA kernel, split into key segments of whole 256-key chunks
+    split_mfma = nat.VA_KERNELS_SELECT_MFMA | nat.VA_KERNELS_ATTN_MFMA | nat.VA_KERNELS_SPLIT
+    assert _plan(L, G=3) == split_mfma | ring
     assert L.va_select_segment_keys(3000, 16, 3) % 768 == 0
 
 

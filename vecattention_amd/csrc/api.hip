@@ -189,8 +189,8 @@ int64_t va_select_scratch_floats(int64_t B, int64_t Hk) {
 
 // A group longer than the key range is a single group: any value covering
 // every tile gives the same selection.  Capped so that bk * group stays small,
-// and to a multiple of 4 tiles so that the capped span stays a multiple of 64
-// keys (the wave kernel starts groups at 64-key chunk boundaries).
+// and to a multiple of 4 tiles so that a capped span is a multiple of 64 keys
+// (the wave kernel takes spans of 16 or 32 keys or multiples of 64).
 static int64_t effective_group(int64_t group, int64_t Sk, int64_t bk) {
   const int64_t gmax = (cdiv(Sk, bk) + 1 + 3) / 4 * 4;
   return group > gmax ? gmax : group;
@@ -284,7 +284,8 @@ int va_select(int dtype, const void* qs, int64_t sqb, int64_t sqh, int64_t sqn,
     if (kernel == VA_SEL_WAVE && !wave_ok)
       return fail(VA_ERR_UNSUPPORTED,
                   "wave selection needs bf16/fp16, D in {64,128}, k_local_size in {16,32,64}, "
-                  "k_local_size * group_k_block a multiple of 64, 16-byte aligned rows, "
+                  "k_local_size * group_k_block 16, 32 or a multiple of 64, 16-byte aligned "
+                  "rows, "
                   "Sk < 2^24, < 2 GiB of key rows per kv head and a first selectable key "
                   "at a multiple of 64");
     if (!have_scratch) return fail(VA_ERR_ARG, "MFMA selection needs scratch");

@@ -37,6 +37,13 @@
 // rest of the group, and the list is cleared.  Everything exact runs on the
 // rare path of the wave that needs it.
 //
+// Groups shorter than a chunk.  A group span of 16 or 32 keys (k_local_size
+// 16 or 32 with group_k_block 1 or 2) divides the 64-key chunk: every chunk
+// starts a group and the running maximum also restarts at the group starts
+// inside the chunk.  A row's exact maximum at a key then depends only on the
+// key's own group, which lies in the chunk, so nothing is listed: the rare
+// path takes, for each ambiguous key, the tiles of its group up to its own.
+//
 // Output.  Each lane writes its selected keys straight to the row's index
 // list (ascending: the low half's tile before the high half's).
 #include "lanes.h"
@@ -144,6 +151,9 @@ __global__ __launch_bounds__(256, 2) void select_wave_kernel(
   const float kn = kmax[b * Hk + hk];
   const int smin = int(lay.smin());
   const int sk = int(Sk);  // < 2^24 (host check)
+  // Groups of 16 or 32 keys (the span then divides the chunk): the running
+  // maximum restarts inside chunks and no near-max tiles are listed.
+  const bool short_groups = BK < kWChunk && gspan < uint32_t(kWChunk);
 
   // Causal tile limit of a row: tiles with start < lim are selectable.  The
   // reference's test r > trunc((k_off - off0) / qps), r the row inside its
@@ -308,17 +318,34 @@ __global__ __launch_bounds__(256, 2) void select_wave_kernel(
   // keys (ambm, as chunk offsets from kb0); the exact tile maxima give the
   // exact running maximum at each ambiguous key's tile.  Resolved selections
   // go to ovr, the listed tiles are folded into the row's exact maximum and
-  // the list is cleared.
+  // the list is cleared.  With short groups the row's list is instead made
+  // here: the tiles of the chunk from each ambiguous key's group start up to
+  // the key's own tile.
   auto resolve = [&](uint64_t need, int kb0, uint32_t (&ovr)[2]) {
     while (need) {
       const int r = __builtin_ctzll(need);
       need &= need - 1;
-      const int n = __builtin_amdgcn_readlane(listcnt, r);
+      int n = __builtin_amdgcn_readlane(listcnt, r);
       const T* qr = qs + b * sqb + h * sqh + (jr_wave + r) * sqn;
       // Ambiguous keys of row r, as chunk offsets 32b + 16hh + e (64 bits).
       const uint64_t a64 = uint64_t(ambm[wave][r][0]) | (uint64_t(ambm[wave][r][1]) << 16) |
                            (uint64_t(ambm[wave][r][2]) << 32) |
                            (uint64_t(ambm[wave][r][3]) << 48);
+      if constexpr (BK < kWChunk) {
+        if (short_groups) {
+          constexpr int NT = kWChunk / BK;  // tiles per chunk
+          const int tpg = int(gspan) / BK;  // tiles per group
+          uint32_t tneed = 0;
+#pragma unroll
+          for (int t = 0; t < NT; ++t)
+            if ((a64 >> (t * BK)) & ((uint64_t(1) << BK) - 1u))
+              tneed |= ((2u << t) - 1u) & ~((1u << (t / tpg * tpg)) - 1u);
+          tneed = __builtin_amdgcn_readfirstlane(tneed);
+          n = __builtin_popcount(tneed);
+          if (lane < NT && ((tneed >> lane) & 1u))
+            nml[wave][r][__builtin_popcount(tneed & ((1u << lane) - 1u))] = kb0 / BK + lane;
+        }
+      }
       if ((a64 >> lane) & 1u)
         ambk[wave][__builtin_amdgcn_mbcnt_hi(uint32_t(a64 >> 32),
                                              __builtin_amdgcn_mbcnt_lo(uint32_t(a64), 0))] =
@@ -342,10 +369,15 @@ __global__ __launch_bounds__(256, 2) void select_wave_kernel(
         // come from this or earlier passes)
         bool tk = false;
         if (j >= ntile && j < njobs) {
+          // listed tiles of the key's group up to its own tile (with long
+          // groups every listed tile is of the current group: tg = 0)
           const int t = key / BK;
+          const int tg = short_groups ? int(uint32_t(key) & ~(gspan - 1u)) / BK : 0;
           float E = E0;
-          for (int i = 0; i < n; ++i)
-            if (nml[wave][r][i] <= t) E = __builtin_fmaxf(E, tmx[wave][i]);
+          for (int i = 0; i < n; ++i) {
+            const int u = nml[wave][r][i];
+            if (u <= t && u >= tg) E = __builtin_fmaxf(E, tmx[wave][i]);
+          }
           tk = (ex + gap) >= E;
         }
         // Fold: bit (key - kb0) of the row's resolved selections.
@@ -360,10 +392,11 @@ __global__ __launch_bounds__(256, 2) void select_wave_kernel(
         ovr[0] |= uint32_t(take >> (16 * hh)) & 0xffffu;
         ovr[1] |= uint32_t(take >> (32 + 16 * hh)) & 0xffffu;
       }
-      // Fold the listed tiles into the row's exact maximum.
+      // Fold the listed tiles into the row's exact maximum (short groups end
+      // with the chunk: nothing to fold).
       float E = E0;
       for (int i = 0; i < n; ++i) E = __builtin_fmaxf(E, tmx[wave][i]);
-      if (lane == 0) exr[wave][r] = E;
+      if (lane == 0 && !short_groups) exr[wave][r] = E;
       if (l32 == r) listcnt = 0;
     }
   };
@@ -473,13 +506,16 @@ __global__ __launch_bounds__(256, 2) void select_wave_kernel(
 
       // ---- running maximum per tile -------------------------------------------
       // A tile is worth listing only for a valid row, before the row's causal
-      // limit (later tiles select nothing), and when it holds a visited key.
+      // limit (later tiles select nothing), and when it holds a visited key;
+      // short groups list nothing.  Groups of 16 keys restart the running
+      // maximum at every tile, groups of 32 at chunk offset 32 (rs1, rs2).
       bool live[2];
 #pragma unroll
       for (int bb = 0; bb < 2; ++bb) {
         const int koff = BK == 16 ? kb0 + 32 * bb + 16 * hh : (BK == 32 ? kb0 + 32 * bb : kb0);
-        live[bb] = valid && koff < lim && koff + BK > smin && koff < sk;
+        live[bb] = !short_groups && valid && koff < lim && koff + BK > smin && koff < sk;
       }
+      const bool rs1 = short_groups && gspan <= 16u, rs2 = short_groups;
       const float tm0 = max16(acc[0]), tm1 = max16(acc[1]);
       const float om0 = other_half(tm0), om1 = other_half(tm1);
       const float m_prev = m;  // running maximum before this chunk's tiles
@@ -492,8 +528,10 @@ __global__ __launch_bounds__(256, 2) void select_wave_kernel(
         const float t00 = hh ? om0 : tm0, t01 = hh ? tm0 : om0;
         const float t10 = hh ? om1 : tm1, t11 = hh ? tm1 : om1;
         if (BK == 16) {
-          const float r00 = max_plain(m, t00), r01 = max_plain(r00, t01);
-          const float r10 = max_plain(r01, t10), r11 = max_plain(r10, t11);
+          const float r00 = max_plain(m, t00);
+          const float r01 = rs1 ? t01 : max_plain(r00, t01);
+          const float r10 = rs2 ? t10 : max_plain(r01, t10);
+          const float r11 = rs1 ? t11 : max_plain(r10, t11);
           mt[0] = hh ? r01 : r00;
           mt[1] = hh ? r11 : r10;
           m = r11;
@@ -509,7 +547,7 @@ __global__ __launch_bounds__(256, 2) void select_wave_kernel(
           rmax[1] = tm1;
         } else if (BK == 32) {
           const float bm0 = max_plain(t00, t01), bm1 = max_plain(t10, t11);
-          const float r0 = max_plain(m, bm0), r1 = max_plain(r0, bm1);
+          const float r0 = max_plain(m, bm0), r1 = rs2 ? bm1 : max_plain(r0, bm1);
           mt[0] = r0;
           mt[1] = r1;
           m = r1;
@@ -553,18 +591,19 @@ __global__ __launch_bounds__(256, 2) void select_wave_kernel(
       // rejected above.  The sign bits are shifted into the lane's mask
       // (v_alignbit), and as unsigned integers the smallest non-negative x is
       // the smallest bit pattern (negative x sort above 2*band), so one
-      // unsigned minimum tests ambiguity.  Tiles past the causal limit select
-      // nothing (hi = +inf).  x is never NaN: s^ is -inf only for keys past Sk,
-      // which follow a finite running maximum, since the host runs this
-      // kernel only when the first selectable key starts a 64-key chunk (keys
-      // below it are never visited).
+      // unsigned minimum tests ambiguity.  Tiles past the causal limit or
+      // starting at or past Sk select nothing (hi = +inf).  x is never NaN:
+      // s^ is -inf only for keys past Sk, and any other tile holds a key below
+      // Sk, so its running maximum is finite, since the host runs this kernel
+      // only when the first selectable key starts a 64-key chunk (keys below
+      // it are never visited).
       uint32_t bits[2];
       float hi[2];
       uint32_t xmin = 0xffffffffu;
 #pragma unroll
       for (int bb = 0; bb < 2; ++bb) {
         const int koff = BK == 16 ? kb0 + 32 * bb + 16 * hh : (BK == 32 ? kb0 + 32 * bb : kb0);
-        const bool ok = valid && koff < lim && mode != kPassMax;  // maxima pass: select nothing
+        const bool ok = valid && koff < lim && koff < sk && mode != kPassMax;  // maxima pass: none
         hi[bb] = ok ? (mt[bb] - gap) + band : __builtin_inff();
         uint32_t bt = 0;
 #pragma unroll
@@ -686,10 +725,11 @@ static int64_t segment_target(int64_t Sk) {
 int64_t select_wave_segment_keys(int64_t Sk, int64_t bk, int64_t group) {
   constexpr int64_t kMaxSeg = 64;
   const int64_t gs = bk * group;
-  if (gs % kWChunk != 0 || gs >= Sk) return 0;
+  if ((gs % kWChunk != 0 && kWChunk % gs != 0) || gs >= Sk) return 0;
+  const int64_t unit = gs > kWChunk ? gs : kWChunk;  // groups of 16 or 32 keys: whole chunks
   int64_t want = (Sk + kMaxSeg - 1) / kMaxSeg;  // at most 64 segments
   if (want < segment_target(Sk)) want = segment_target(Sk);
-  const int64_t segk = (want + gs - 1) / gs * gs;
+  const int64_t segk = (want + unit - 1) / unit * unit;
   return segk < Sk ? segk : 0;
 }
 
@@ -706,9 +746,13 @@ int64_t select_wave_carry_segment_keys(int64_t Sk, int64_t bk, int64_t group) {
   return segk < Sk ? segk : 0;
 }
 
+// Group spans: multiples of the 64-key chunk, or 16 and 32 keys (spans that
+// divide the chunk).
 bool select_wave_supported(int dtype, int64_t D, int64_t bk, int64_t group) {
+  const int64_t gs = bk * group;
   return (dtype == kBF16 || dtype == kF16) && (D == 64 || D == 128) &&
-         (bk == 16 || bk == 32 || bk == 64) && (bk * group) % kWChunk == 0;
+         (bk == 16 || bk == 32 || bk == 64) && gs > 0 &&
+         (gs % kWChunk == 0 || kWChunk % gs == 0);
 }
 
 template <typename T, int D, int BK>
