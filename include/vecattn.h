@@ -148,6 +148,37 @@ int va_select_segments(int dtype, const void* qs, int64_t sqb, int64_t sqh, int6
                        int64_t dense_stride, int64_t segment_keys, int32_t* counts,
                        int32_t* indices, float* scratch, int64_t scratch_floats, void* stream);
 
+/*
+ * Compact (CSR) selection: the same selected sets as va_select, stored with
+ * no padding, in two calls on one stream and with the same arguments.
+ *   Counting call (indices == NULL): counts[(b*Hq + h)*nc + jr] (times nseg,
+ *   plus the segment, when split) and the int64 row offsets
+ *   offsets[0 .. B*Hq*nc]: offsets[0] = 0, row r = (b*Hq + h)*nc + jr holds
+ *   offsets[r+1] - offsets[r] keys.  No keys are stored; the offsets are
+ *   computed on the device (no host round trip).
+ *   Writing call (indices != NULL, room for offsets[B*Hq*nc] int32): row r's
+ *   keys in ascending order at indices[offsets[r] ..]; counts and offsets
+ *   must hold the counting call's results and are left unchanged.
+ * segment_keys: 0 selects each row in one pass (kernel as VA_SEL_AUTO;
+ * scratch of va_select_scratch_floats, or NULL for the exact kernel), > 0
+ * splits the keys as va_select_segments does (its conditions and scratch),
+ * nseg = ceil(Sk / segment_keys).  The writing call runs the selection again
+ * (bit-identical), so a compact list costs two selections and
+ * 4*offsets[B*Hq*nc] bytes instead of the capacity layout's slots.
+ * Replaces the output of fuse_qk_softmax_minp_wo_causal
+ * (spattn/src/kernels/vecattention_kernels.py:131-136,178-180: a zeroed dense
+ * B*H*nqb*padded_Sk int32 buffer, then trimmed to the longest row) with the
+ * count / scan / write form of the same sets; the reference itself has no
+ * compact output.
+ */
+int va_select_csr(int dtype, const void* qs, int64_t sqb, int64_t sqh, int64_t sqn,
+                  const void* k, int64_t skb, int64_t skh, int64_t sks, int64_t B, int64_t Hq,
+                  int64_t Hk, int64_t Sk, int64_t D, int64_t q_pooling_size, int64_t k_local_size,
+                  int64_t group_k_block, int causal, int wo_init, int64_t J0, int64_t nc,
+                  int64_t bsq, float gap, const float* gaps, int64_t segment_keys,
+                  int32_t* counts, int64_t* offsets, int32_t* indices, float* scratch,
+                  int64_t scratch_floats, void* stream);
+
 /* fp32 scratch floats va_select's MFMA kernel needs (B*Hk key-norm slots). */
 int64_t va_select_scratch_floats(int64_t B, int64_t Hk);
 

@@ -93,6 +93,27 @@ def test_select_argument_errors_before_launch(L):
     assert _null_select(L, kernel=9) == nat.VA_ERR_ARG
 
 
+def _null_csr(L, **over):
+    args = dict(dtype=nat.VA_BF16, qs=256, sqb=0, sqh=0, sqn=0, k=256, skb=0, skh=0, sks=128, B=1,
+                Hq=4, Hk=2, Sk=1024, D=128, qps=64, bk=16, G=16, causal=1, wo_init=1, J0=0, nc=16,
+                bsq=64, gap=0.2, gaps=None, segk=0, counts=1, offsets=1, indices=None,
+                scratch=None, scratch_floats=0, stream=None)
+    args.update(over)
+    return L.va_select_csr(*args.values())
+
+
+def test_select_csr_argument_errors_before_launch(L):
+    assert _null_csr(L, counts=None) == nat.VA_ERR_ARG
+    assert _null_csr(L, offsets=None) == nat.VA_ERR_ARG
+    assert _null_csr(L, segk=-64) == nat.VA_ERR_ARG
+    assert _null_csr(L, Hk=3) == nat.VA_ERR_ARG
+    assert _null_csr(L, bk=48) == nat.VA_ERR_UNSUPPORTED
+    # split: segment length rules and scratch as va_select_segments
+    assert _null_csr(L, segk=100) == nat.VA_ERR_ARG                 # not a multiple of 64
+    assert _null_csr(L, segk=512) == nat.VA_ERR_ARG                 # no scratch
+    assert b"scratch" in L.va_last_error()
+
+
 def test_prefill_argument_errors_before_launch(L):
     f = L.va_prefill
     base = [nat.VA_BF16, 1, 0, 0, 128, 1, 0, 0, 128, 1, 0, 0, 128, 1, 0, 0, 128,

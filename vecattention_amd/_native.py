@@ -45,6 +45,9 @@ SIGNATURES = {
     "va_select_segments": (_int, [_int, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _i64, _i64,
                                   _i64, _i64, _i64, _i64, _i64, _i64, _int, _int, _i64, _i64, _i64,
                                   _f32, _vp, _i64, _i64, _vp, _vp, _vp, _i64, _vp]),
+    "va_select_csr": (_int, [_int, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _i64, _i64, _i64,
+                             _i64, _i64, _i64, _i64, _i64, _int, _int, _i64, _i64, _i64, _f32, _vp,
+                             _i64, _vp, _vp, _vp, _vp, _i64, _vp]),
     "va_select_scratch_floats": (_i64, [_i64, _i64]),
     "va_select_segments_scratch_floats": (_i64, [_i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64]),
     "va_select_index_capacity": (_i64, [_i64, _i64, _i64, _i64, _int, _int, _i64, _i64, _i64]),

@@ -47,6 +47,8 @@ int64_t select_wave_segment_keys(int64_t Sk, int64_t bk, int64_t group);
 int64_t select_mfma_segment_keys(int64_t Sk, int64_t bk, int64_t group);
 int64_t select_wave_carry_segment_keys(int64_t Sk, int64_t bk, int64_t group);
 int64_t key_norm_scratch_floats(int64_t B, int64_t Hk);
+hipError_t launch_csr_offsets(const int32_t* counts, int64_t rows, int nseg, int64_t* offsets,
+                              hipStream_t stream);
 hipError_t launch_key_norm(int dtype, const void* k, int64_t skb, int64_t skh, int64_t sks,
                            int64_t B, int64_t Hk, int64_t Sk, int64_t D, float* scratch,
                            hipStream_t stream);
@@ -206,8 +208,11 @@ static int select_impl(int dtype, const void* qs, int64_t sqb, int64_t sqh, int6
                        int64_t bsq, float gap, const float* gaps, int64_t dense_stride,
                        int32_t* counts, int32_t* indices, SelKernel which, const float* kmax,
                        int64_t segk, hipStream_t stream, void* carry = nullptr,
-                       int mode = 0) {
-  const va::RowLayout lay = make_layout(J0, nc, qps, Sk, causal, wo_init, dense_stride);
+                       int mode = 0, const int64_t* csr = nullptr,
+                       const int32_t* seg_counts = nullptr) {
+  va::RowLayout lay = make_layout(J0, nc, qps, Sk, causal, wo_init, dense_stride);
+  lay.csr = csr;  // compact output (non-null) instead of the capacity layout
+  lay.seg_counts = seg_counts;
   group = effective_group(group, Sk, bk);
   hipError_t e;
   if (which == kSelWave)
@@ -340,6 +345,40 @@ int64_t va_select_segments_scratch_floats(int64_t B, int64_t Hq, int64_t Hk, int
   return kn + va::kSegCarryBytes / 4 * B * Hq * nc * cdiv(Sk, segment_keys);  // carry records
 }
 
+// Kernel and passes of a split selection: segment lengths that are multiples
+// of 64 and of the group span (one pass), or any multiple of 64 when one
+// group covers the row (maxima pass, then carry pass), at most 64 segments.
+// The wave kernel takes every split; the 64-row MFMA kernel (tiles of 128 and
+// 256 keys) takes segments of whole 256-key chunks that start groups.
+static int plan_segments(int dtype, const void* qs, int64_t sqb, int64_t sqh, int64_t sqn,
+                         const void* k, int64_t skb, int64_t skh, int64_t sks, int64_t B,
+                         int64_t Hq, int64_t Hk, int64_t Sk, int64_t D, int64_t qps, int64_t bk,
+                         int64_t group, int causal, int wo_init, int64_t nc,
+                         int64_t segment_keys, const float* scratch, int64_t scratch_floats,
+                         SelKernel& which, bool& two_pass) {
+  const int64_t gs = bk * effective_group(group, Sk, bk);
+  if (segment_keys <= 0 || segment_keys % 64 || cdiv(Sk, segment_keys) > 64 ||
+      (segment_keys % gs != 0 && gs < Sk))
+    return fail(VA_ERR_ARG, "segment_keys %lld: need a multiple of 64 and of the group span "
+                            "(%lld keys) unless one group covers the row, at most 64 segments",
+                (long long)segment_keys, (long long)gs);
+  two_pass = segments_two_pass(Sk, bk, group, segment_keys);
+  which = (select_wave_ok(dtype, qs, sqb, sqh, sqn, k, skb, skh, sks, Sk, D, bk, group) &&
+           first_key_aligned(qps, Sk, causal, wo_init))
+              ? kSelWave
+          : (!two_pass && segment_keys % 256 == 0 &&
+             select_mfma_ok(dtype, qs, sqb, sqh, sqn, k, skb, skh, sks, D, bk))
+              ? kSelMfma
+              : kSelExact;
+  if (which == kSelExact)
+    return fail(VA_ERR_UNSUPPORTED, "segmented selection needs the wave selection kernel, or "
+                                    "the MFMA kernel with segments of whole 256-key chunks");
+  const int64_t need = va_select_segments_scratch_floats(B, Hq, Hk, Sk, nc, segment_keys, bk, group);
+  if (!scratch || scratch_floats < need)
+    return fail(VA_ERR_ARG, "segmented selection needs %lld scratch floats", (long long)need);
+  return VA_OK;
+}
+
 int va_select_segments(int dtype, const void* qs, int64_t sqb, int64_t sqh, int64_t sqn,
                        const void* k, int64_t skb, int64_t skh, int64_t sks, int64_t B,
                        int64_t Hq, int64_t Hk, int64_t Sk, int64_t D, int64_t qps, int64_t bk,
@@ -353,29 +392,11 @@ int va_select_segments(int dtype, const void* qs, int64_t sqb, int64_t sqh, int6
   if (!counts || !indices) return fail(VA_ERR_ARG, "null output pointer");
   if (dense_stride < 0 || (dense_stride > 0 && dense_stride < Sk))
     return fail(VA_ERR_ARG, "invalid dense_stride");
-  const int64_t gs = bk * effective_group(group, Sk, bk);
-  if (segment_keys <= 0 || segment_keys % 64 || cdiv(Sk, segment_keys) > 64 ||
-      (segment_keys % gs != 0 && gs < Sk))
-    return fail(VA_ERR_ARG, "segment_keys %lld: need a multiple of 64 and of the group span "
-                            "(%lld keys) unless one group covers the row, at most 64 segments",
-                (long long)segment_keys, (long long)gs);
-  const bool two_pass = segments_two_pass(Sk, bk, group, segment_keys);
-  // The wave kernel takes every split; the 64-row MFMA kernel (tiles of 128
-  // and 256 keys) takes segments of whole 256-key chunks that start groups.
-  const SelKernel which =
-      (select_wave_ok(dtype, qs, sqb, sqh, sqn, k, skb, skh, sks, Sk, D, bk, group) &&
-       first_key_aligned(qps, Sk, causal, wo_init))
-          ? kSelWave
-      : (!two_pass && segment_keys % 256 == 0 &&
-         select_mfma_ok(dtype, qs, sqb, sqh, sqn, k, skb, skh, sks, D, bk))
-          ? kSelMfma
-          : kSelExact;
-  if (which == kSelExact)
-    return fail(VA_ERR_UNSUPPORTED, "segmented selection needs the wave selection kernel, or "
-                                    "the MFMA kernel with segments of whole 256-key chunks");
-  const int64_t need = va_select_segments_scratch_floats(B, Hq, Hk, Sk, nc, segment_keys, bk, group);
-  if (!scratch || scratch_floats < need)
-    return fail(VA_ERR_ARG, "segmented selection needs %lld scratch floats", (long long)need);
+  SelKernel which;
+  bool two_pass;
+  rc = plan_segments(dtype, qs, sqb, sqh, sqn, k, skb, skh, sks, B, Hq, Hk, Sk, D, qps, bk, group,
+                     causal, wo_init, nc, segment_keys, scratch, scratch_floats, which, two_pass);
+  if (rc) return rc;
   hipStream_t st = static_cast<hipStream_t>(stream);
   rc = hip_check(va::launch_key_norm(dtype, k, skb, skh, sks, B, Hk, Sk, D, scratch, st),
                  "key norm launch");
@@ -392,6 +413,69 @@ int va_select_segments(int dtype, const void* qs, int64_t sqb, int64_t sqh, int6
                    which, scratch, segment_keys, st, carry,
                    two_pass ? va::kPassCarry : va::kPassPlain);
   return rc ? rc : ok();
+}
+
+int va_select_csr(int dtype, const void* qs, int64_t sqb, int64_t sqh, int64_t sqn,
+                  const void* k, int64_t skb, int64_t skh, int64_t sks, int64_t B, int64_t Hq,
+                  int64_t Hk, int64_t Sk, int64_t D, int64_t qps, int64_t bk, int64_t group,
+                  int causal, int wo_init, int64_t J0, int64_t nc, int64_t bsq, float gap,
+                  const float* gaps, int64_t segment_keys, int32_t* counts, int64_t* offsets,
+                  int32_t* indices, float* scratch, int64_t scratch_floats, void* stream) {
+  int rc = check_select_args(dtype, qs, k, B, Hq, Hk, Sk, D, qps, bk, group, causal, wo_init, J0,
+                             nc, bsq);
+  if (rc) return rc;
+  if (!counts || !offsets) return fail(VA_ERR_ARG, "null counts or offsets");
+  if (segment_keys < 0) return fail(VA_ERR_ARG, "negative segment_keys");
+  SelKernel which;
+  bool two_pass = false;
+  int64_t nseg = 1;
+  if (segment_keys > 0) {
+    rc = plan_segments(dtype, qs, sqb, sqh, sqn, k, skb, skh, sks, B, Hq, Hk, Sk, D, qps, bk,
+                       group, causal, wo_init, nc, segment_keys, scratch, scratch_floats, which,
+                       two_pass);
+    if (rc) return rc;
+    nseg = cdiv(Sk, segment_keys);
+  } else {
+    // every kernel selects the same keys: the counting and the writing call
+    // agree even when only one of them is given scratch
+    const bool have_scratch = scratch != nullptr &&
+                              scratch_floats >= va::key_norm_scratch_floats(B, Hk);
+    const bool wave = select_wave_ok(dtype, qs, sqb, sqh, sqn, k, skb, skh, sks, Sk, D, bk,
+                                     group) &&
+                      first_key_aligned(qps, Sk, causal, wo_init);
+    which = (wave && have_scratch) ? kSelWave
+            : (select_mfma_ok(dtype, qs, sqb, sqh, sqn, k, skb, skh, sks, D, bk) && have_scratch)
+                ? kSelMfma
+                : kSelExact;
+  }
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (which != kSelExact) {
+    rc = hip_check(va::launch_key_norm(dtype, k, skb, skh, sks, B, Hk, Sk, D, scratch, st),
+                   "key norm launch");
+    if (rc) return rc;
+  }
+  void* carry = scratch ? scratch + (va::key_norm_scratch_floats(B, Hk) + 7) / 8 * 8 : nullptr;
+  const bool write = indices != nullptr;
+  if (two_pass) {  // the maxima pass stores neither counts nor keys
+    rc = select_impl(dtype, qs, sqb, sqh, sqn, k, skb, skh, sks, B, Hq, Hk, Sk, D, qps, bk, group,
+                     causal, wo_init, J0, nc, bsq, gap, gaps, 0, nullptr, nullptr, kSelWave,
+                     scratch, segment_keys, st, carry, va::kPassMax);
+    if (rc) return rc;
+  }
+  // Counting call: counts only (no keys stored), then the offsets.  Writing
+  // call: the keys, at the offsets and segment counts of the counting call.
+  rc = select_impl(dtype, qs, sqb, sqh, sqn, k, skb, skh, sks, B, Hq, Hk, Sk, D, qps, bk, group,
+                   causal, wo_init, J0, nc, bsq, gap, gaps, 0, write ? nullptr : counts, indices,
+                   which, scratch, segment_keys, st, carry,
+                   two_pass ? va::kPassCarry : va::kPassPlain, write ? offsets : nullptr,
+                   write ? counts : nullptr);
+  if (rc) return rc;
+  if (!write) {
+    rc = hip_check(va::launch_csr_offsets(counts, B * Hq * nc, int(nseg), offsets, st),
+                   "offsets launch");
+    if (rc) return rc;
+  }
+  return ok();
 }
 
 // Whether the MFMA attention kernel can run these operands: bf16/fp16, D in

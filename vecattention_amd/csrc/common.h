@@ -223,11 +223,18 @@ struct WorkOrder {
 // (the reference's dense (B, H, nqb, padded_k) layout).
 //   causal:     keys [smin, J*qps) with smin = wo_init ? qps : 0
 //   non-causal: keys [smin, Sk)    with smin = wo_init ? min(qps, Sk) : 0
+// A non-null `csr` selects the compact layout instead: row r = bh*nc + jr
+// holds exactly its selected keys from slot csr[r] on (csr[r+1] - csr[r] of
+// them), as counted by an earlier run of the same selection; with key
+// segments, segment s of the row follows the keys of its earlier segments and
+// holds seg_counts[r*nseg + s] of them.
 // ---------------------------------------------------------------------------
 struct RowLayout {
   int64_t J0, nc, qps, Sk;
   int64_t dense_stride;  // > 0: dense rows
   int causal, wo_init;
+  const int64_t* csr = nullptr;         // compact layout: row offsets (B*Hq*nc + 1)
+  const int32_t* seg_counts = nullptr;  // compact layout: keys per (row, segment)
 
   __host__ __device__ int64_t smin() const {
     if (!wo_init) return 0;
@@ -258,6 +265,32 @@ struct RowLayout {
   __host__ __device__ int64_t block_size() const { return row_in_block(nc); }
   __host__ __device__ int64_t row_offset(int64_t bh, int64_t jr) const {
     return bh * block_size() + row_in_block(jr);
+  }
+  // First slot of row jr of (b, h) (jr == nc: the end of the (b, h) block).
+  __device__ int64_t row_start(int64_t bh, int64_t jr) const {
+    return csr ? csr[bh * nc + jr] : row_offset(bh, jr);
+  }
+  // First slot and number of slots of key segment `seg` (of nseg, keys from
+  // seg_lo on) of row jr: in the capacity layout slot k - smin holds key k;
+  // in the compact layout the segment holds exactly its counted keys.
+  __device__ void segment_slots(int64_t bh, int64_t jr, int seg, int nseg, int64_t seg_lo,
+                                int64_t& start, int64_t& cap) const {
+    if (csr) {
+      const int64_t r = bh * nc + jr;
+      start = csr[r];
+      if (nseg > 1) {
+        for (int s = 0; s < seg; ++s) start += seg_counts[r * nseg + s];
+        cap = seg_counts[r * nseg + seg];
+      } else {
+        cap = csr[r + 1] - csr[r];
+      }
+      return;
+    }
+    const int64_t sm = smin();
+    const int64_t slot = (seg_lo > sm ? seg_lo : sm) - sm;
+    start = row_offset(bh, jr) + slot;
+    const int64_t c = capacity(J0 + jr) - slot;
+    cap = c > 0 ? c : 0;
   }
 };
 

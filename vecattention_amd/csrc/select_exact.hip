@@ -164,8 +164,8 @@ __global__ __launch_bounds__(256) void select_exact_kernel(
         const int64_t jr = jr0 + i;
         const int64_t J = J0 + jr;
         const int64_t lim = klim[i];
-        const int64_t row_off = lay.row_offset(bh, jr);
-        const int64_t cap = lay.capacity(J);
+        int64_t row_off, cap;
+        lay.segment_slots(bh, jr, 0, 1, 0, row_off, cap);
         int32_t c = cnt[i];
         for (int step = 0; step < kSelChunk / 64; ++step) {
           const int kk = step * 64 + lane;
@@ -178,7 +178,7 @@ __global__ __launch_bounds__(256) void select_exact_kernel(
           const uint32_t below = __builtin_amdgcn_mbcnt_hi(
               uint32_t(ballot >> 32), __builtin_amdgcn_mbcnt_lo(uint32_t(ballot), 0u));
           const int64_t pos = int64_t(c) + below;
-          if (sel && pos < cap) indices[row_off + pos] = int32_t(key);
+          if (sel && pos < cap && indices) indices[row_off + pos] = int32_t(key);
           c += __builtin_popcountll(ballot);
         }
         if (lane == 0) cnt[i] = c;
@@ -187,8 +187,9 @@ __global__ __launch_bounds__(256) void select_exact_kernel(
     __syncthreads();
   }
 
-  if (tid < rows_here) {
-    const int64_t cap = lay.capacity(J0 + jr0 + tid);
+  if (tid < rows_here && counts) {
+    int64_t start, cap;
+    lay.segment_slots(bh, jr0 + tid, 0, 1, 0, start, cap);
     const int32_t c = cnt[tid];
     counts[bh * nc + jr0 + tid] = (c < cap) ? c : int32_t(cap);
   }

@@ -142,9 +142,6 @@ __global__ __launch_bounds__(256) void select_mfma_kernel(
     if (lim < kend) kend = lim;
   }
   if (nseg > 1 && seg_lo + segk < kend) kend = seg_lo + segk;
-  // The segment writes its keys from slot kstart - smin of each row (the slot
-  // of its first selectable key): segments never overlap.
-  const int64_t seg_slot = kstart - smin;
   const T* qbase = qs + b * sqb + h * sqh;
   const T* kbh = k + b * skb + hk * skh;
 
@@ -186,9 +183,11 @@ __global__ __launch_bounds__(256) void select_mfma_kernel(
     int64_t lim = 0x7fffffff;
     if (causal) lim = (r == 0) ? (J - 1) * qps + 1 : J * qps;
     klim[tid] = int32_t(lim < 0 ? 0 : (lim > 0x7fffffff ? 0x7fffffff : lim));
-    rowoff[tid] = tid < rows_here ? lay.row_offset(bh, jr) + seg_slot : 0;
-    const int64_t capr = tid < rows_here ? lay.capacity(J) - seg_slot : 0;
-    rowcap[tid] = capr > 0 ? capr : 0;
+    // the segment's slots of the row (segments never overlap)
+    int64_t start = 0, capr = 0;
+    if (tid < rows_here) lay.segment_slots(bh, jr, seg, nseg, seg_lo, start, capr);
+    rowoff[tid] = start;
+    rowcap[tid] = capr;
   }
   // Q^T operands of all 64 rows: row 32*rb + l32, features (D/2)*hh + 8*s.
   vec qop[2][NS];
@@ -526,9 +525,9 @@ __global__ __launch_bounds__(256) void select_mfma_kernel(
     }
     lds_barrier();
 
-    // ================= G: ordered stores =====================================
+    // ================= G: ordered stores (none when only counting) ===========
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb) {
+    for (int rb = 0; rb < 2 && indices; ++rb) {
       const int row = rb * 32 + l32;
       if (row < rows_here) {
         const int64_t row_off = rowoff[row];
@@ -550,7 +549,7 @@ __global__ __launch_bounds__(256) void select_mfma_kernel(
     }
   }
   lds_barrier();
-  if (tid < rows_here) {
+  if (tid < rows_here && counts) {
     const int64_t cap = rowcap[tid];
     const int32_t c = rcnt[tid];
     counts[(bh * nc + jr0 + tid) * nseg + seg] = (c < cap) ? c : int32_t(cap);

@@ -217,21 +217,21 @@ __global__ __launch_bounds__(256, 2) void select_wave_kernel(
   }
 
   // ---- output of this lane's row ------------------------------------------
-  // Segment seg writes its keys from slot max(seg_lo, smin) - smin of the row,
-  // the slot of its first selectable key: segments never overlap.
-  const int seg_slot = (seg_lo > smin ? seg_lo : smin) - smin;
-  const int cap = valid ? int(lay.capacity(J0 + jr)) - seg_slot : 0;
+  // Segment seg writes its keys from its first slot of the row (segments
+  // never overlap); no keys are stored when only counting (indices null).
+  int64_t ostart = 0, ocap = 0;
+  if (valid) lay.segment_slots(bh, jr, seg, nseg, seg_lo, ostart, ocap);
+  const int cap = int(ocap);
   // The keys are stored through a buffer resource over this wave's rows (the
   // rows of one (b, h) are contiguous, at most 32 * 2^24 slots: the byte
   // offsets fit 32 bits).  A lane's offset starts at its row's first slot of
   // the segment and is clamped to the row's last slot, so that no store
   // leaves its row and the loop needs no bounds branch.
-  const int64_t wrow0 = lay.row_offset(bh, jr_wave);
-  const int64_t wrow_end = lay.row_offset(bh, jr_wave + (nvalid_wave > 0 ? nvalid_wave : 0));
-  const __amdgpu_buffer_rsrc_t ors =
-      make_rsrc(indices + wrow0, uint32_t(nvalid_wave > 0 ? (wrow_end - wrow0) * 4 : 0));
-  const uint32_t ofirst =
-      valid ? uint32_t(lay.row_offset(bh, jr) - wrow0 + seg_slot) * 4u : 0xfffffff0u;
+  const int64_t wrow0 = nvalid_wave > 0 ? lay.row_start(bh, jr_wave) : 0;
+  const int64_t wrow_end = nvalid_wave > 0 ? lay.row_start(bh, jr_wave + nvalid_wave) : 0;
+  const __amdgpu_buffer_rsrc_t ors = make_rsrc(
+      indices ? indices + wrow0 : indices, uint32_t(indices ? (wrow_end - wrow0) * 4 : 0));
+  const uint32_t ofirst = valid ? uint32_t(ostart - wrow0) * 4u : 0xfffffff0u;
   const uint32_t olast = valid && cap > 0 ? ofirst + uint32_t(cap - 1) * 4u : 0xfffffff0u;
   int rowcnt = 0;   // keys selected so far for this row
   int listcnt = 0;  // near-max tiles listed for this row
@@ -299,16 +299,20 @@ __global__ __launch_bounds__(256, 2) void select_wave_kernel(
   }
   ambk[wave][64 + lane] = 0;  // resolved flags start cleared
 
+  // Counts block bb's selections of the row and, unless only counting
+  // (indices null), stores them.
   auto append = [&](int kb0, int bb, uint32_t bt) {
     const int cnt = __builtin_popcount(bt);
     const int ocnt = int(other_half(uint32_t(cnt)));
-    uint32_t off = ofirst + uint32_t(rowcnt + (hh ? ocnt : 0)) * 4u;
-    const int key0 = kb0 + 32 * bb + 16 * hh;
-    while (bt) {
-      const int e = __builtin_ctz(bt);
-      bt &= bt - 1;
-      __builtin_amdgcn_raw_buffer_store_b32(key0 + e, ors, off < olast ? off : olast, 0, 0);
-      off += 4u;
+    if (indices) {
+      uint32_t off = ofirst + uint32_t(rowcnt + (hh ? ocnt : 0)) * 4u;
+      const int key0 = kb0 + 32 * bb + 16 * hh;
+      while (bt) {
+        const int e = __builtin_ctz(bt);
+        bt &= bt - 1;
+        __builtin_amdgcn_raw_buffer_store_b32(key0 + e, ors, off < olast ? off : olast, 0, 0);
+        off += 4u;
+      }
     }
     rowcnt += cnt + ocnt;
   };
@@ -704,7 +708,7 @@ __global__ __launch_bounds__(256, 2) void select_wave_kernel(
     return;
   }
 
-  if (valid && hh == 0) counts[(bh * nc + jr) * nseg + seg] = rowcnt < cap ? rowcnt : (cap > 0 ? cap : 0);
+  if (valid && hh == 0 && counts) counts[(bh * nc + jr) * nseg + seg] = rowcnt < cap ? rowcnt : cap;
 }
 
 // Segment length the splits aim for: Sk / 16 keys, within [2048, 4096].  Short

@@ -153,6 +153,52 @@ def select_segments(qs_chunk, k, J0, gap, gaps, causal, q_pooling_size, k_local_
     return counts, indices
 
 
+def select_csr(qs_chunk, k, J0, gap, gaps, causal, q_pooling_size, k_local_size, group_k_block,
+               wo_init, segk=0, bsq=None):
+    """TilingSelect into the compact (CSR) layout: returns (counts, offsets,
+    indices) with offsets (B*Hq*nc + 1,) int64 and row r = (b*Hq + h)*nc + jr
+    holding its keys, ascending, at indices[offsets[r]:offsets[r+1]].  counts
+    is (B, Hq, nc) int32, or (B, Hq, nc, nseg) with segk > 0 (the split of
+    select_segments).  Two library calls: the counting one, a read of the
+    total (one host synchronisation, to size `indices`), the writing one.
+    """
+    if qs_chunk.stride(-1) != 1:
+        qs_chunk = qs_chunk.contiguous()
+    if k.stride(-1) != 1:
+        k = k.contiguous()
+    B, Hq, nc, D = qs_chunk.shape
+    Hk, Sk = k.shape[1], k.shape[2]
+    if bsq is None:
+        bsq = reference_block_size_q(q_pooling_size, k_local_size, group_k_block, D, causal)
+    if segk:
+        counts = torch.empty(B, Hq, nc, -(-Sk // segk), dtype=torch.int32, device=k.device)
+        nscr = int(nat.lib().va_select_segments_scratch_floats(B, Hq, Hk, Sk, nc, segk,
+                                                                k_local_size, group_k_block))
+    else:
+        counts = torch.empty(B, Hq, nc, dtype=torch.int32, device=k.device)
+        nscr = int(nat.lib().va_select_scratch_floats(B, Hk))
+    if nscr < 0:
+        raise AssertionError("scratch size query: invalid sizes")
+    scratch = torch.empty(max(nscr, 1), dtype=torch.float32, device=k.device)
+    offsets = torch.empty(B * Hq * nc + 1, dtype=torch.int64, device=k.device)
+
+    def call(indices):
+        with torch.cuda.device(k.device):
+            rc = nat.lib().va_select_csr(
+                nat.dtype_code(k), nat.ptr(qs_chunk), qs_chunk.stride(0), qs_chunk.stride(1),
+                qs_chunk.stride(2), nat.ptr(k), k.stride(0), k.stride(1), k.stride(2), B, Hq, Hk,
+                Sk, D, q_pooling_size, k_local_size, group_k_block, int(causal), int(wo_init), J0,
+                nc, bsq, float(gap), nat.ptr(gaps), segk, nat.ptr(counts), nat.ptr(offsets),
+                nat.ptr(indices), nat.ptr(scratch), nscr, _stream(k))
+        nat.check("va_select_csr", rc)
+
+    call(None)
+    total = int(offsets[-1].item())
+    indices = torch.empty(max(total, 1), dtype=torch.int32, device=k.device)
+    call(indices)
+    return counts, offsets, indices[:total]
+
+
 def sparse_attention(q, k, v, out, J0, nc, counts, indices, causal, q_pooling_size, wo_init=None,
                      dense_stride=0, softmax_scale=None, kernel=nat.VA_ATTN_AUTO, segk=0):
     """Vector-sparse attention of q-block rows [J0, J0+nc) into `out` (B, Hq, Sq, D).
