@@ -14,7 +14,8 @@
 // or 64): each score is the quad's four partial dot products added with two
 // lane swaps, so the four lanes hold the same score and run the same online
 // softmax.  A work-group covers 64 rows of a q-block; every key row is read by
-// all quads of the work-group at once, so loads broadcast through L1.
+// all quads of the work-group at once, so loads broadcast through L1, and the
+// keys are taken in batches whose loads are issued together.
 //
 // dense_qoff >= 0: every key instead (KeyList::dense, causal rows aligned at
 // offset dense_qoff).  stats != nullptr: no V; row i of head bh writes
@@ -85,25 +86,70 @@ __global__ __launch_bounds__(4 * kSimpleRows) void attn_simple_kernel(
   const T* vh = v + b * svb + hk * svh;
   float m = -__builtin_inff(), l = 0.f;
   const int64_t n = kl.total();
-  for (int64_t p = 0; p < n; ++p) {
-    const int64_t key = kl.key(p);  // the same key in every lane of the work-group
-    if (key < 0 || key >= Sk) continue;  // never read outside K / V
-    const T* kr = kh + key * sks + d0;
-    float s = 0.f;
+  // Keys in batches of NB: the batch's K rows are loaded together, the online
+  // softmax rescales once per batch (by the batch maximum), then the V rows
+  // are loaded together, so a batch waits on memory twice instead of each key
+  // twice.  A masked slot (past the list, outside [0, Sk), or after the row on
+  // the diagonal block) reads key row 0 and weighs 0.
+  constexpr int NB = DQ <= 16 ? 8 : (DQ <= 32 ? 4 : 2);
+  for (int64_t p0 = 0; p0 < n; p0 += NB) {
+    int64_t key[NB];
+    bool ok[NB];
+    const int64_t c0 = kl.n_init + kl.n_diag;  // first position of the selected columns
+    if (p0 >= c0 && p0 + NB <= n) {
+      // a whole batch of selected columns (every batch of a non-causal row):
+      // its ids in one block of consecutive (scalar) loads
 #pragma unroll
-    for (int i = 0; i < DQ; ++i) s += (kFull || d0 + i < D) ? qv[i] * to_f32(kr[i]) : 0.f;
-    s = quad_sum(s) * scale_log2;
-    if (causal && kl.is_diag(p) && key > qkey) continue;  // (after the swaps: whole quads)
-    const float m_new = __builtin_fmaxf(m, s);
-    const float alpha = __builtin_amdgcn_exp2f(m - m_new);
-    const float pe = __builtin_amdgcn_exp2f(s - m_new);
-    l = l * alpha + pe;
-    m = m_new;
+      for (int j = 0; j < NB; ++j) {
+        const int64_t kk = kl.cols[p0 - c0 + j];
+        ok[j] = kk >= 0 && kk < Sk;
+        key[j] = ok[j] ? kk : 0;
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < NB; ++j) {
+        const int64_t p = p0 + j;
+        const int64_t kk = p < n ? kl.key(p) : -1;  // the same key in every lane of the work-group
+        ok[j] = kk >= 0 && kk < Sk && !(causal && kl.is_diag(p) && kk > qkey);
+        key[j] = ok[j] ? kk : 0;
+      }
+    }
+    float s[NB];
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      const T* kr = kh + key[j] * sks + d0;
+      float a = 0.f;
+#pragma unroll
+      for (int i = 0; i < DQ; ++i) a += (kFull || d0 + i < D) ? qv[i] * to_f32(kr[i]) : 0.f;
+      s[j] = a;
+    }
+    float mb = m;
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      s[j] = quad_sum(s[j]) * scale_log2;  // the quad's four lanes share the row: same ok[j]
+      if (ok[j]) mb = __builtin_fmaxf(mb, s[j]);
+    }
+    // a batch with no key of the row so far leaves (m, l, acc) unchanged
+    const bool any = mb != -__builtin_inff();
+    const float alpha = any ? __builtin_amdgcn_exp2f(m - mb) : 1.f;
+    float pe[NB], ps = 0.f;
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      pe[j] = ok[j] ? __builtin_amdgcn_exp2f(s[j] - mb) : 0.f;
+      ps += pe[j];
+    }
+    l = l * alpha + ps;
+    m = mb;
     if (stats) continue;
-    const T* vr = vh + key * svs + d0;
 #pragma unroll
-    for (int i = 0; i < DQ; ++i)
-      if (kFull || d0 + i < D) acc[i] = acc[i] * alpha + pe * to_f32(vr[i]);
+    for (int i = 0; i < DQ; ++i) acc[i] *= alpha;
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      const T* vr = vh + key[j] * svs + d0;
+#pragma unroll
+      for (int i = 0; i < DQ; ++i)
+        if (kFull || d0 + i < D) acc[i] += pe[j] * to_f32(vr[i]);
+    }
   }
   if (!live) return;
   if (stats) {
