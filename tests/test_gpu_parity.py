@@ -144,6 +144,10 @@ SELECT_CASES = [
      None),
     ("bf16-causal-qps128-bk32-G1-chunked", 2, 4, 1, 1800, 128, torch.bfloat16, True, 128, 32, 1,
      0.10, 6),
+    # tiny key ranges: groups wholly past Sk inside the last chunk
+    ("bf16-causal-bk16-G1-S200", 1, 2, 1, 200, 64, torch.bfloat16, True, 64, 16, 1, 0.30, None),
+    ("fp16-noncausal-bk16-G2-S130", 1, 2, 2, 130, 64, torch.float16, False, 64, 16, 2, 0.50,
+     None),
 ]
 
 
