@@ -35,7 +35,7 @@ import torch  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
-FP32_PEAK_TFLOPS = 157.3  # MI355X vector fp32 (the fp32 workload's per-row attention kernel)
+FP32_PEAK_TFLOPS = 157.3  # MI355X fp32: dense matrix cores (and packed vector fp32)
 FP64_PEAK_TFLOPS = 78.6   # MI355X fp64 (the exact selection kernel)
 METRIC = "prefill attn latency (ms) + effective TFLOPS at 32k/128k; speedup vs dense"
 
@@ -697,9 +697,8 @@ def measure_prefill(args, wl, dev, with_cpu):
     if not args.no_dense:
         dense_ms, dense_backend = time_dense(wl, q, k, v)
         print(f"[bench] dense SDPA ({dense_backend}): {dense_ms} ms", file=sys.stderr, flush=True)
-        if wl.dtype != torch.float32:
-            dense_va_ms = time_dense_va(wl, q, k, v)
-            print(f"[bench] dense va_dense_attn: {dense_va_ms:.3f} ms", file=sys.stderr, flush=True)
+        dense_va_ms = time_dense_va(wl, q, k, v)
+        print(f"[bench] dense va_dense_attn: {dense_va_ms:.3f} ms", file=sys.stderr, flush=True)
 
     t_sel_total = t_pool + t_sel
     # value: the whole VecAttention_prefill step, as timed above
@@ -708,8 +707,11 @@ def measure_prefill(args, wl, dev, with_cpu):
     from vecattention_amd import _native as nat
     plan = prefill_plan(wl, q, k, v, out)
     attn_mfma = bool(plan & nat.VA_KERNELS_ATTN_MFMA)
-    attn_kernel = "attn_mfma_kernel" if attn_mfma else "attn_simple_kernel"
+    attn_f32 = bool(plan & nat.VA_KERNELS_ATTN_F32)
+    attn_kernel = ("attn_mfma_kernel" if attn_mfma else "attn_f32_kernel" if attn_f32
+                   else "attn_simple_kernel")
     attn_peak = BF16_PEAK_TFLOPS if attn_mfma else FP32_PEAK_TFLOPS
+    attn_bound = "mfma" if attn_mfma else "mfma-fp32" if attn_f32 else "valu-fp32"
     # Selection (pooling + TilingSelect) against max(Bytes_sel / HBM peak,
     # F_sel / the scoring kernel's peak): F_sel = 2*D per selectable (row, key).
     F_sel = 2.0 * wl.D * selectable(wl, S)
@@ -766,7 +768,7 @@ def measure_prefill(args, wl, dev, with_cpu):
         "dense_va_ms": None if dense_va_ms is None else round(dense_va_ms, 4),
         "dense_va_tflops": None if dense_va_ms is None else round(F_dense / (dense_va_ms * 1e-3) / 1e12, 1),
         "speedup_vs_dense_va": None if dense_va_ms is None else round(dense_va_ms / ms_per_step, 3),
-        "roofline": {"bound": "mfma" if attn_mfma else "valu-fp32", "kernel": attn_kernel,
+        "roofline": {"bound": attn_bound, "kernel": attn_kernel,
                      "achieved": round(attn_tflops, 3), "peak": attn_peak,
                      "unit": "TFLOP/s", "frac": round(attn_tflops / attn_peak, 4),
                      "traffic": traffic,

@@ -200,7 +200,10 @@ int64_t va_select_row_offset(int64_t Sk, int64_t q_pooling_size, int causal, int
  * spattn/src/VecAttention.py:104-121 (vertical + local-block semantics of
  * spattn/threshold/model_tuner.py:193-216).  Rows with no key are 0.
  * `kernel`: VA_ATTN_AUTO (MFMA for bf16/fp16, D in {64,128}, qps in {64,128};
- * otherwise the per-row kernel), VA_ATTN_MFMA or VA_ATTN_SIMPLE.  The MFMA
+ * for fp32 with the same D and qps and 16-byte aligned rows the fp32
+ * matrix-core kernel (v_mfma_f32_32x32x2_f32, fp32 throughout); otherwise the
+ * per-row kernel), VA_ATTN_MFMA (either matrix-core kernel, by dtype) or
+ * VA_ATTN_SIMPLE (the per-row kernel).  The bf16/fp16 MFMA
  * kernel's loop has two forms at D = 128, qps = 64, which VA_ATTN_AUTO and
  * VA_ATTN_MFMA pick by shape: staged (two stages of a K and a V tile, two
  * work-groups per CU) and ring (three tile slots, three work-groups per CU);
@@ -223,7 +226,8 @@ int va_sparse_attn(int dtype, const void* q, int64_t sqb, int64_t sqh, int64_t s
  * spattn/src/Fullprefill.py:4-16 (Full_prefill, flashinfer
  * single_prefill_with_kv_cache), which the dispatcher at
  * spattn/src/models/utils.py:99-128 calls on the text tokens around a vision
- * span.  bf16/fp16, D in {64, 128}; GQA as in va_sparse_attn.
+ * span.  bf16/fp16, or fp32 on the fp32 matrix-core kernel (16-byte aligned
+ * rows); D in {64, 128}; GQA as in va_sparse_attn.
  */
 int va_dense_attn(int dtype, const void* q, int64_t sqb, int64_t sqh, int64_t sqs,
                   const void* k, int64_t skb, int64_t skh, int64_t sks, const void* v,
@@ -327,9 +331,11 @@ int64_t va_prefill_workspace_size(int dtype, int64_t B, int64_t Hq, int64_t Sq, 
  * {64, 128}, k_local_size outside {16, 32, 64, 128, 256}, unaligned K; the
  * wave kernel takes tiles of 16 to 64 keys, the 64-row MFMA kernel 128 and
  * 256); the attention on
- * the MFMA kernel (VA_KERNELS_ATTN_MFMA) or the per-row kernel
- * (VA_KERNELS_ATTN_ROW: fp32, D or q_pooling_size outside {64, 128}, K/V row
- * strides of 16 KiB or more, unaligned tensors), with VA_KERNELS_ATTN_RING
+ * the MFMA kernel (VA_KERNELS_ATTN_MFMA), for fp32 inputs the fp32 matrix-core
+ * kernel (VA_KERNELS_ATTN_F32: D and q_pooling_size 64 or 128, 16-byte
+ * aligned rows), or the per-row kernel (VA_KERNELS_ATTN_ROW: D or
+ * q_pooling_size outside {64, 128}, K/V row strides of 16 KiB or more,
+ * unaligned tensors), with VA_KERNELS_ATTN_RING
  * when that kernel runs its ring form (see va_sparse_attn); VA_KERNELS_SPLIT
  * when the selection runs in key segments.  The exact selection and the per-row
  * attention are several times slower than the MFMA kernels.  No counterpart
@@ -342,6 +348,7 @@ int64_t va_prefill_workspace_size(int dtype, int64_t B, int64_t Hq, int64_t Sq, 
 #define VA_KERNELS_ATTN_ROW 32
 #define VA_KERNELS_SPLIT 64
 #define VA_KERNELS_ATTN_RING 128
+#define VA_KERNELS_ATTN_F32 256
 int va_prefill_kernels(int dtype, const void* q, int64_t sqb, int64_t sqh, int64_t sqs,
                        const void* k, int64_t skb, int64_t skh, int64_t sks, const void* v,
                        int64_t svb, int64_t svh, int64_t svs, const void* out, int64_t sob,

@@ -440,6 +440,10 @@ ATTN_CASES = [
     ("fp16-noncausal-d128", 2, 4, 2, 1100, 1100, 128, torch.float16, False, 64, 0.15),
     ("bf16-noncausal-sq-ne-sk", 1, 4, 4, 700, 1300, 128, torch.bfloat16, False, 64, 0.2),
     ("fp32-noncausal-d64", 1, 4, 4, 1024, 1024, 64, torch.float32, False, 64, 0.1),
+    # fp32 on the fp32 matrix-core kernel (auto) and the per-row kernel (simple)
+    ("fp32-causal-gqa-d128-qps128", 1, 4, 2, 1000, 1000, 128, torch.float32, True, 128, 0.1),
+    ("fp32-causal-batch2-tail-d64", 2, 4, 2, 1100, 1100, 64, torch.float32, True, 64, 0.1),
+    ("fp32-noncausal-sq-ne-sk-d128", 1, 2, 2, 700, 1300, 128, torch.float32, False, 64, 0.2),
 ]
 
 
@@ -495,6 +499,32 @@ def test_sparse_attention_matches_oracle(device, case, kernel):
     err = np.abs(out.float().cpu().numpy() - want)
     tol = (ATOL_MAX_F32, ATOL_MEAN_F32) if dtype == torch.float32 else (ATOL_MAX, ATOL_MEAN)
     assert err.max() <= tol[0] and err.mean() <= tol[1], (err.max(), err.mean())
+
+
+def test_fp32_matrix_core_attention_equals_per_row_kernel(device):
+    # fp32 inputs: the fp32 matrix-core kernel (VA_ATTN_MFMA) and the per-row
+    # kernel agree to fp32 rounding on the same lists, and the prefill plan
+    # reports the matrix-core kernel.
+    case = ("fp32-causal-gqa-d64", 1, 4, 2, 1536, 1536, 64, torch.float32, True, 64, 0.1)
+    name, B, Hq, Hk, Sq, Sk, D, dtype, causal, qps, keep = case
+    note("attn fp32 mfma vs per-row")
+    q, k, v = make_inputs(B, Hq, Hk, Sq, D, dtype, seed=17)
+    nqb, lists, cnt, idx = _oracle_lists_as_layout(q, k, case)
+    qd, kd, vd = q.to(device), k.to(device), v.to(device)
+    outs = []
+    for kernel in (nat.VA_ATTN_MFMA, nat.VA_ATTN_SIMPLE):
+        out = torch.zeros(B, Hq, Sq, D, dtype=dtype, device=device)
+        stages.sparse_attention(qd, kd, vd, out, 0, nqb, cnt.to(device), idx.to(device), causal,
+                                qps, kernel=kernel)
+        outs.append(out.cpu())
+    d = (outs[0] - outs[1]).abs()
+    assert float(d.max()) <= 2e-5 and float(d.mean()) <= 2e-6, (float(d.max()), float(d.mean()))
+    flags = nat.lib().va_prefill_kernels(
+        nat.VA_F32, nat.ptr(qd), qd.stride(0), qd.stride(1), qd.stride(2), nat.ptr(kd),
+        kd.stride(0), kd.stride(1), kd.stride(2), nat.ptr(vd), vd.stride(0), vd.stride(1),
+        vd.stride(2), nat.ptr(qd), qd.stride(0), qd.stride(1), qd.stride(2), Hq, Hk, Sk, D, qps,
+        16, 16)
+    assert flags & nat.VA_KERNELS_ATTN_F32 and not flags & nat.VA_KERNELS_ATTN_ROW
 
 
 @pytest.mark.parametrize("case", [c for c in ATTN_CASES if c[6] == 128 and c[9] == 64 and

@@ -176,7 +176,10 @@ def test_dense_attn_argument_errors_before_launch(L):
     assert _dense(L, Sq=400) == nat.VA_ERR_ARG                 # causal needs Sq <= Sk
     assert _dense(L, Hk=3) == nat.VA_ERR_ARG
     assert _dense(L, Sk=0) == nat.VA_ERR_ARG
-    assert _dense(L, dtype=nat.VA_F32) == nat.VA_ERR_UNSUPPORTED
+    # fp32 runs on the fp32 matrix-core kernel: D 64 or 128, 16-byte aligned rows
+    assert _dense(L, dtype=nat.VA_F32, D=96) == nat.VA_ERR_UNSUPPORTED
+    assert _dense(L, dtype=nat.VA_F32, sks=130) == nat.VA_ERR_UNSUPPORTED
+    assert _dense(L, dtype=nat.VA_F32, out=260) == nat.VA_ERR_UNSUPPORTED
     assert _dense(L, D=256) == nat.VA_ERR_UNSUPPORTED
     assert _dense(L, sks=1 << 14) == nat.VA_ERR_UNSUPPORTED   # row stride past the 14-bit field
     assert _dense(L, scale=-1.0) == nat.VA_ERR_UNSUPPORTED
@@ -292,9 +295,11 @@ def test_prefill_kernels_reports_the_slow_paths(L):
     assert _plan(L, bk=128, G=8192) == (nat.VA_KERNELS_SELECT_MFMA | nat.VA_KERNELS_ATTN_MFMA |
                                         nat.VA_KERNELS_ATTN_RING)
     assert _plan(L, bk=512, G=1) & nat.VA_KERNELS_SELECT_EXACT
-    # fp32 inputs: exact selection and the per-row attention
+    # fp32 inputs: exact selection and the fp32 matrix-core attention; the
+    # per-row attention for a head_dim that kernel does not take
     f = _plan(L, dtype=nat.VA_F32)
-    assert f == nat.VA_KERNELS_SELECT_EXACT | nat.VA_KERNELS_ATTN_ROW
+    assert f == nat.VA_KERNELS_SELECT_EXACT | nat.VA_KERNELS_ATTN_F32
+    assert _plan(L, dtype=nat.VA_F32, D=96) == nat.VA_KERNELS_SELECT_EXACT | nat.VA_KERNELS_ATTN_ROW
     # head_dim 96: neither MFMA kernel
     f = _plan(L, D=96)
     assert f & nat.VA_KERNELS_SELECT_EXACT and f & nat.VA_KERNELS_ATTN_ROW

@@ -20,7 +20,7 @@ VA_ATTN_MFMA_STAGED, VA_ATTN_MFMA_RING = 3, 4  # forms of the MFMA kernel's loop
 VA_SEL_AUTO, VA_SEL_EXACT, VA_SEL_MFMA, VA_SEL_WAVE = 0, 1, 2, 3
 VA_KERNELS_SELECT_WAVE, VA_KERNELS_SELECT_MFMA, VA_KERNELS_SELECT_EXACT = 1, 2, 4
 VA_KERNELS_ATTN_MFMA, VA_KERNELS_ATTN_ROW, VA_KERNELS_SPLIT = 16, 32, 64
-VA_KERNELS_ATTN_RING = 128
+VA_KERNELS_ATTN_RING, VA_KERNELS_ATTN_F32 = 128, 256
 
 _DTYPES = {torch.float32: VA_F32, torch.bfloat16: VA_BF16, torch.float16: VA_F16}
 

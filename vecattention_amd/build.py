@@ -14,7 +14,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libvecattn.so")
 SOURCES = ["pool.hip", "select_exact.hip", "select_mfma.hip", "select_wave.hip", "key_norm.hip",
-           "attn_simple.hip", "attn_mfma.hip", "decode.hip", "csr.hip", "api.hip", "noalloc.hip"]
+           "attn_simple.hip", "attn_mfma.hip", "attn_f32.hip", "decode.hip", "csr.hip", "api.hip", "noalloc.hip"]
 ARCH = os.environ.get("VA_OFFLOAD_ARCH", "gfx950")
 
 # -packed-fp32-ops: no v_pk_{add,mul,fma}_f32 are generated (they have given

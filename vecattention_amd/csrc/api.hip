@@ -60,6 +60,13 @@ hipError_t launch_attn_mfma(int dtype, int64_t D, int64_t qps, const void* q, co
                             int nseg, int segk, int64_t dense_qoff, float* stats, int form,
                             hipStream_t stream);
 bool attn_mfma_ring_supported(int dtype, int64_t D, int64_t qps);
+bool attn_f32_supported(int64_t D, int64_t qps);
+hipError_t launch_attn_f32(const void* q, const int64_t* sq, const void* k, const int64_t* sk,
+                           const void* v, const int64_t* sv, void* out, const int64_t* so,
+                           int64_t B, int64_t Hq, int64_t Hk, int64_t Sq, int64_t Sk, int64_t D,
+                           int64_t qps, int causal, float scale_log2, const int32_t* counts,
+                           const int32_t* indices, const RowLayout& lay, int64_t dense_qoff,
+                           hipStream_t stream);
 bool ring_form_preferred(int64_t Hq, int64_t Hk, int64_t Sk, int64_t D);
 hipError_t launch_attn_split(int dtype, int64_t D, const void* q, const int64_t* sq,
                              const void* k, const int64_t* sk, const void* v, const int64_t* sv,
@@ -509,6 +516,20 @@ static AttnMfmaCheck attn_mfma_check(int dtype, const void* q, const int64_t* sq
   return c;
 }
 
+// Whether the fp32 matrix-core attention takes these operands: fp32, D in
+// {64, 128}, qps in {64, 128}, rows 16-byte aligned (it loads float4 runs of
+// Q, K and V rows and stores float4 runs of output rows).
+static bool attn_f32_ok(int dtype, const void* q, const int64_t* sq, const void* k,
+                        const int64_t* sk, const void* v, const int64_t* sv, const void* out,
+                        const int64_t* so, int64_t D, int64_t qps) {
+  auto aligned = [](const void* p, const int64_t* st) {
+    return reinterpret_cast<uintptr_t>(p) % 16 == 0 && st[0] % 4 == 0 && st[1] % 4 == 0 &&
+           st[2] % 4 == 0;
+  };
+  return dtype == VA_F32 && va::attn_f32_supported(D, qps) && aligned(q, sq) && aligned(k, sk) &&
+         aligned(v, sv) && aligned(out, so);
+}
+
 static int attn_dispatch(int dtype, const void* q, const int64_t* sq, const void* k,
                          const int64_t* sk, const void* v, const int64_t* sv, void* out,
                          const int64_t* so, int64_t B, int64_t Hq, int64_t Hk, int64_t Sq,
@@ -530,7 +551,18 @@ static int attn_dispatch(int dtype, const void* q, const int64_t* sq, const void
     form = kernel == VA_ATTN_MFMA_RING ? va::kAttnFormRing : va::kAttnFormStaged;
     kernel = VA_ATTN_MFMA;
   }
-  if (kernel == VA_ATTN_MFMA) {
+  // fp32 inputs: the fp32 matrix-core kernel (attention output, one key
+  // segment), else the per-row kernel
+  const bool f32 = !stats && nseg <= 1 && attn_f32_ok(dtype, q, sq, k, sk, v, sv, out, so, D, qps);
+  bool use_f32 = false;
+  if (form != va::kAttnFormAuto && dtype == VA_F32)
+    return fail(VA_ERR_UNSUPPORTED, "the staged and ring forms are the bf16/fp16 MFMA kernel's");
+  if (kernel == VA_ATTN_MFMA && dtype == VA_F32) {
+    if (!f32)
+      return fail(VA_ERR_UNSUPPORTED, "fp32 MFMA attention needs D in {64,128}, qps in {64,128}, "
+                                      "16-byte aligned rows and attention output");
+    use_f32 = true;
+  } else if (kernel == VA_ATTN_MFMA) {
     if (!mfma_shape)
       return fail(VA_ERR_UNSUPPORTED, "MFMA attention needs bf16/fp16, D in {64,128}, qps in {64,128}");
     if (!mfma_align) return fail(VA_ERR_UNSUPPORTED, "MFMA attention needs 16-byte aligned rows");
@@ -542,12 +574,17 @@ static int attn_dispatch(int dtype, const void* q, const int64_t* sq, const void
     use_mfma = true;
   } else if (kernel == VA_ATTN_AUTO) {
     use_mfma = mfma_shape && mfma_align && mfma_span && softmax_scale > 0.f;
+    use_f32 = !use_mfma && f32;
   } else if (kernel != VA_ATTN_SIMPLE) {
     return fail(VA_ERR_ARG, "unknown kernel selector %d", kernel);
   }
   if (!use_mfma && qps > 1024) return fail(VA_ERR_UNSUPPORTED, "q_pooling_size > 1024");
   if (!use_mfma && nseg > 1)
     return fail(VA_ERR_UNSUPPORTED, "segmented key lists need the MFMA attention kernel");
+  if (use_f32)
+    return hip_check(va::launch_attn_f32(q, sq, k, sk, v, sv, out, so, B, Hq, Hk, Sq, Sk, D, qps,
+                                         causal, scale_log2, counts, indices, lay, -1, stream),
+                     "attention launch");
   hipError_t e = use_mfma
                      ? va::launch_attn_mfma(dtype, D, qps, q, sq, k, sk, v, sv, out, so, B, Hq,
                                             Hk, Sq, Sk, causal, scale_log2, counts, indices, lay,
@@ -615,9 +652,21 @@ int va_dense_attn(int dtype, const void* q, int64_t sqb, int64_t sqh, int64_t sq
   if (nc * B * Hq > kMaxGrid) return fail(VA_ERR_UNSUPPORTED, "grid too large");
   const int64_t sq[3] = {sqb, sqh, sqs}, sk[3] = {skb, skh, sks}, sv[3] = {svb, svh, svs},
                 so[3] = {sob, soh, sos};
+  if (dtype == VA_F32) {  // the fp32 matrix-core kernel over every key
+    if (!attn_f32_ok(dtype, q, sq, k, sk, v, sv, out, so, D, qps))
+      return fail(VA_ERR_UNSUPPORTED, "fp32 dense attention needs D in {64, 128} and 16-byte "
+                                      "aligned rows");
+    const va::RowLayout lay = make_layout(0, nc, qps, Sk, causal, 0, 0);
+    const int rc = hip_check(
+        va::launch_attn_f32(q, sq, k, sk, v, sv, out, so, B, Hq, Hk, Sq, Sk, D, qps, causal,
+                            softmax_scale * 1.4426950408889634f, nullptr, nullptr, lay,
+                            causal ? Sk - Sq : 0, static_cast<hipStream_t>(stream)),
+        "dense attention launch");
+    return rc ? rc : ok();
+  }
   const AttnMfmaCheck chk = attn_mfma_check(dtype, q, sq, k, sk, v, sv, out, so, Sk, D, qps);
   if (!chk.shape)
-    return fail(VA_ERR_UNSUPPORTED, "dense attention needs bf16/fp16 and D in {64, 128}");
+    return fail(VA_ERR_UNSUPPORTED, "dense attention needs bf16/fp16/fp32 and D in {64, 128}");
   if (!chk.align) return fail(VA_ERR_UNSUPPORTED, "dense attention needs 16-byte aligned rows");
   if (!chk.span)
     return fail(VA_ERR_UNSUPPORTED, "dense attention needs Sk < 2^24, K/V row strides < 16 KiB "
@@ -911,7 +960,9 @@ int va_prefill_kernels(int dtype, const void* q, int64_t sqb, int64_t sqh, int64
   const int64_t sq[3] = {sqb, sqh, sqs}, sk[3] = {skb, skh, sks}, sv[3] = {svb, svh, svs},
                 so[3] = {sob, soh, sos};
   const bool attn = attn_mfma_check(dtype, q, sq, k, sk, v, sv, out, so, Sk, D, qps).ok();
-  flags |= attn ? VA_KERNELS_ATTN_MFMA : VA_KERNELS_ATTN_ROW;
+  flags |= attn ? VA_KERNELS_ATTN_MFMA
+                : attn_f32_ok(dtype, q, sq, k, sk, v, sv, out, so, D, qps) ? VA_KERNELS_ATTN_F32
+                                                                           : VA_KERNELS_ATTN_ROW;
   if (attn && va::attn_mfma_ring_supported(dtype, D, qps) && va::ring_form_preferred(Hq, Hk, Sk, D))
     flags |= VA_KERNELS_ATTN_RING;
   if (attn && (flags & (VA_KERNELS_SELECT_WAVE | VA_KERNELS_SELECT_MFMA))) {

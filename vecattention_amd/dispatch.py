@@ -79,7 +79,7 @@ def Full_prefill(query_states: torch.Tensor, key_states: torch.Tensor,
 
     Causal rows see keys up to ``i + Sk - Sq`` (the last query aligned with the
     last key, flashinfer's convention for Sq < Sk).  Key/value heads may divide
-    the query heads (GQA).  bf16/fp16, head_dim 64 or 128.
+    the query heads (GQA).  bf16/fp16/fp32, head_dim 64 or 128.
     """
     if query_states.dim() != 4 or key_states.dim() != 4 or value_states.dim() != 4:
         raise AssertionError("query/key/value must be (batch, heads, seq, head_dim)")
