@@ -215,6 +215,23 @@ def test_select_big_tiles_bit_exact(device, case, kernel):
     _select_case(device, case, kernel)
 
 
+# Small grids on the exact kernel: B*Hq*ceil(nc/R) < 256 work-groups for R = 4
+# takes 2 rows (R=2: 1 x 4 heads x 128 rows) or 1 row per work-group (A's 64
+# rows, and a causal chunked case).
+EXACT_SMALL_GRID_CASES = [
+    # name, B, Hq, Hk, S, D, dtype, causal, qps, bk, G, keep, chunk_rows
+    ("fp32-noncausal-2rows", 1, 4, 4, 8192, 64, torch.float32, False, 64, 16, 16, 0.10, None),
+    ("fp32-causal-1row-chunked", 1, 2, 1, 2500, 64, torch.float32, True, 64, 16, 16, 0.10, 13),
+    ("bf16-noncausal-1row-G8192", 1, 2, 2, 1900, 128, torch.bfloat16, False, 64, 16, 8192, 0.15,
+     None),
+]
+
+
+@pytest.mark.parametrize("case", EXACT_SMALL_GRID_CASES, ids=[c[0] for c in EXACT_SMALL_GRID_CASES])
+def test_select_exact_small_grids(device, case):
+    _select_case(device, case, nat.VA_SEL_EXACT)
+
+
 def _select_case(device, case, kernel):
     name, B, Hq, Hk, S, D, dtype, causal, qps, bk, G, keep, chunk_rows = case
     note("select", name, kernel)

@@ -27,9 +27,9 @@ namespace va {
 constexpr int kSelChunk = 256;   // keys per inner chunk (== blockDim.x)
 constexpr int kSelMaxD = 256;
 
-// kSelRows: pooled rows per work-group (16, 8 or 4: the host takes the most
-// rows that still give at least 256 work-groups, since each work-group walks
-// every key of its rows).
+// kSelRows: pooled rows per work-group (16, 8, 4, 2 or 1: the host takes the
+// most rows that still give at least 256 work-groups, since each work-group
+// walks every key of its rows; small grids take one row per work-group).
 template <typename T, int kSelRows>
 __global__ __launch_bounds__(256) void select_exact_kernel(
     const T* __restrict__ qs, int64_t sqb, int64_t sqh, int64_t sqn, const T* __restrict__ k,
@@ -215,7 +215,9 @@ static hipError_t launch_select_exact_t(
   constexpr int64_t kMinGroups = 256;
   if ((lay.nc + 15) / 16 * B * Hq >= kMinGroups) return launch(std::integral_constant<int, 16>{});
   if ((lay.nc + 7) / 8 * B * Hq >= kMinGroups) return launch(std::integral_constant<int, 8>{});
-  return launch(std::integral_constant<int, 4>{});
+  if ((lay.nc + 3) / 4 * B * Hq >= kMinGroups) return launch(std::integral_constant<int, 4>{});
+  if ((lay.nc + 1) / 2 * B * Hq >= kMinGroups) return launch(std::integral_constant<int, 2>{});
+  return launch(std::integral_constant<int, 1>{});
 }
 
 hipError_t launch_select_exact(int dtype, const void* qs, int64_t sqb, int64_t sqh,
