@@ -221,8 +221,10 @@ def run_stages(wl, q, k, v, gap, out, events=None):
     from vecattention_amd import stages
     qps, S = wl.q_pooling_size, q.shape[2]
     # the key segments the prefill uses, when its plan splits the selection
-    split = prefill_plan(wl, q, k, v, out) & nat.VA_KERNELS_SPLIT
-    segk = stages.segment_keys(k.shape[2], wl.k_local_size, wl.group_k_block) if split else 0
+    plan = prefill_plan(wl, q, k, v, out)
+    exact = bool(plan & nat.VA_KERNELS_SELECT_EXACT)
+    segk = (stages.segment_keys(k.shape[2], wl.k_local_size, wl.group_k_block, exact=exact)
+            if plan & nat.VA_KERNELS_SPLIT else 0)
     ev = events
     if ev is not None:
         ev["p0"].record()

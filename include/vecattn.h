@@ -124,9 +124,10 @@ int va_select(int dtype, const void* qs, int64_t sqb, int64_t sqh, int64_t sqn,
  * counts[((b*Hq + h)*nc + (J - J0))*nseg + s], nseg = ceil(Sk / segment_keys);
  * a row's list is the concatenation of its segments.  Runs on the VA_SEL_WAVE
  * kernel where its conditions hold, else on the 64-row MFMA kernel (VA_SEL_MFMA
- * conditions, one pass, segment_keys a multiple of 256).  No counterpart in
- * the reference (its single launch writes dense rows); the selected sets are
- * the reference rule's, as for va_select.
+ * conditions, one pass, segment_keys a multiple of 256), else (one pass only:
+ * fp32 inputs, other head dims) on the exact kernel.  No counterpart in the
+ * reference (its single launch writes dense rows); the selected sets are the
+ * reference rule's, as for va_select.
  * va_select_segment_keys returns the segment length va_prefill uses for
  * bf16/fp16 inputs with head_dim 64 or 128: the wave kernel's (tiles of 16 to
  * 64 keys, group span of 16 or 32 keys or a multiple of 64), else the 64-row
@@ -135,6 +136,12 @@ int va_select(int dtype, const void* qs, int64_t sqb, int64_t sqh, int64_t sqn,
  * or -1 on invalid sizes.
  */
 int64_t va_select_segment_keys(int64_t Sk, int64_t k_local_size, int64_t group_k_block);
+/* The segment length va_prefill uses for fp32 inputs that run on the fp32
+ * matrix-core attention (VA_KERNELS_ATTN_F32 with VA_KERNELS_SELECT_EXACT):
+ * the exact kernel's one-pass split, multiples of 256 keys and of the group
+ * span, at least Sk/64 keys; 0 when the keys are not split (one group covers
+ * the row), -1 on invalid sizes.  No counterpart in the reference. */
+int64_t va_select_exact_segment_keys(int64_t Sk, int64_t k_local_size, int64_t group_k_block);
 /* fp32 scratch floats va_select_segments needs: the key norms, plus two floats
  * per (row, segment) in the two-pass form.  -1 on invalid sizes. */
 int64_t va_select_segments_scratch_floats(int64_t B, int64_t Hq, int64_t Hk, int64_t Sk,
@@ -302,8 +309,9 @@ int va_decode_attn_noalloc(int dtype, const void* q, int64_t sqh, const void* k,
 
 /*
  * va_sparse_attn on the segmented lists of va_select_segments (counts of shape
- * (B, Hq, nc, ceil(Sk/segment_keys))); MFMA kernel only.  No counterpart in
- * the reference: it is the second half of va_prefill's chunk step.
+ * (B, Hq, nc, ceil(Sk/segment_keys))); the bf16/fp16 MFMA kernel or the fp32
+ * matrix-core kernel only.  No counterpart in the reference: it is the second
+ * half of va_prefill's chunk step.
  */
 int va_sparse_attn_segments(int dtype, const void* q, int64_t sqb, int64_t sqh, int64_t sqs,
                             const void* k, int64_t skb, int64_t skh, int64_t sks, const void* v,
@@ -337,7 +345,9 @@ int64_t va_prefill_workspace_size(int dtype, int64_t B, int64_t Hq, int64_t Sq, 
  * q_pooling_size outside {64, 128}, K/V row strides of 16 KiB or more,
  * unaligned tensors), with VA_KERNELS_ATTN_RING
  * when that kernel runs its ring form (see va_sparse_attn); VA_KERNELS_SPLIT
- * when the selection runs in key segments.  The exact selection and the per-row
+ * when the selection runs in key segments (va_select_segment_keys, or
+ * va_select_exact_segment_keys with VA_KERNELS_SELECT_EXACT, which splits only
+ * for the fp32 matrix-core attention).  The exact selection and the per-row
  * attention are several times slower than the MFMA kernels.  No counterpart
  * in the reference: it lets callers see which path a configuration takes.
  */

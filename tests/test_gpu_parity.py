@@ -404,6 +404,85 @@ def test_select_segments_mfma_kernel_bit_exact(device, case):
     assert want_c.sum() > 0
 
 
+# fp32 inputs (and head dims the MFMA kernels do not take) select on the
+# exact kernel; va_prefill splits it into key segments (one pass: every
+# segment starts a group) when the fp32 matrix-core attention reads the lists.
+EXACT_SPLIT_CASES = [
+    # name, B, Hq, Hk, S, D, dtype, causal, qps, bk, G, keep, segk, chunk_rows
+    ("A-fp32-noncausal-seg256", 1, 4, 4, 4096, 64, torch.float32, False, 64, 16, 16, 0.10, 256,
+     None),
+    ("fp32-causal-gqa-bk32-G4-seg384-chunked", 2, 4, 2, 2500, 64, torch.float32, True, 64, 32, 4,
+     0.10, 384, 13),
+    ("fp32-noncausal-qps128-d128-seg512-gap0", 1, 2, 1, 1800, 128, torch.float32, False, 128, 16,
+     16, None, 512, None),
+    ("fp32-causal-seg256-gap0", 1, 2, 1, 2048, 64, torch.float32, True, 64, 16, 16, None, 256,
+     None),
+    # segments that are not whole 256-key chunks
+    ("bf16-d96-noncausal-bk16-G2-seg320", 1, 2, 2, 1900, 96, torch.bfloat16, False, 64, 16, 2,
+     0.15, 320, None),
+]
+
+
+@pytest.mark.parametrize("case", EXACT_SPLIT_CASES, ids=[c[0] for c in EXACT_SPLIT_CASES])
+def test_select_segments_exact_kernel_bit_exact(device, case):
+    # The exact kernel's split: per-segment lists, concatenated, equal the
+    # oracle's rows (every segment's keys inside the segment, within the row's
+    # capacity).
+    name, B, Hq, Hk, S, D, dtype, causal, qps, bk, G, keep, segk, chunk_rows = case
+    note("select segments exact", name)
+    q, k, _ = make_inputs(B, Hq, Hk, S, D, dtype, seed=S + segk + D)
+    if keep is None:
+        gaps = np.zeros(B * Hq, np.float32)
+    else:
+        gaps = orc.gap_from_threshold(calibrated_threshold(keep, q, k, qps, bk, G, causal), B, Hq)
+    _, qs_cpu = orc.pool(q, qps, DTN[dtype])
+    nqb = qs_cpu.shape[2]
+    qs, _ = stages.pool_scaled(q.to(device), qps)
+    kd = k.to(device)
+    step = chunk_rows or nqb
+    total = 0
+    for J0 in range(0, nqb, step):
+        nc = min(step, nqb - J0)
+        want_c, want = orc.select(qs_cpu, k, J0, nc, gaps, qps, bk, G, causal, causal, 64)
+        cnt, idx = stages.select_segments(qs[:, :, J0:J0 + nc], kd, J0, float(gaps[0]), None,
+                                          causal, qps, bk, G, causal, segk, bsq=64)
+        lists = SegmentedLists(cnt, idx, J0, nc, qps, S, causal, causal, segk)
+        for b in range(B):
+            for h in range(Hq):
+                for jr in range(nc):
+                    assert np.array_equal(lists.row(b, h, jr), want[b][h][jr]), (name, b, h,
+                                                                                  J0 + jr)
+        total += int(want_c.sum())
+    assert total > 0
+
+
+@pytest.mark.parametrize("causal,qps,D", [(True, 64, 64), (False, 128, 128)],
+                         ids=["causal-qps64-d64", "noncausal-qps128-d128"])
+def test_fp32_attention_on_segmented_lists_equals_unsplit(device, causal, qps, D):
+    # The fp32 matrix-core attention on a split selection's segmented lists
+    # (va_prefill's fp32 form) gives the output of the unsplit lists bit for
+    # bit: the concatenated lists hold the same keys in the same order, so
+    # every tile holds the same keys.
+    B, Hq, Hk, S, bk, G = 2, 4, 2, 1700, 16, 16
+    note("attn fp32 segmented", causal, qps, D)
+    q, k, v = make_inputs(B, Hq, Hk, S, D, torch.float32, seed=D + qps)
+    qd, kd, vd = q.to(device), k.to(device), v.to(device)
+    qs, _ = stages.pool_scaled(qd, qps)
+    nqb = qs.shape[2]
+    segk = stages.segment_keys(S, bk, G, exact=True)
+    assert segk > 0 and -(-S // segk) > 1
+    gap = -math.log(0.3)
+    cnt1, idx1 = stages.select_rows(qs, kd, 0, gap, None, causal, qps, bk, G, causal)
+    cnt2, idx2 = stages.select_segments(qs, kd, 0, gap, None, causal, qps, bk, G, causal, segk)
+    assert torch.equal(cnt2.sum(-1), cnt1) and int(cnt1.sum()) > 0
+    outs = []
+    for cnt, idx, sk in ((cnt1, idx1, 0), (cnt2, idx2, segk)):
+        out = torch.zeros(B, Hq, S, D, dtype=torch.float32, device=device)
+        stages.sparse_attention(qd, kd, vd, out, 0, nqb, cnt, idx, causal, qps, segk=sk)
+        outs.append(out.cpu())
+    assert torch.equal(outs[0], outs[1])
+
+
 # (the wave kernel takes tiles of at most 64 keys)
 STRESS_PARAMS = [pytest.param(case, kern, id=f"{case[0]}-{kid}") for case in MFMA_STRESS
                  for kern, kid in ((nat.VA_SEL_MFMA, "mfma"), (nat.VA_SEL_WAVE, "wave"))
@@ -622,6 +701,10 @@ E2E_CASES = [
     # the reference models' defaults (k_local_size 16, group_k_block 1)
     ("model-defaults-causal-G1", 1, 4, 2, 3000, 128, torch.bfloat16, True, 64, 16, 1, 1024, 0.9),
     ("A-fp32-noncausal", 1, 4, 4, 4096, 64, torch.float32, False, 64, 16, 16, 4096, 0.35),
+    # fp32 split selection under the causal rule, over chunks
+    ("fp32-causal-gqa-chunked", 1, 4, 2, 2500, 64, torch.float32, True, 64, 16, 16, 1024, 0.5),
+    ("fp32-noncausal-qps128-d128", 2, 2, 1, 1500, 128, torch.float32, False, 128, 32, 4, 1024,
+     0.4),
     # batches: every (b, h) work item, strides over the batch dimension
     ("batch2-causal-gqa", 2, 8, 2, 1536, 128, torch.bfloat16, True, 64, 16, 16, 1024, 0.5),
     ("batch3-noncausal-fp16-d64", 3, 4, 2, 1100, 64, torch.float16, False, 64, 16, 8192, 1024, 0.3),

@@ -297,8 +297,21 @@ def test_prefill_kernels_reports_the_slow_paths(L):
     assert _plan(L, bk=512, G=1) & nat.VA_KERNELS_SELECT_EXACT
     # fp32 inputs: exact selection and the fp32 matrix-core attention; the
     # per-row attention for a head_dim that kernel does not take
+    # (in key segments the exact kernel splits at in one pass)
     f = _plan(L, dtype=nat.VA_F32)
-    assert f == nat.VA_KERNELS_SELECT_EXACT | nat.VA_KERNELS_ATTN_F32
+    f32 = nat.VA_KERNELS_SELECT_EXACT | nat.VA_KERNELS_ATTN_F32
+    assert f == f32 | nat.VA_KERNELS_SPLIT
+    # one group per row: no one-pass split on the exact kernel
+    assert _plan(L, dtype=nat.VA_F32, G=8192, Sk=32760, Hq=12, Hk=12) == f32
+    # segments of 256 keys or more, multiples of 256 and of the group span,
+    # at most 64 of them
+    assert L.va_select_exact_segment_keys(4096, 16, 16) == 256
+    assert L.va_select_exact_segment_keys(32768, 16, 16) == 512
+    assert L.va_select_exact_segment_keys(131072, 16, 1) == 2048
+    assert L.va_select_exact_segment_keys(4096, 16, 3) == 768       # span 48: lcm 768
+    assert L.va_select_exact_segment_keys(4096, 16, 8192) == 0      # one group per row
+    assert L.va_select_exact_segment_keys(200, 16, 16) == 0         # one group covers Sk
+    assert L.va_select_exact_segment_keys(0, 16, 16) == -1
     assert _plan(L, dtype=nat.VA_F32, D=96) == nat.VA_KERNELS_SELECT_EXACT | nat.VA_KERNELS_ATTN_ROW
     # head_dim 96: neither MFMA kernel
     f = _plan(L, D=96)

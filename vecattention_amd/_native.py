@@ -42,6 +42,7 @@ SIGNATURES = {
                          _i64, _i64, _i64, _i64, _i64, _int, _int, _i64, _i64, _i64, _f32, _vp,
                          _i64, _vp, _vp, _int, _vp, _i64, _vp]),
     "va_select_segment_keys": (_i64, [_i64, _i64, _i64]),
+    "va_select_exact_segment_keys": (_i64, [_i64, _i64, _i64]),
     "va_select_segments": (_int, [_int, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _i64, _i64,
                                   _i64, _i64, _i64, _i64, _i64, _i64, _int, _int, _i64, _i64, _i64,
                                   _f32, _vp, _i64, _i64, _vp, _vp, _vp, _i64, _vp]),

@@ -18,7 +18,7 @@ hipError_t launch_select_exact(int dtype, const void* qs, int64_t sqb, int64_t s
                                int64_t Hk, int64_t Sk, int64_t D, int64_t qps, int64_t bk,
                                int64_t group, int causal, int64_t bsq, float gap_scalar,
                                const float* gaps, const RowLayout& lay, int32_t* counts,
-                               int32_t* indices, hipStream_t stream);
+                               int32_t* indices, int64_t segk, hipStream_t stream);
 hipError_t launch_attn_simple(int dtype, const void* q, const int64_t* sq, const void* k,
                               const int64_t* sk, const void* v, const int64_t* sv, void* out,
                               const int64_t* so, int64_t B, int64_t Hq, int64_t Hk, int64_t Sq,
@@ -46,6 +46,7 @@ constexpr int64_t kSegCarryBytes = 32;  // per (row, segment) record of the two-
 int64_t select_wave_segment_keys(int64_t Sk, int64_t bk, int64_t group);
 int64_t select_mfma_segment_keys(int64_t Sk, int64_t bk, int64_t group);
 int64_t select_wave_carry_segment_keys(int64_t Sk, int64_t bk, int64_t group);
+int64_t select_exact_segment_keys(int64_t Sk, int64_t bk, int64_t group);
 int64_t key_norm_scratch_floats(int64_t B, int64_t Hk);
 hipError_t launch_csr_offsets(const int32_t* counts, int64_t rows, int nseg, int64_t* offsets,
                               hipStream_t stream);
@@ -65,8 +66,8 @@ hipError_t launch_attn_f32(const void* q, const int64_t* sq, const void* k, cons
                            const void* v, const int64_t* sv, void* out, const int64_t* so,
                            int64_t B, int64_t Hq, int64_t Hk, int64_t Sq, int64_t Sk, int64_t D,
                            int64_t qps, int causal, float scale_log2, const int32_t* counts,
-                           const int32_t* indices, const RowLayout& lay, int64_t dense_qoff,
-                           hipStream_t stream);
+                           const int32_t* indices, const RowLayout& lay, int nseg, int segk,
+                           int64_t dense_qoff, hipStream_t stream);
 bool ring_form_preferred(int64_t Hq, int64_t Hk, int64_t Sk, int64_t D);
 hipError_t launch_attn_split(int dtype, int64_t D, const void* q, const int64_t* sq,
                              const void* k, const int64_t* sk, const void* v, const int64_t* sv,
@@ -233,7 +234,7 @@ static int select_impl(int dtype, const void* qs, int64_t sqb, int64_t sqh, int6
   else
     e = va::launch_select_exact(dtype, qs, sqb, sqh, sqn, k, skb, skh, sks, B, Hq, Hk, Sk, D,
                                 qps, bk, group, causal, bsq, gap, gaps, lay, counts, indices,
-                                stream);
+                                segk, stream);
   return hip_check(e, "select launch");
 }
 
@@ -334,6 +335,12 @@ int64_t va_select_segment_keys(int64_t Sk, int64_t k_local_size, int64_t group_k
   return va::select_mfma_segment_keys(Sk, k_local_size, g);
 }
 
+int64_t va_select_exact_segment_keys(int64_t Sk, int64_t k_local_size, int64_t group_k_block) {
+  if (Sk <= 0 || k_local_size <= 0 || group_k_block <= 0) return -1;
+  return va::select_exact_segment_keys(Sk, k_local_size,
+                                       effective_group(group_k_block, Sk, k_local_size));
+}
+
 // The two-pass form: the groups cover every key of a row and the segments do
 // not start groups.
 static bool segments_two_pass(int64_t Sk, int64_t bk, int64_t group, int64_t segment_keys) {
@@ -356,7 +363,8 @@ int64_t va_select_segments_scratch_floats(int64_t B, int64_t Hq, int64_t Hk, int
 // of 64 and of the group span (one pass), or any multiple of 64 when one
 // group covers the row (maxima pass, then carry pass), at most 64 segments.
 // The wave kernel takes every split; the 64-row MFMA kernel (tiles of 128 and
-// 256 keys) takes segments of whole 256-key chunks that start groups.
+// 256 keys) takes segments of whole 256-key chunks that start groups; the
+// exact kernel (other inputs, fp32 among them) takes every one-pass split.
 static int plan_segments(int dtype, const void* qs, int64_t sqb, int64_t sqh, int64_t sqn,
                          const void* k, int64_t skb, int64_t skh, int64_t sks, int64_t B,
                          int64_t Hq, int64_t Hk, int64_t Sk, int64_t D, int64_t qps, int64_t bk,
@@ -377,9 +385,12 @@ static int plan_segments(int dtype, const void* qs, int64_t sqb, int64_t sqh, in
              select_mfma_ok(dtype, qs, sqb, sqh, sqn, k, skb, skh, sks, D, bk))
               ? kSelMfma
               : kSelExact;
-  if (which == kSelExact)
-    return fail(VA_ERR_UNSUPPORTED, "segmented selection needs the wave selection kernel, or "
-                                    "the MFMA kernel with segments of whole 256-key chunks");
+  if (which == kSelExact && two_pass)
+    return fail(VA_ERR_UNSUPPORTED, "two-pass segmented selection (one group per row) needs "
+                                    "the wave selection kernel");
+  // exact kernel: up to 16 rows per work-group, one work-group per (rows, segment)
+  if (which == kSelExact && cdiv(nc, 16) * cdiv(Sk, segment_keys) * B * Hq > (int64_t(1) << 24))
+    return fail(VA_ERR_UNSUPPORTED, "grid too large");
   const int64_t need = va_select_segments_scratch_floats(B, Hq, Hk, Sk, nc, segment_keys, bk, group);
   if (!scratch || scratch_floats < need)
     return fail(VA_ERR_ARG, "segmented selection needs %lld scratch floats", (long long)need);
@@ -405,9 +416,11 @@ int va_select_segments(int dtype, const void* qs, int64_t sqb, int64_t sqh, int6
                      causal, wo_init, nc, segment_keys, scratch, scratch_floats, which, two_pass);
   if (rc) return rc;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  rc = hip_check(va::launch_key_norm(dtype, k, skb, skh, sks, B, Hk, Sk, D, scratch, st),
-                 "key norm launch");
-  if (rc) return rc;
+  if (which != kSelExact) {
+    rc = hip_check(va::launch_key_norm(dtype, k, skb, skh, sks, B, Hk, Sk, D, scratch, st),
+                   "key norm launch");
+    if (rc) return rc;
+  }
   void* carry = scratch + (va::key_norm_scratch_floats(B, Hk) + 7) / 8 * 8;
   if (two_pass) {
     rc = select_impl(dtype, qs, sqb, sqh, sqn, k, skb, skh, sks, B, Hq, Hk, Sk, D, qps, bk, group,
@@ -551,9 +564,9 @@ static int attn_dispatch(int dtype, const void* q, const int64_t* sq, const void
     form = kernel == VA_ATTN_MFMA_RING ? va::kAttnFormRing : va::kAttnFormStaged;
     kernel = VA_ATTN_MFMA;
   }
-  // fp32 inputs: the fp32 matrix-core kernel (attention output, one key
-  // segment), else the per-row kernel
-  const bool f32 = !stats && nseg <= 1 && attn_f32_ok(dtype, q, sq, k, sk, v, sv, out, so, D, qps);
+  // fp32 inputs: the fp32 matrix-core kernel (attention output), else the
+  // per-row kernel
+  const bool f32 = !stats && attn_f32_ok(dtype, q, sq, k, sk, v, sv, out, so, D, qps);
   bool use_f32 = false;
   if (form != va::kAttnFormAuto && dtype == VA_F32)
     return fail(VA_ERR_UNSUPPORTED, "the staged and ring forms are the bf16/fp16 MFMA kernel's");
@@ -579,11 +592,12 @@ static int attn_dispatch(int dtype, const void* q, const int64_t* sq, const void
     return fail(VA_ERR_ARG, "unknown kernel selector %d", kernel);
   }
   if (!use_mfma && qps > 1024) return fail(VA_ERR_UNSUPPORTED, "q_pooling_size > 1024");
-  if (!use_mfma && nseg > 1)
-    return fail(VA_ERR_UNSUPPORTED, "segmented key lists need the MFMA attention kernel");
+  if (!use_mfma && !use_f32 && nseg > 1)
+    return fail(VA_ERR_UNSUPPORTED, "segmented key lists need a matrix-core attention kernel");
   if (use_f32)
     return hip_check(va::launch_attn_f32(q, sq, k, sk, v, sv, out, so, B, Hq, Hk, Sq, Sk, D, qps,
-                                         causal, scale_log2, counts, indices, lay, -1, stream),
+                                         causal, scale_log2, counts, indices, lay, nseg,
+                                         int(segk), -1, stream),
                      "attention launch");
   hipError_t e = use_mfma
                      ? va::launch_attn_mfma(dtype, D, qps, q, sq, k, sk, v, sv, out, so, B, Hq,
@@ -659,7 +673,7 @@ int va_dense_attn(int dtype, const void* q, int64_t sqb, int64_t sqh, int64_t sq
     const va::RowLayout lay = make_layout(0, nc, qps, Sk, causal, 0, 0);
     const int rc = hip_check(
         va::launch_attn_f32(q, sq, k, sk, v, sv, out, so, B, Hq, Hk, Sq, Sk, D, qps, causal,
-                            softmax_scale * 1.4426950408889634f, nullptr, nullptr, lay,
+                            softmax_scale * 1.4426950408889634f, nullptr, nullptr, lay, 1, 0,
                             causal ? Sk - Sq : 0, static_cast<hipStream_t>(stream)),
         "dense attention launch");
     return rc ? rc : ok();
@@ -965,12 +979,15 @@ int va_prefill_kernels(int dtype, const void* q, int64_t sqb, int64_t sqh, int64
                                                                            : VA_KERNELS_ATTN_ROW;
   if (attn && va::attn_mfma_ring_supported(dtype, D, qps) && va::ring_form_preferred(Hq, Hk, Sk, D))
     flags |= VA_KERNELS_ATTN_RING;
+  const int64_t g = effective_group(group, Sk, bk);
   if (attn && (flags & (VA_KERNELS_SELECT_WAVE | VA_KERNELS_SELECT_MFMA))) {
-    const int64_t g = effective_group(group, Sk, bk);
     if (wave ? (va::select_wave_segment_keys(Sk, bk, g) > 0 ||
                 va::select_wave_carry_segment_keys(Sk, bk, g) > 0)
              : va::select_mfma_segment_keys(Sk, bk, g) > 0)
       flags |= VA_KERNELS_SPLIT;
+  } else if ((flags & VA_KERNELS_ATTN_F32) && !(flags & (VA_KERNELS_SELECT_WAVE |
+                                                          VA_KERNELS_SELECT_MFMA))) {
+    if (va::select_exact_segment_keys(Sk, bk, g) > 0) flags |= VA_KERNELS_SPLIT;
   }
   ok();
   return flags;
@@ -1043,6 +1060,11 @@ int va_prefill(int dtype, const void* q, int64_t sqb, int64_t sqh, int64_t sqs, 
     } else if (which == kSelMfma && attn) {
       // the 64-row MFMA kernel splits at whole 256-key chunks (no carry pass)
       segk = va::select_mfma_segment_keys(Sk, bk, g);
+    } else if (which == kSelExact && attn_f32_ok(dtype, q, sq, k, sk, v, sv, out, so, D, qps)) {
+      // fp32: the exact kernel's one-pass split, read by the fp32 matrix-core attention
+      segk = va::select_exact_segment_keys(Sk, bk, g);
+      if (segk > 0 && cdiv(cdiv(chunk_size, qps), 16) * cdiv(Sk, segk) * B * Hq > (int64_t(1) << 24))
+        segk = 0;  // grid of (16-row sets, segment) work-groups too large
     }
   }
   const float scale = float(1.0 / std::sqrt(double(D)));

@@ -22,6 +22,13 @@
 // operand is one float per lane of the V row of the step's key (ids shared
 // through lane shuffles).  Every K and V row feeds all 32 rows of a block from
 // registers, against one row per load in the per-row kernel.
+//
+// Segmented lists (nseg > 1, the split selection): segment s of the row holds
+// counts[(bh*nc + jr)*nseg + s] keys from slot max(s*segk, smin) - smin of the
+// row.  Lane s of every wave keeps the exclusive prefix sv[s] of the segment
+// counts, and column p of the concatenated list is found by a binary search
+// over the lanes for the last s with sv[s] <= p (segment counts are clamped
+// to the slots left in the row, as the MFMA kernel does).
 #include "keylist.h"
 #include "lanes.h"
 #include "mfma.h"
@@ -42,7 +49,7 @@ __global__ __launch_bounds__(256) void attn_f32_kernel(
     float* __restrict__ out, int64_t sob, int64_t soh, int64_t sos, int64_t B, int64_t Hq,
     int64_t Hk, int64_t Sq, int64_t Sk, int causal, float scale_log2,
     const int32_t* __restrict__ counts, const int32_t* __restrict__ indices, RowLayout lay,
-    int64_t dense_qoff) {
+    int nseg, int segk, int64_t dense_qoff) {
   constexpr int RB = QPS / 32;  // row blocks
   constexpr int KS = 4 / RB;    // key splits
   constexpr int NS = D / 2;     // QK^T steps (two features each)
@@ -64,8 +71,24 @@ __global__ __launch_bounds__(256) void attn_f32_kernel(
   const int64_t b = bh / Hq, h = bh % Hq, hk = h / (Hq / Hk);
   const int64_t J = lay.J0 + jr;
 
-  int64_t cnt = counts ? counts[bh * lay.nc + jr] : 0;
   const int64_t cap = lay.capacity(J);
+  const int smin = int(lay.smin());
+  auto seg_slot = [&](int sg) { return (sg * segk > smin ? sg * segk : smin) - smin; };
+  int64_t cnt = 0;
+  int sv = 0x7fffffff;  // lane s < nseg: first list column of segment s
+  if (counts && nseg <= 1) {
+    cnt = counts[bh * lay.nc + jr];
+  } else if (counts) {
+    int c = 0;
+    if (lane < nseg) {
+      c = counts[(bh * lay.nc + jr) * nseg + lane];
+      const int room = int(cap) - seg_slot(lane);
+      c = c < 0 ? 0 : (c > room ? (room > 0 ? room : 0) : c);
+    }
+    const int incl = wave_inclusive_sum(c);
+    if (lane < nseg) sv = incl - c;
+    cnt = __builtin_amdgcn_readlane(incl, nseg - 1);
+  }
   if (cnt > cap) cnt = cap;
   const int32_t* cols = indices ? indices + lay.row_offset(bh, jr) : nullptr;
   const KeyList kl = dense_qoff >= 0 ? KeyList::dense(J, QPS, Sk, causal, dense_qoff)
@@ -111,6 +134,7 @@ __global__ __launch_bounds__(256) void attn_f32_kernel(
   for (int64_t t = ks; t < ntiles; t += KS) {
     int64_t p0, lim, dkey0 = 0;
     bool diag = false;
+    int64_t slot_shift = 0;  // slot - list column of this lane's column
     if (t < t_init) {
       p0 = t * kF32Tile;
       lim = n_init - p0;
@@ -124,10 +148,25 @@ __global__ __launch_bounds__(256) void attn_f32_kernel(
       const int64_t c = (t - t_init - t_diag) * kF32Tile;
       p0 = n_init + n_diag + c;
       lim = n_col - c;
+      if (nseg > 1) {  // every lane takes part: the search reads other lanes
+        const int col = int(c) + l32;
+        int sg = 0;
+#pragma unroll
+        for (int step = 32; step >= 1; step /= 2) {
+          const int cand = sg + step;
+          const int bound = __shfl(sv, cand < 64 ? cand : 63);
+          if (cand < nseg && bound <= col) sg = cand;
+        }
+        slot_shift = seg_slot(sg) - __shfl(sv, sg);
+      }
     }
     if (lim > kF32Tile) lim = kF32Tile;
     // key of slot l32 (row 0 for empty slots and keys outside [0, Sk): read, weighed 0)
-    int64_t key = l32 < lim ? kl.key(p0 + l32) : 0;
+    int64_t key = 0;
+    if (l32 < lim) {
+      const int64_t p = p0 + l32;
+      key = p < n_init + n_diag ? kl.key(p) : kl.cols[p - n_init - n_diag + slot_shift];
+    }
     if (key < 0 || key >= Sk) key = 0;
     const float4* kr = reinterpret_cast<const float4*>(kh + key * sks + hh * (D / 2));
     float kv[NS];
@@ -245,8 +284,8 @@ hipError_t launch_attn_f32(const void* q, const int64_t* sq, const void* k, cons
                            const void* v, const int64_t* sv, void* out, const int64_t* so,
                            int64_t B, int64_t Hq, int64_t Hk, int64_t Sq, int64_t Sk, int64_t D,
                            int64_t qps, int causal, float scale_log2, const int32_t* counts,
-                           const int32_t* indices, const RowLayout& lay, int64_t dense_qoff,
-                           hipStream_t stream) {
+                           const int32_t* indices, const RowLayout& lay, int nseg, int segk,
+                           int64_t dense_qoff, hipStream_t stream) {
   const int64_t nblocks = lay.nc * B * Hq;
   auto go = [&](auto kernel) {
     hipLaunchKernelGGL(kernel, dim3(unsigned(nblocks)), dim3(256), 0, stream,
@@ -254,7 +293,7 @@ hipError_t launch_attn_f32(const void* q, const int64_t* sq, const void* k, cons
                        static_cast<const float*>(k), sk[0], sk[1], sk[2],
                        static_cast<const float*>(v), sv[0], sv[1], sv[2],
                        static_cast<float*>(out), so[0], so[1], so[2], B, Hq, Hk, Sq, Sk, causal,
-                       scale_log2, counts, indices, lay, dense_qoff);
+                       scale_log2, counts, indices, lay, nseg, segk, dense_qoff);
     return hipGetLastError();
   };
   if (D == 64 && qps == 64) return go(attn_f32_kernel<64, 64>);

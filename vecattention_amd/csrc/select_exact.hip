@@ -30,13 +30,18 @@ constexpr int kSelMaxD = 256;
 // kSelRows: pooled rows per work-group (16, 8, 4, 2 or 1: the host takes the
 // most rows that still give at least 256 work-groups, since each work-group
 // walks every key of its rows; small grids take one row per work-group).
+// Key segments (nseg > 1): work-group (row set, segment) walks the keys
+// [seg*segk, (seg+1)*segk) only; segments are multiples of the group span, so
+// each starts a group, and a segment writes its keys from its own first slot
+// of the row and its count to counts[(bh*nc + jr)*nseg + seg].
 template <typename T, int kSelRows>
 __global__ __launch_bounds__(256) void select_exact_kernel(
     const T* __restrict__ qs, int64_t sqb, int64_t sqh, int64_t sqn, const T* __restrict__ k,
     int64_t skb, int64_t skh, int64_t sks, int64_t B, int64_t Hq, int64_t Hk,
     int64_t Sk, int64_t D, int64_t qps, int64_t bk, int64_t group, int causal,
     int64_t bsq, float gap_scalar, const float* __restrict__ gaps, RowLayout lay,
-    int32_t* __restrict__ counts, int32_t* __restrict__ indices, int64_t nrowsets) {
+    int32_t* __restrict__ counts, int32_t* __restrict__ indices, int64_t nrowsets,
+    int64_t segk, int nseg) {
   __shared__ double qd[kSelMaxD * kSelRows];          // [d][row]
   __shared__ float sc[kSelRows * kSelChunk];          // [row][key]
   __shared__ float mt[kSelRows * (kSelChunk / 16)];   // [row][tile] running max
@@ -46,7 +51,10 @@ __global__ __launch_bounds__(256) void select_exact_kernel(
 
   const int tid = threadIdx.x;
   const int64_t BH = B * Hq;
-  const int64_t rs = nrowsets - 1 - int64_t(blockIdx.x) / BH;  // heavy rows first
+  const int64_t item = int64_t(blockIdx.x) / BH;
+  const int64_t rs = nrowsets - 1 - item / nseg;  // heavy rows first
+  const int seg = int(item % nseg);
+  const int64_t seg_lo = nseg > 1 ? int64_t(seg) * segk : 0;
   const int64_t bh = int64_t(blockIdx.x) % BH;
   const int64_t b = bh / Hq, h = bh % Hq;
   const int64_t hk = h / (Hq / Hk);
@@ -60,12 +68,13 @@ __global__ __launch_bounds__(256) void select_exact_kernel(
   const int lbk = __builtin_ctzll(uint64_t(bk));  // bk is a power of two
 
   // Key range of this work-group: [kstart, kend).
-  const int64_t kstart = smin;
+  const int64_t kstart = seg_lo > smin ? seg_lo : smin;
   int64_t kend = Sk;
   if (causal) {
     const int64_t lim = (J0 + jr0 + rows_here - 1) * qps;  // keys < J*qps only
     if (lim < kend) kend = lim;
   }
+  if (nseg > 1 && seg_lo + segk < kend) kend = seg_lo + segk;
 
   // Stage the R pooled rows in fp64, transposed for broadcast reads.
   for (int64_t e = tid; e < int64_t(kSelRows) * D; e += blockDim.x) {
@@ -165,7 +174,7 @@ __global__ __launch_bounds__(256) void select_exact_kernel(
         const int64_t J = J0 + jr;
         const int64_t lim = klim[i];
         int64_t row_off, cap;
-        lay.segment_slots(bh, jr, 0, 1, 0, row_off, cap);
+        lay.segment_slots(bh, jr, seg, nseg, seg_lo, row_off, cap);
         int32_t c = cnt[i];
         for (int step = 0; step < kSelChunk / 64; ++step) {
           const int kk = step * 64 + lane;
@@ -189,9 +198,9 @@ __global__ __launch_bounds__(256) void select_exact_kernel(
 
   if (tid < rows_here && counts) {
     int64_t start, cap;
-    lay.segment_slots(bh, jr0 + tid, 0, 1, 0, start, cap);
+    lay.segment_slots(bh, jr0 + tid, seg, nseg, seg_lo, start, cap);
     const int32_t c = cnt[tid];
-    counts[bh * nc + jr0 + tid] = (c < cap) ? c : int32_t(cap);
+    counts[(bh * nc + jr0 + tid) * nseg + seg] = (c < cap) ? c : int32_t(cap);
   }
 }
 
@@ -201,23 +210,49 @@ static hipError_t launch_select_exact_t(
     int64_t sks, int64_t B, int64_t Hq, int64_t Hk, int64_t Sk, int64_t D,
     int64_t qps, int64_t bk, int64_t group, int causal, int64_t bsq,
     float gap_scalar, const float* gaps, const RowLayout& lay, int32_t* counts,
-    int32_t* indices, hipStream_t stream) {
+    int32_t* indices, int64_t segk, hipStream_t stream) {
+  const int64_t nseg = segk > 0 ? (Sk + segk - 1) / segk : 1;
   auto launch = [&](auto rows_tag) {
     constexpr int R = decltype(rows_tag)::value;
     const int64_t nrowsets = (lay.nc + R - 1) / R;
-    const int64_t nblocks = nrowsets * B * Hq;
+    const int64_t nblocks = nrowsets * nseg * B * Hq;
     hipLaunchKernelGGL((select_exact_kernel<T, R>), dim3(unsigned(nblocks)), dim3(kSelChunk), 0,
                        stream, static_cast<const T*>(qs), sqb, sqh, sqn,
                        static_cast<const T*>(k), skb, skh, sks, B, Hq, Hk, Sk, D, qps, bk, group,
-                       causal, bsq, gap_scalar, gaps, lay, counts, indices, nrowsets);
+                       causal, bsq, gap_scalar, gaps, lay, counts, indices, nrowsets,
+                       segk > 0 ? segk : Sk, int(nseg));
     return hipGetLastError();
   };
   constexpr int64_t kMinGroups = 256;
-  if ((lay.nc + 15) / 16 * B * Hq >= kMinGroups) return launch(std::integral_constant<int, 16>{});
-  if ((lay.nc + 7) / 8 * B * Hq >= kMinGroups) return launch(std::integral_constant<int, 8>{});
-  if ((lay.nc + 3) / 4 * B * Hq >= kMinGroups) return launch(std::integral_constant<int, 4>{});
-  if ((lay.nc + 1) / 2 * B * Hq >= kMinGroups) return launch(std::integral_constant<int, 2>{});
+  const int64_t items = nseg * B * Hq;  // work-groups per row set
+  if ((lay.nc + 15) / 16 * items >= kMinGroups) return launch(std::integral_constant<int, 16>{});
+  if ((lay.nc + 7) / 8 * items >= kMinGroups) return launch(std::integral_constant<int, 8>{});
+  if ((lay.nc + 3) / 4 * items >= kMinGroups) return launch(std::integral_constant<int, 4>{});
+  if ((lay.nc + 1) / 2 * items >= kMinGroups) return launch(std::integral_constant<int, 2>{});
   return launch(std::integral_constant<int, 1>{});
+}
+
+// Key segments of the exact kernel's split (one pass): multiples of 256 keys
+// and of the group span, so that each segment starts a group, at least
+// Sk / 64 keys (at most 64 segments) and otherwise as short as one 256-key
+// chunk: a work-group then scores its rows' keys in one chunk instead of
+// walking the row, and the row sets take 16 rows each sooner (more rows per
+// K load).  0 when one group covers the row (no one-pass split) or nothing
+// is split.
+int64_t select_exact_segment_keys(int64_t Sk, int64_t bk, int64_t group) {
+  constexpr int64_t kMaxSeg = 64;
+  const int64_t gs = bk * group;
+  if (gs <= 0 || gs >= Sk) return 0;
+  int64_t a = kSelChunk, b = gs;  // lcm(kSelChunk, gs)
+  while (b) {
+    const int64_t t = a % b;
+    a = b;
+    b = t;
+  }
+  const int64_t unit = kSelChunk / a * gs;
+  const int64_t want = (Sk + kMaxSeg - 1) / kMaxSeg;
+  const int64_t segk = (want + unit - 1) / unit * unit;
+  return segk < Sk ? segk : 0;
 }
 
 hipError_t launch_select_exact(int dtype, const void* qs, int64_t sqb, int64_t sqh,
@@ -226,20 +261,20 @@ hipError_t launch_select_exact(int dtype, const void* qs, int64_t sqb, int64_t s
                                int64_t qps, int64_t bk, int64_t group, int causal,
                                int64_t bsq, float gap_scalar, const float* gaps,
                                const RowLayout& lay, int32_t* counts, int32_t* indices,
-                               hipStream_t stream) {
+                               int64_t segk, hipStream_t stream) {
   switch (dtype) {
     case kF32:
       return launch_select_exact_t<float>(qs, sqb, sqh, sqn, k, skb, skh, sks, B, Hq, Hk, Sk, D, qps, bk,
                                           group, causal, bsq, gap_scalar, gaps, lay, counts,
-                                          indices, stream);
+                                          indices, segk, stream);
     case kBF16:
       return launch_select_exact_t<bf16_t>(qs, sqb, sqh, sqn, k, skb, skh, sks, B, Hq, Hk, Sk, D, qps,
                                            bk, group, causal, bsq, gap_scalar, gaps, lay, counts,
-                                           indices, stream);
+                                           indices, segk, stream);
     case kF16:
       return launch_select_exact_t<f16_t>(qs, sqb, sqh, sqn, k, skb, skh, sks, B, Hq, Hk, Sk, D, qps, bk,
                                           group, causal, bsq, gap_scalar, gaps, lay, counts,
-                                          indices, stream);
+                                          indices, segk, stream);
   }
   return hipErrorInvalidValue;
 }

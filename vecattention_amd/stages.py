@@ -102,9 +102,12 @@ def select_rows(qs_chunk, k, J0, gap, gaps, causal, q_pooling_size, k_local_size
     return counts, indices
 
 
-def segment_keys(Sk, k_local_size, group_k_block):
-    """Segment length of the split selection va_prefill uses (0: not split)."""
-    return int(nat.lib().va_select_segment_keys(Sk, k_local_size, group_k_block))
+def segment_keys(Sk, k_local_size, group_k_block, exact=False):
+    """Segment length of the split selection va_prefill uses (0: not split):
+    the wave/MFMA kernels' for bf16/fp16, the exact kernel's (`exact`) for
+    fp32 inputs on the fp32 matrix-core attention."""
+    fn = nat.lib().va_select_exact_segment_keys if exact else nat.lib().va_select_segment_keys
+    return int(fn(Sk, k_local_size, group_k_block))
 
 
 def select_segments(qs_chunk, k, J0, gap, gaps, causal, q_pooling_size, k_local_size,
