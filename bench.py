@@ -265,6 +265,32 @@ def run_stages(wl, q, k, v, gap, out, events=None):
     return res
 
 
+class StreamHold:
+    """Holds the current stream with torch's spin kernel while the host
+    enqueues work behind it, so that events recorded between those launches
+    time the kernels and not the host's launch gaps (at the small
+    configurations a launch from Python takes longer than its kernel)."""
+
+    def __init__(self):
+        self.ms_per_cycle = None
+        try:
+            cyc = 2_000_000
+            torch.cuda._sleep(cyc)  # first launch (module load) outside the calibration
+            torch.cuda.synchronize()
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            torch.cuda._sleep(cyc)
+            b.record()
+            torch.cuda.synchronize()
+            self.ms_per_cycle = a.elapsed_time(b) / cyc
+        except (AttributeError, RuntimeError) as e:  # no spin kernel: events time the gaps too
+            print(f"[bench] no stream hold ({e})", file=sys.stderr, flush=True)
+
+    def __call__(self, ms):
+        if self.ms_per_cycle and ms > 0:
+            torch.cuda._sleep(int(min(ms, 200.0) / self.ms_per_cycle))
+
+
 def calibrate_threshold(wl, q, k, v, out):
     """Bisection on the threshold for the workload's keep ratio (GPU selection)."""
     target = wl.keep * selectable(wl, q.shape[2])
@@ -661,11 +687,27 @@ def measure_prefill(args, wl, dev, with_cpu):
     names = ["p0", "p1"] + [f"{p}_{c}" for c in range(nch) for p in ("s0", "s1", "a1")]
     t_pool, t_sel, t_attn = [], [], []
     counts = None
+    hold = StreamHold()
+    hold_ms = 0.0
     for r in range(max(args.stage_reps, 1) + 1):
         ev = {n: torch.cuda.Event(enable_timing=True) for n in names}
+        hold(hold_ms)
+        h0 = time.perf_counter()
         counts = run_stages(wl, q, k, v, gap, out, ev)
+        host_ms = (time.perf_counter() - h0) * 1e3  # the host's time to enqueue the pass
         torch.cuda.synchronize()
         if r == 0:
+            gpu_ms = ev["p0"].elapsed_time(ev[f"a1_{nch - 1}"])
+            # Short passes (A, B, D: a few ms or less) are held: launches
+            # that reach an idle GPU there add tens of microseconds of gaps
+            # and dispatch latency inside the stages (B's attention measured
+            # 6-11% slower unheld than its kernel trace).  Long passes (C, E)
+            # are not: the GPU idles through the hold and starts the pass at
+            # a lower clock (C's stages measured 5% slower held).
+            if gpu_ms < 5.0:
+                hold_ms = 2.0 * host_ms + 1.0
+            print(f"[bench] stage pass: host enqueue {host_ms:.3f} ms, GPU {gpu_ms:.3f} ms; "
+                  f"stream hold {hold_ms:.3f} ms", file=sys.stderr, flush=True)
             continue
         t_pool.append(ev["p0"].elapsed_time(ev["p1"]))
         t_sel.append(sum(ev[f"s0_{c}"].elapsed_time(ev[f"s1_{c}"]) for c in range(nch)))
