@@ -37,6 +37,9 @@ CSR_CASES = [
     ("mfma-causal-qps96-unaligned", 1, 4, 2, 1536, 128, torch.bfloat16, True, 96, 16, 4, 0.10, 0,
      None),
     ("exact-fp32-noncausal", 1, 4, 4, 2048, 64, torch.float32, False, 64, 16, 16, 0.10, 0, None),
+    # the exact kernel's one-pass split (segments of whole groups)
+    ("exact-fp32-causal-seg256-chunked", 1, 4, 2, 2500, 64, torch.float32, True, 64, 16, 16,
+     0.10, 256, 13),
 ]
 
 
