@@ -28,8 +28,9 @@ constexpr int kSelChunk = 256;   // keys per inner chunk (== blockDim.x)
 constexpr int kSelMaxD = 256;
 
 // kSelRows: pooled rows per work-group (16, 8, 4, 2 or 1: the host takes the
-// most rows that still give at least 256 work-groups, since each work-group
-// walks every key of its rows; small grids take one row per work-group).
+// most rows that still give at least 256 work-groups (1024 with key
+// segments), since each work-group walks every key of its rows; small grids
+// take one row per work-group).
 // Key segments (nseg > 1): work-group (row set, segment) walks the keys
 // [seg*segk, (seg+1)*segk) only; segments are multiples of the group span, so
 // each starts a group, and a segment writes its keys from its own first slot
@@ -223,7 +224,11 @@ static hipError_t launch_select_exact_t(
                        segk > 0 ? segk : Sk, int(nseg));
     return hipGetLastError();
   };
-  constexpr int64_t kMinGroups = 256;
+  // Work-groups wanted: 256 for whole rows (more rows per work-group share
+  // each K load: 1-row work-groups made the tuner's 8192-row chunks 15-50%
+  // slower), 1024 for key segments, whose work-groups each score one or a
+  // few 256-key chunks and are bound by latency (A: 27.5 -> 18.9 us).
+  const int64_t kMinGroups = nseg > 1 ? 1024 : 256;
   const int64_t items = nseg * B * Hq;  // work-groups per row set
   if ((lay.nc + 15) / 16 * items >= kMinGroups) return launch(std::integral_constant<int, 16>{});
   if ((lay.nc + 7) / 8 * items >= kMinGroups) return launch(std::integral_constant<int, 8>{});
