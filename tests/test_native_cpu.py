@@ -112,6 +112,11 @@ def test_select_csr_argument_errors_before_launch(L):
     assert _null_csr(L, segk=100) == nat.VA_ERR_ARG                 # not a multiple of 64
     assert _null_csr(L, segk=512) == nat.VA_ERR_ARG                 # no scratch
     assert b"scratch" in L.va_last_error()
+    # the exact kernel (fp32) splits in one pass only: a group that spans the
+    # row (carried maxima) needs the wave kernel
+    assert _null_csr(L, dtype=nat.VA_F32, G=8192, segk=512) == nat.VA_ERR_UNSUPPORTED
+    assert b"two-pass" in L.va_last_error()
+    assert _null_csr(L, dtype=nat.VA_F32, segk=320) == nat.VA_ERR_ARG  # not whole 256-key groups
 
 
 def test_prefill_argument_errors_before_launch(L):
