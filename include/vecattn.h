@@ -265,6 +265,19 @@ int va_sparse_row_stats(int dtype, const void* q, int64_t sqb, int64_t sqh, int6
                         int64_t q_pooling_size, int causal, int wo_init, int64_t J0, int64_t nc,
                         int64_t dense_stride, const int32_t* counts, const int32_t* indices,
                         float softmax_scale, int kernel, float* stats, void* stream);
+/* va_sparse_row_stats on the segmented lists of va_select_segments (counts of
+ * shape (B, Hq, nc, ceil(Sk/segment_keys))), on the MFMA kernel (bf16/fp16, D
+ * in {64, 128}); the statistics equal those of the concatenated lists.  No
+ * counterpart in the reference: it lets the tuner's fp32 selection run split
+ * on the exact kernel. */
+int va_sparse_row_stats_segments(int dtype, const void* q, int64_t sqb, int64_t sqh,
+                                 int64_t sqs, const void* k, int64_t skb, int64_t skh,
+                                 int64_t sks, int64_t B, int64_t Hq, int64_t Hk, int64_t Sq,
+                                 int64_t Sk, int64_t D, int64_t q_pooling_size, int causal,
+                                 int wo_init, int64_t J0, int64_t nc, int64_t dense_stride,
+                                 int64_t segment_keys, const int32_t* counts,
+                                 const int32_t* indices, float softmax_scale, float* stats,
+                                 void* stream);
 int va_dense_row_stats(int dtype, const void* q, int64_t sqb, int64_t sqh, int64_t sqs,
                        const void* k, int64_t skb, int64_t skh, int64_t sks, int64_t B,
                        int64_t Hq, int64_t Hk, int64_t Sq, int64_t Sk, int64_t D, int causal,

@@ -139,3 +139,29 @@ def test_seg_pr_perhead_gqa_and_long_keys():
     rr, ss = orc.seg_pr_perhead(q, k, 64, 16, 16, th.numpy(), causal=False)
     np.testing.assert_allclose(r.cpu().numpy(), rr, atol=1e-5)
     np.testing.assert_allclose(s.cpu().numpy(), ss, atol=1e-6)
+
+
+@pytest.mark.parametrize("causal,qps,D", [(True, 64, 128), (False, 128, 64)],
+                         ids=["causal-qps64-d128", "noncausal-qps128-d64"])
+def test_sparse_row_stats_on_segmented_lists_equal_unsplit(causal, qps, D):
+    # The split exact selection (fp32 pooled queries, the tuner's form) and the
+    # MFMA statistics over its segmented lists give the statistics of the
+    # unsplit lists bit for bit: the concatenated lists are the same keys in
+    # the same order.
+    note("sparse stats segmented", causal, qps, D)
+    B, Hq, Hk, S, bk, G = 1, 4, 2, 2300, 16, 16
+    q, k = _qk(B, Hq, Hk, S, S, D, torch.float32, 16)
+    qd, kd = q.to(DEV), k.to(DEV)
+    qb, kb = qd.to(torch.bfloat16), kd.to(torch.bfloat16)
+    qs, _ = stages.pool_scaled(qd, qps)
+    nqb = qs.shape[2]
+    segk = stages.segment_keys(S, bk, G, exact=True)
+    assert segk > 0 and -(-S // segk) > 1
+    gaps = torch.full((B, Hq), 1.0, dtype=torch.float32, device=DEV)
+    c1, i1 = stages.select_rows(qs, kd, 0, 0.0, gaps, causal, qps, bk, G, causal)
+    c2, i2 = stages.select_segments(qs, kd, 0, 0.0, gaps, causal, qps, bk, G, causal, segk)
+    assert torch.equal(c2.sum(-1, dtype=torch.int32), c1) and int(c1.sum()) > 0
+    s1 = stages.sparse_row_stats(qb, kb, 0, nqb, c1, i1, causal, qps)
+    s2 = stages.sparse_row_stats(qb, kb, 0, nqb, c2, i2, causal, qps, segk=segk)
+    torch.cuda.synchronize()
+    assert torch.equal(s1, s2)

@@ -66,6 +66,9 @@ SIGNATURES = {
     "va_sparse_row_stats": (_int, [_int, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _i64, _i64,
                                    _i64, _i64, _i64, _i64, _i64, _int, _int, _i64, _i64, _i64, _vp,
                                    _vp, _f32, _int, _vp, _vp]),
+    "va_sparse_row_stats_segments": (_int, [_int, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64,
+                                            _i64, _i64, _i64, _i64, _i64, _i64, _i64, _int, _int,
+                                            _i64, _i64, _i64, _i64, _vp, _vp, _f32, _vp, _vp]),
     "va_dense_row_stats": (_int, [_int, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _i64, _i64,
                                   _i64, _i64, _i64, _i64, _int, _f32, _int, _vp, _vp]),
     "va_decode_workspace_size": (_i64, [_i64, _i64, _i64, _i64]),

@@ -707,6 +707,25 @@ int va_sparse_row_stats(int dtype, const void* q, int64_t sqb, int64_t sqh, int6
                           counts, indices, softmax_scale, kernel, 1, 0, stream, stats);
 }
 
+int va_sparse_row_stats_segments(int dtype, const void* q, int64_t sqb, int64_t sqh,
+                                 int64_t sqs, const void* k, int64_t skb, int64_t skh,
+                                 int64_t sks, int64_t B, int64_t Hq, int64_t Hk, int64_t Sq,
+                                 int64_t Sk, int64_t D, int64_t qps, int causal, int wo_init,
+                                 int64_t J0, int64_t nc, int64_t dense_stride,
+                                 int64_t segment_keys, const int32_t* counts,
+                                 const int32_t* indices, float softmax_scale, float* stats,
+                                 void* stream) {
+  if (!stats) return fail(VA_ERR_ARG, "null stats");
+  if (!counts || !indices) return fail(VA_ERR_ARG, "null counts / indices");
+  if (segment_keys <= 0 || segment_keys % 64 || cdiv(Sk, segment_keys) > kMaxSegments)
+    return fail(VA_ERR_ARG, "segment_keys %lld: need a positive multiple of 64, at most %lld "
+                            "segments", (long long)segment_keys, (long long)kMaxSegments);
+  return sparse_attn_impl(dtype, q, sqb, sqh, sqs, k, skb, skh, sks, nullptr, 0, 0, 0, nullptr, 0,
+                          0, 0, B, Hq, Hk, Sq, Sk, D, qps, causal, wo_init, J0, nc, dense_stride,
+                          counts, indices, softmax_scale, VA_ATTN_MFMA,
+                          int(cdiv(Sk, segment_keys)), segment_keys, stream, stats);
+}
+
 int va_dense_row_stats(int dtype, const void* q, int64_t sqb, int64_t sqh, int64_t sqs,
                        const void* k, int64_t skb, int64_t skh, int64_t sks, int64_t B,
                        int64_t Hq, int64_t Hk, int64_t Sq, int64_t Sk, int64_t D, int causal,

@@ -35,7 +35,7 @@ constexpr int kSelMaxD = 256;
 // [seg*segk, (seg+1)*segk) only; segments are multiples of the group span, so
 // each starts a group, and a segment writes its keys from its own first slot
 // of the row and its count to counts[(bh*nc + jr)*nseg + seg].
-template <typename T, int kSelRows>
+template <typename T, int kSelRows, int kD>
 __global__ __launch_bounds__(256) void select_exact_kernel(
     const T* __restrict__ qs, int64_t sqb, int64_t sqh, int64_t sqn, const T* __restrict__ k,
     int64_t skb, int64_t skh, int64_t sks, int64_t B, int64_t Hq, int64_t Hk,
@@ -101,6 +101,9 @@ __global__ __launch_bounds__(256) void select_exact_kernel(
   constexpr int VEC = int(16 / sizeof(T));
   const bool vec_ok = (D % VEC == 0) && (reinterpret_cast<uintptr_t>(kh) % 16 == 0) &&
                       (sks % VEC == 0);
+  // kD: the head dim as a compile-time constant (64 or 128; 0: runtime), so
+  // that the scoring loop unrolls and its LDS reads are issued ahead of use.
+  const int64_t Dk = kD ? int64_t(kD) : D;
 
   for (int64_t kbase = kstart; kbase < kend; kbase += kSelChunk) {
     // ---- Phase A: canonical scores for R rows x 256 keys -----------------
@@ -112,7 +115,8 @@ __global__ __launch_bounds__(256) void select_exact_kernel(
       if (key < kend) {
         const T* kr = kh + key * sks;
         if (vec_ok) {
-          for (int64_t d0 = 0; d0 < D; d0 += VEC) {
+#pragma unroll
+          for (int64_t d0 = 0; d0 < Dk; d0 += VEC) {
             T v[VEC];
             *reinterpret_cast<uint4*>(v) = *reinterpret_cast<const uint4*>(kr + d0);
 #pragma unroll
@@ -217,11 +221,18 @@ static hipError_t launch_select_exact_t(
     constexpr int R = decltype(rows_tag)::value;
     const int64_t nrowsets = (lay.nc + R - 1) / R;
     const int64_t nblocks = nrowsets * nseg * B * Hq;
-    hipLaunchKernelGGL((select_exact_kernel<T, R>), dim3(unsigned(nblocks)), dim3(kSelChunk), 0,
-                       stream, static_cast<const T*>(qs), sqb, sqh, sqn,
-                       static_cast<const T*>(k), skb, skh, sks, B, Hq, Hk, Sk, D, qps, bk, group,
-                       causal, bsq, gap_scalar, gaps, lay, counts, indices, nrowsets,
-                       segk > 0 ? segk : Sk, int(nseg));
+    auto go = [&](auto kernel) {
+      hipLaunchKernelGGL(kernel, dim3(unsigned(nblocks)), dim3(kSelChunk), 0, stream,
+                         static_cast<const T*>(qs), sqb, sqh, sqn, static_cast<const T*>(k), skb,
+                         skh, sks, B, Hq, Hk, Sk, D, qps, bk, group, causal, bsq, gap_scalar,
+                         gaps, lay, counts, indices, nrowsets, segk > 0 ? segk : Sk, int(nseg));
+    };
+    if (D == 128)
+      go(select_exact_kernel<T, R, 128>);
+    else if (D == 64)
+      go(select_exact_kernel<T, R, 64>);
+    else
+      go(select_exact_kernel<T, R, 0>);
     return hipGetLastError();
   };
   // Work-groups wanted: 256 for whole rows (more rows per work-group share

@@ -289,10 +289,13 @@ def dense_row_stats(q, k, causal, softmax_scale=None, kernel=nat.VA_ATTN_AUTO, s
 
 
 def sparse_row_stats(q, k, J0, nc, counts, indices, causal, q_pooling_size, wo_init=None,
-                     dense_stride=0, softmax_scale=None, kernel=nat.VA_ATTN_AUTO, stats=None):
+                     dense_stride=0, softmax_scale=None, kernel=nat.VA_ATTN_AUTO, stats=None,
+                     segk=0):
     """Softmax statistics of the rows of q-blocks [J0, J0+nc) over their
     vector-sparse key sets (va_sparse_row_stats); other rows of `stats` are
-    left as they are.  Same (m, l) convention as dense_row_stats."""
+    left as they are.  Same (m, l) convention as dense_row_stats.  With
+    segk > 0, (counts, indices) are the segmented lists of select_segments
+    (va_sparse_row_stats_segments, MFMA kernel)."""
     q = q if q.stride(-1) == 1 else q.contiguous()
     k = k if k.stride(-1) == 1 else k.contiguous()
     B, Hq, Sq, D = q.shape
@@ -303,6 +306,14 @@ def sparse_row_stats(q, k, J0, nc, counts, indices, causal, q_pooling_size, wo_i
     if softmax_scale is None:
         softmax_scale = 1.0 / math.sqrt(D)
     with torch.cuda.device(q.device):
+        if segk:
+            rc = nat.lib().va_sparse_row_stats_segments(
+                nat.dtype_code(q), nat.ptr(q), q.stride(0), q.stride(1), q.stride(2), nat.ptr(k),
+                k.stride(0), k.stride(1), k.stride(2), B, Hq, Hk, Sq, Sk, D, q_pooling_size,
+                int(causal), int(wo_init), J0, nc, dense_stride, segk, nat.ptr(counts),
+                nat.ptr(indices), float(softmax_scale), nat.ptr(stats), _stream(q))
+            nat.check("va_sparse_row_stats_segments", rc)
+            return stats
         rc = nat.lib().va_sparse_row_stats(
             nat.dtype_code(q), nat.ptr(q), q.stride(0), q.stride(1), q.stride(2), nat.ptr(k),
             k.stride(0), k.stride(1), k.stride(2), B, Hq, Hk, Sq, Sk, D, q_pooling_size,

@@ -104,14 +104,29 @@ def seg_pr_perHead(q, k, block_size_q, block_size_k=16, group_size_k=16, thresho
     sparse = torch.zeros_like(dense)
     nqb = math.ceil(S / block_size_q)
     counts_all = torch.empty(B, H, nqb, dtype=torch.int32, device=q.device)
+    # fp32 queries select on the exact kernel; when the statistics run on the
+    # MFMA kernel (bf16-exact inputs) that selection is split into key
+    # segments (the lists are the same keys in the same order)
+    segk = 0
+    if (q.dtype == torch.float32 and qa.dtype != torch.float32 and D in (64, 128)
+            and block_size_q in (64, 128)):
+        segk = stages.segment_keys(Sk, block_size_k, group_size_k, exact=True)
     for c0 in range(0, S, chunk_size):
         rows = min(chunk_size, S - c0)
         J0, nc = c0 // block_size_q, math.ceil(rows / block_size_q)
         scaled, _ = stages.pool_scaled(q[:, :, c0:c0 + rows], block_size_q)
-        counts, indices = stages.select_rows(scaled, k, J0, 0.0, gaps, causal, block_size_q,
-                                             block_size_k, group_size_k, causal)
-        stages.sparse_row_stats(qa, ka, J0, nc, counts, indices, causal, block_size_q,
-                                wo_init=causal, stats=sparse)
+        if segk:
+            counts, indices = stages.select_segments(scaled, k, J0, 0.0, gaps, causal,
+                                                     block_size_q, block_size_k, group_size_k,
+                                                     causal, segk)
+            stages.sparse_row_stats(qa, ka, J0, nc, counts, indices, causal, block_size_q,
+                                    wo_init=causal, stats=sparse, segk=segk)
+            counts = counts.sum(-1, dtype=torch.int32)
+        else:
+            counts, indices = stages.select_rows(scaled, k, J0, 0.0, gaps, causal, block_size_q,
+                                                 block_size_k, group_size_k, causal)
+            stages.sparse_row_stats(qa, ka, J0, nc, counts, indices, causal, block_size_q,
+                                    wo_init=causal, stats=sparse)
         counts_all[:, :, J0:J0 + nc] = counts
 
     recall = recall_from_stats(dense, sparse)  # (B, H, S)
