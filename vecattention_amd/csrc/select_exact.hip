@@ -107,7 +107,51 @@ __global__ __launch_bounds__(256) void select_exact_kernel(
 
   for (int64_t kbase = kstart; kbase < kend; kbase += kSelChunk) {
     // ---- Phase A: canonical scores for R rows x 256 keys -----------------
-    {
+    bool scored = false;
+    if constexpr (kD > 0 && kSelRows >= 16) {
+      if (vec_ok) {
+        // Two keys per thread (kk and kk + 128) for half of the rows (threads
+        // [0, 128): rows [0, R/2), the others rows [R/2, R)): every fp64 query
+        // value read from LDS feeds two FMAs.  With a key per thread the
+        // scoring loop is bound by these broadcast LDS reads (one per FMA) at
+        // 16 rows (pairs: 20-40% faster); at 8 and 4 rows the second read of
+        // each K row costs more than the LDS reads it saves (15-65% slower).
+        constexpr int RH = kSelRows / 2;
+        const int half = tid / (kSelChunk / 2), kk = tid % (kSelChunk / 2);
+        const int64_t key0 = kbase + kk, key1 = key0 + kSelChunk / 2;
+        // keys past the range score a valid row (the first one of the range):
+        // their scores are written as 0 and never read
+        const T* kr0 = kh + (key0 < kend ? key0 : kstart) * sks;
+        const T* kr1 = kh + (key1 < kend ? key1 : kstart) * sks;
+        double a0[RH], a1[RH];
+#pragma unroll
+        for (int i = 0; i < RH; ++i) a0[i] = a1[i] = 0.0;
+#pragma unroll
+        for (int d0 = 0; d0 < kD; d0 += VEC) {
+          T v0[VEC], v1[VEC];
+          *reinterpret_cast<uint4*>(v0) = *reinterpret_cast<const uint4*>(kr0 + d0);
+          *reinterpret_cast<uint4*>(v1) = *reinterpret_cast<const uint4*>(kr1 + d0);
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) {
+            const double kd0 = double(to_f32(v0[e])), kd1 = double(to_f32(v1[e]));
+            const double* qrow = &qd[(d0 + e) * kSelRows + half * RH];
+#pragma unroll
+            for (int i = 0; i < RH; ++i) {
+              const double qv = qrow[i];
+              a0[i] = __builtin_fma(qv, kd0, a0[i]);
+              a1[i] = __builtin_fma(qv, kd1, a1[i]);
+            }
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < RH; ++i) {
+          sc[(half * RH + i) * kSelChunk + kk] = key0 < kend ? float(a0[i]) : 0.f;
+          sc[(half * RH + i) * kSelChunk + kk + kSelChunk / 2] = key1 < kend ? float(a1[i]) : 0.f;
+        }
+        scored = true;
+      }
+    }
+    if (!scored) {
       const int64_t key = kbase + tid;
       double acc[kSelRows];
 #pragma unroll
