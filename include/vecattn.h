@@ -124,8 +124,8 @@ int va_select(int dtype, const void* qs, int64_t sqb, int64_t sqh, int64_t sqn,
  * counts[((b*Hq + h)*nc + (J - J0))*nseg + s], nseg = ceil(Sk / segment_keys);
  * a row's list is the concatenation of its segments.  Runs on the VA_SEL_WAVE
  * kernel where its conditions hold, else on the 64-row MFMA kernel (VA_SEL_MFMA
- * conditions, one pass, segment_keys a multiple of 256), else (one pass only:
- * fp32 inputs, other head dims) on the exact kernel.  No counterpart in the
+ * conditions, one pass, segment_keys a multiple of 256), else (fp32 inputs,
+ * other head dims) on the exact kernel, in one or two passes.  No counterpart in the
  * reference (its single launch writes dense rows); the selected sets are the
  * reference rule's, as for va_select.
  * va_select_segment_keys returns the segment length va_prefill uses for
@@ -138,9 +138,10 @@ int va_select(int dtype, const void* qs, int64_t sqb, int64_t sqh, int64_t sqn,
 int64_t va_select_segment_keys(int64_t Sk, int64_t k_local_size, int64_t group_k_block);
 /* The segment length va_prefill uses for fp32 inputs that run on the fp32
  * matrix-core attention (VA_KERNELS_ATTN_F32 with VA_KERNELS_SELECT_EXACT):
- * the exact kernel's one-pass split, multiples of 256 keys and of the group
- * span, at least Sk/64 keys; 0 when the keys are not split (one group covers
- * the row), -1 on invalid sizes.  No counterpart in the reference. */
+ * the exact kernel's split, at least Sk/64 keys, multiples of 256 keys and of
+ * the group span (one pass), or of 256 keys when one group spans the row
+ * (maxima pass, then carry pass); 0 when the keys are not split, -1 on
+ * invalid sizes.  No counterpart in the reference. */
 int64_t va_select_exact_segment_keys(int64_t Sk, int64_t k_local_size, int64_t group_k_block);
 /* fp32 scratch floats va_select_segments needs: the key norms, plus two floats
  * per (row, segment) in the two-pass form.  -1 on invalid sizes. */

@@ -40,6 +40,8 @@ CSR_CASES = [
     # the exact kernel's one-pass split (segments of whole groups)
     ("exact-fp32-causal-seg256-chunked", 1, 4, 2, 2500, 64, torch.float32, True, 64, 16, 16,
      0.10, 256, 13),
+    ("exact-fp32-noncausal-G8192-2pass-seg512", 1, 2, 2, 2300, 64, torch.float32, False, 64, 16,
+     8192, 0.15, 512, None),
 ]
 
 

@@ -420,6 +420,15 @@ EXACT_SPLIT_CASES = [
     # segments that are not whole 256-key chunks
     ("bf16-d96-noncausal-bk16-G2-seg320", 1, 2, 2, 1900, 96, torch.bfloat16, False, 64, 16, 2,
      0.15, 320, None),
+    # one group spans the row: maxima pass, then carry pass
+    ("fp32-noncausal-G8192-2pass-seg512", 1, 2, 2, 2300, 64, torch.float32, False, 64, 16, 8192,
+     0.15, 512, None),
+    ("fp32-causal-Glong-2pass-seg256-chunked", 1, 4, 2, 2048, 64, torch.float32, True, 64, 16,
+     1024, 0.10, 256, 9),
+    ("fp32-noncausal-2pass-gap0-seg768-d128", 1, 2, 1, 2000, 128, torch.float32, False, 64, 16,
+     8192, None, 768, None),
+    ("bf16-d96-noncausal-G8192-2pass-seg256", 1, 2, 2, 1100, 96, torch.bfloat16, False, 64, 16,
+     8192, 0.15, 256, None),
 ]
 
 
@@ -703,6 +712,8 @@ E2E_CASES = [
     ("A-fp32-noncausal", 1, 4, 4, 4096, 64, torch.float32, False, 64, 16, 16, 4096, 0.35),
     # fp32 split selection under the causal rule, over chunks
     ("fp32-causal-gqa-chunked", 1, 4, 2, 2500, 64, torch.float32, True, 64, 16, 16, 1024, 0.5),
+    # fp32 with one group per row: the exact kernel's two-pass split
+    ("fp32-dit-like-2pass", 1, 2, 2, 3000, 64, torch.float32, False, 64, 16, 8192, 1024, 0.3),
     ("fp32-noncausal-qps128-d128", 2, 2, 1, 1500, 128, torch.float32, False, 128, 32, 4, 1024,
      0.4),
     # batches: every (b, h) work item, strides over the batch dimension

@@ -112,10 +112,10 @@ def test_select_csr_argument_errors_before_launch(L):
     assert _null_csr(L, segk=100) == nat.VA_ERR_ARG                 # not a multiple of 64
     assert _null_csr(L, segk=512) == nat.VA_ERR_ARG                 # no scratch
     assert b"scratch" in L.va_last_error()
-    # the exact kernel (fp32) splits in one pass only: a group that spans the
-    # row (carried maxima) needs the wave kernel
-    assert _null_csr(L, dtype=nat.VA_F32, G=8192, segk=512) == nat.VA_ERR_UNSUPPORTED
-    assert b"two-pass" in L.va_last_error()
+    # the exact kernel (fp32) also takes the two-pass split (a group spans the
+    # row), with its carry records in scratch
+    assert _null_csr(L, dtype=nat.VA_F32, G=8192, segk=512) == nat.VA_ERR_ARG
+    assert b"scratch" in L.va_last_error()
     assert _null_csr(L, dtype=nat.VA_F32, segk=320) == nat.VA_ERR_ARG  # not whole 256-key groups
 
 
@@ -306,15 +306,16 @@ def test_prefill_kernels_reports_the_slow_paths(L):
     f = _plan(L, dtype=nat.VA_F32)
     f32 = nat.VA_KERNELS_SELECT_EXACT | nat.VA_KERNELS_ATTN_F32
     assert f == f32 | nat.VA_KERNELS_SPLIT
-    # one group per row: no one-pass split on the exact kernel
-    assert _plan(L, dtype=nat.VA_F32, G=8192, Sk=32760, Hq=12, Hk=12) == f32
+    # one group per row: the exact kernel's two-pass split
+    assert _plan(L, dtype=nat.VA_F32, G=8192, Sk=32760, Hq=12, Hk=12) == f32 | nat.VA_KERNELS_SPLIT
     # segments of 256 keys or more, multiples of 256 and of the group span,
     # at most 64 of them
     assert L.va_select_exact_segment_keys(4096, 16, 16) == 256
     assert L.va_select_exact_segment_keys(32768, 16, 16) == 512
     assert L.va_select_exact_segment_keys(131072, 16, 1) == 2048
     assert L.va_select_exact_segment_keys(4096, 16, 3) == 768       # span 48: lcm 768
-    assert L.va_select_exact_segment_keys(4096, 16, 8192) == 0      # one group per row
+    assert L.va_select_exact_segment_keys(4096, 16, 8192) == 256    # one group per row: 2 passes
+    assert L.va_select_exact_segment_keys(32760, 16, 8192) == 512
     assert L.va_select_exact_segment_keys(200, 16, 16) == 0         # one group covers Sk
     assert L.va_select_exact_segment_keys(0, 16, 16) == -1
     assert _plan(L, dtype=nat.VA_F32, D=96) == nat.VA_KERNELS_SELECT_EXACT | nat.VA_KERNELS_ATTN_ROW

@@ -18,7 +18,8 @@ hipError_t launch_select_exact(int dtype, const void* qs, int64_t sqb, int64_t s
                                int64_t Hk, int64_t Sk, int64_t D, int64_t qps, int64_t bk,
                                int64_t group, int causal, int64_t bsq, float gap_scalar,
                                const float* gaps, const RowLayout& lay, int32_t* counts,
-                               int32_t* indices, int64_t segk, hipStream_t stream);
+                               int32_t* indices, int64_t segk, float* carry, int mode,
+                               hipStream_t stream);
 hipError_t launch_attn_simple(int dtype, const void* q, const int64_t* sq, const void* k,
                               const int64_t* sk, const void* v, const int64_t* sv, void* out,
                               const int64_t* so, int64_t B, int64_t Hq, int64_t Hk, int64_t Sq,
@@ -234,7 +235,7 @@ static int select_impl(int dtype, const void* qs, int64_t sqb, int64_t sqh, int6
   else
     e = va::launch_select_exact(dtype, qs, sqb, sqh, sqn, k, skb, skh, sks, B, Hq, Hk, Sk, D,
                                 qps, bk, group, causal, bsq, gap, gaps, lay, counts, indices,
-                                segk, stream);
+                                segk, static_cast<float*>(carry), mode, stream);
   return hip_check(e, "select launch");
 }
 
@@ -364,7 +365,7 @@ int64_t va_select_segments_scratch_floats(int64_t B, int64_t Hq, int64_t Hk, int
 // group covers the row (maxima pass, then carry pass), at most 64 segments.
 // The wave kernel takes every split; the 64-row MFMA kernel (tiles of 128 and
 // 256 keys) takes segments of whole 256-key chunks that start groups; the
-// exact kernel (other inputs, fp32 among them) takes every one-pass split.
+// exact kernel (other inputs, fp32 among them) takes every split.
 static int plan_segments(int dtype, const void* qs, int64_t sqb, int64_t sqh, int64_t sqn,
                          const void* k, int64_t skb, int64_t skh, int64_t sks, int64_t B,
                          int64_t Hq, int64_t Hk, int64_t Sk, int64_t D, int64_t qps, int64_t bk,
@@ -385,9 +386,6 @@ static int plan_segments(int dtype, const void* qs, int64_t sqb, int64_t sqh, in
              select_mfma_ok(dtype, qs, sqb, sqh, sqn, k, skb, skh, sks, D, bk))
               ? kSelMfma
               : kSelExact;
-  if (which == kSelExact && two_pass)
-    return fail(VA_ERR_UNSUPPORTED, "two-pass segmented selection (one group per row) needs "
-                                    "the wave selection kernel");
   // exact kernel: up to 16 rows per work-group, one work-group per (rows, segment)
   if (which == kSelExact && cdiv(nc, 16) * cdiv(Sk, segment_keys) * B * Hq > (int64_t(1) << 24))
     return fail(VA_ERR_UNSUPPORTED, "grid too large");
@@ -425,7 +423,7 @@ int va_select_segments(int dtype, const void* qs, int64_t sqb, int64_t sqh, int6
   if (two_pass) {
     rc = select_impl(dtype, qs, sqb, sqh, sqn, k, skb, skh, sks, B, Hq, Hk, Sk, D, qps, bk, group,
                      causal, wo_init, J0, nc, bsq, gap, gaps, dense_stride, counts, indices,
-                     kSelWave, scratch, segment_keys, st, carry, va::kPassMax);
+                     which, scratch, segment_keys, st, carry, va::kPassMax);
     if (rc) return rc;
   }
   rc = select_impl(dtype, qs, sqb, sqh, sqn, k, skb, skh, sks, B, Hq, Hk, Sk, D, qps, bk, group,
@@ -478,7 +476,7 @@ int va_select_csr(int dtype, const void* qs, int64_t sqb, int64_t sqh, int64_t s
   const bool write = indices != nullptr;
   if (two_pass) {  // the maxima pass stores neither counts nor keys
     rc = select_impl(dtype, qs, sqb, sqh, sqn, k, skb, skh, sks, B, Hq, Hk, Sk, D, qps, bk, group,
-                     causal, wo_init, J0, nc, bsq, gap, gaps, 0, nullptr, nullptr, kSelWave,
+                     causal, wo_init, J0, nc, bsq, gap, gaps, 0, nullptr, nullptr, which,
                      scratch, segment_keys, st, carry, va::kPassMax);
     if (rc) return rc;
   }
@@ -1080,8 +1078,10 @@ int va_prefill(int dtype, const void* q, int64_t sqb, int64_t sqh, int64_t sqs, 
       // the 64-row MFMA kernel splits at whole 256-key chunks (no carry pass)
       segk = va::select_mfma_segment_keys(Sk, bk, g);
     } else if (which == kSelExact && attn_f32_ok(dtype, q, sq, k, sk, v, sv, out, so, D, qps)) {
-      // fp32: the exact kernel's one-pass split, read by the fp32 matrix-core attention
+      // fp32: the exact kernel's split (two passes when a group spans the
+      // row), read by the fp32 matrix-core attention
       segk = va::select_exact_segment_keys(Sk, bk, g);
+      two_pass = segk > 0 && segments_two_pass(Sk, bk, group, segk);
       if (segk > 0 && cdiv(cdiv(chunk_size, qps), 16) * cdiv(Sk, segk) * B * Hq > (int64_t(1) << 24))
         segk = 0;  // grid of (16-row sets, segment) work-groups too large
     }

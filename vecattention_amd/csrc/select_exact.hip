@@ -35,6 +35,13 @@ constexpr int kSelMaxD = 256;
 // [seg*segk, (seg+1)*segk) only; segments are multiples of the group span, so
 // each starts a group, and a segment writes its keys from its own first slot
 // of the row and its count to counts[(bh*nc + jr)*nseg + seg].
+// Two passes when one group spans the row (segments then do not start
+// groups): the maxima pass (mode kPassMax) stores each (row, segment)'s
+// exact running maximum at the segment's end, carry[(bh*nc + jr)*nseg + seg],
+// and selects nothing; the carry pass (kPassCarry) starts segment s from the
+// maximum of the carried values of segments 0 .. s-1 (with one group per row
+// the running maximum before the segment is exactly that), then selects as
+// the one-pass form does.
 template <typename T, int kSelRows, int kD>
 __global__ __launch_bounds__(256) void select_exact_kernel(
     const T* __restrict__ qs, int64_t sqb, int64_t sqh, int64_t sqn, const T* __restrict__ k,
@@ -42,7 +49,7 @@ __global__ __launch_bounds__(256) void select_exact_kernel(
     int64_t Sk, int64_t D, int64_t qps, int64_t bk, int64_t group, int causal,
     int64_t bsq, float gap_scalar, const float* __restrict__ gaps, RowLayout lay,
     int32_t* __restrict__ counts, int32_t* __restrict__ indices, int64_t nrowsets,
-    int64_t segk, int nseg) {
+    int64_t segk, int nseg, float* __restrict__ carry, int mode) {
   __shared__ double qd[kSelMaxD * kSelRows];          // [d][row]
   __shared__ float sc[kSelRows * kSelChunk];          // [row][key]
   __shared__ float mt[kSelRows * (kSelChunk / 16)];   // [row][tile] running max
@@ -85,7 +92,11 @@ __global__ __launch_bounds__(256) void select_exact_kernel(
     qd[d * kSelRows + i] = v;
   }
   if (tid < kSelRows) {
-    m_run[tid] = -__builtin_inff();
+    float m0 = -__builtin_inff();
+    if (mode == kPassCarry && tid < rows_here)
+      for (int s2 = 0; s2 < seg; ++s2)
+        m0 = __builtin_fmaxf(m0, carry[(bh * nc + jr0 + tid) * nseg + s2]);
+    m_run[tid] = m0;
     cnt[tid] = 0;
     // The reference's causal tile test r > trunc((k_off - off0) / qps), with r
     // the row inside its BLOCK_SIZE_Q program and off0 = (J - r) * qps, is
@@ -216,7 +227,7 @@ __global__ __launch_bounds__(256) void select_exact_kernel(
     __syncthreads();
 
     // ---- Phase B3: decisions and ordered compaction, one wave per row ------
-    {
+    if (mode != kPassMax) {
       const int wave = tid / 64, lane = tid % 64;
       for (int i = wave; i < rows_here; i += int(blockDim.x / 64)) {
         const int64_t jr = jr0 + i;
@@ -245,6 +256,10 @@ __global__ __launch_bounds__(256) void select_exact_kernel(
     __syncthreads();
   }
 
+  if (mode == kPassMax) {
+    if (tid < rows_here) carry[(bh * nc + jr0 + tid) * nseg + seg] = m_run[tid];
+    return;
+  }
   if (tid < rows_here && counts) {
     int64_t start, cap;
     lay.segment_slots(bh, jr0 + tid, seg, nseg, seg_lo, start, cap);
@@ -259,7 +274,7 @@ static hipError_t launch_select_exact_t(
     int64_t sks, int64_t B, int64_t Hq, int64_t Hk, int64_t Sk, int64_t D,
     int64_t qps, int64_t bk, int64_t group, int causal, int64_t bsq,
     float gap_scalar, const float* gaps, const RowLayout& lay, int32_t* counts,
-    int32_t* indices, int64_t segk, hipStream_t stream) {
+    int32_t* indices, int64_t segk, float* carry, int mode, hipStream_t stream) {
   const int64_t nseg = segk > 0 ? (Sk + segk - 1) / segk : 1;
   auto launch = [&](auto rows_tag) {
     constexpr int R = decltype(rows_tag)::value;
@@ -269,7 +284,8 @@ static hipError_t launch_select_exact_t(
       hipLaunchKernelGGL(kernel, dim3(unsigned(nblocks)), dim3(kSelChunk), 0, stream,
                          static_cast<const T*>(qs), sqb, sqh, sqn, static_cast<const T*>(k), skb,
                          skh, sks, B, Hq, Hk, Sk, D, qps, bk, group, causal, bsq, gap_scalar,
-                         gaps, lay, counts, indices, nrowsets, segk > 0 ? segk : Sk, int(nseg));
+                         gaps, lay, counts, indices, nrowsets, segk > 0 ? segk : Sk, int(nseg),
+                         carry, mode);
     };
     if (D == 128)
       go(select_exact_kernel<T, R, 128>);
@@ -292,24 +308,24 @@ static hipError_t launch_select_exact_t(
   return launch(std::integral_constant<int, 1>{});
 }
 
-// Key segments of the exact kernel's split (one pass): multiples of 256 keys
-// and of the group span, so that each segment starts a group, at least
-// Sk / 64 keys (at most 64 segments) and otherwise as short as one 256-key
-// chunk: a work-group then scores its rows' keys in one chunk instead of
-// walking the row, and the row sets take 16 rows each sooner (more rows per
-// K load).  0 when one group covers the row (no one-pass split) or nothing
-// is split.
+// Key segments of the exact kernel's split: at least Sk / 64 keys (at most
+// 64 segments) and otherwise as short as one 256-key chunk, so that a
+// work-group scores its rows' keys in one or a few chunks instead of walking
+// the row, and row sets take 16 rows each sooner (more rows per K load).
+// Multiples of 256 keys and of the group span (each segment starts a group:
+// one pass), or, when one group spans the row, any whole chunks (maxima pass,
+// then carry pass).  0 when nothing is split.
 int64_t select_exact_segment_keys(int64_t Sk, int64_t bk, int64_t group) {
   constexpr int64_t kMaxSeg = 64;
   const int64_t gs = bk * group;
-  if (gs <= 0 || gs >= Sk) return 0;
-  int64_t a = kSelChunk, b = gs;  // lcm(kSelChunk, gs)
+  if (gs <= 0) return 0;
+  int64_t a = kSelChunk, b = gs < Sk ? gs : kSelChunk;  // lcm(kSelChunk, gs) for short groups
   while (b) {
     const int64_t t = a % b;
     a = b;
     b = t;
   }
-  const int64_t unit = kSelChunk / a * gs;
+  const int64_t unit = gs < Sk ? kSelChunk / a * gs : kSelChunk;
   const int64_t want = (Sk + kMaxSeg - 1) / kMaxSeg;
   const int64_t segk = (want + unit - 1) / unit * unit;
   return segk < Sk ? segk : 0;
@@ -321,20 +337,20 @@ hipError_t launch_select_exact(int dtype, const void* qs, int64_t sqb, int64_t s
                                int64_t qps, int64_t bk, int64_t group, int causal,
                                int64_t bsq, float gap_scalar, const float* gaps,
                                const RowLayout& lay, int32_t* counts, int32_t* indices,
-                               int64_t segk, hipStream_t stream) {
+                               int64_t segk, float* carry, int mode, hipStream_t stream) {
   switch (dtype) {
     case kF32:
       return launch_select_exact_t<float>(qs, sqb, sqh, sqn, k, skb, skh, sks, B, Hq, Hk, Sk, D, qps, bk,
                                           group, causal, bsq, gap_scalar, gaps, lay, counts,
-                                          indices, segk, stream);
+                                          indices, segk, carry, mode, stream);
     case kBF16:
       return launch_select_exact_t<bf16_t>(qs, sqb, sqh, sqn, k, skb, skh, sks, B, Hq, Hk, Sk, D, qps,
                                            bk, group, causal, bsq, gap_scalar, gaps, lay, counts,
-                                           indices, segk, stream);
+                                           indices, segk, carry, mode, stream);
     case kF16:
       return launch_select_exact_t<f16_t>(qs, sqb, sqh, sqn, k, skb, skh, sks, B, Hq, Hk, Sk, D, qps, bk,
                                           group, causal, bsq, gap_scalar, gaps, lay, counts,
-                                          indices, segk, stream);
+                                          indices, segk, carry, mode, stream);
   }
   return hipErrorInvalidValue;
 }
