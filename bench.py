@@ -701,10 +701,11 @@ def measure_prefill(args, wl, dev, with_cpu):
             # Short passes (A, B, D: a few ms or less) are held: launches
             # that reach an idle GPU there add tens of microseconds of gaps
             # and dispatch latency inside the stages (B's attention measured
-            # 6-11% slower unheld than its kernel trace).  Long passes (C, E)
-            # are not: the GPU idles through the hold and starts the pass at
-            # a lower clock (C's stages measured 5% slower held).
-            if gpu_ms < 5.0:
+            # 6-11% slower unheld than its kernel trace), and so are passes
+            # the host takes long to enqueue (a tracer's launch overhead).
+            # Long passes (C, E) are not: the GPU idles through the hold and
+            # starts the pass at a lower clock (C's stages 5% slower held).
+            if gpu_ms < 5.0 or host_ms > 0.5 * gpu_ms:
                 hold_ms = 2.0 * host_ms + 1.0
             print(f"[bench] stage pass: host enqueue {host_ms:.3f} ms, GPU {gpu_ms:.3f} ms; "
                   f"stream hold {hold_ms:.3f} ms", file=sys.stderr, flush=True)
