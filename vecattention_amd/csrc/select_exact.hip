@@ -19,7 +19,8 @@
 // Scores are canonical: a sequential fp64 sum over d of exact products
 // (bf16*bf16, fp16*fp16 and fp32*fp32 products are exact in fp64), rounded
 // once to fp32.  This makes every decision bit-identical to the CPU oracle.
-// The kernel is fp64-FMA bound (R*D FMAs per key per work-group).
+// Its scoring loop (R*D fp64 FMAs per key per work-group) is bound by the LDS
+// broadcast reads of the fp64 query values that feed those FMAs.
 #include "common.h"
 
 namespace va {
@@ -32,9 +33,9 @@ constexpr int kSelMaxD = 256;
 // segments), since each work-group walks every key of its rows; small grids
 // take one row per work-group).
 // Key segments (nseg > 1): work-group (row set, segment) walks the keys
-// [seg*segk, (seg+1)*segk) only; segments are multiples of the group span, so
-// each starts a group, and a segment writes its keys from its own first slot
-// of the row and its count to counts[(bh*nc + jr)*nseg + seg].
+// [seg*segk, (seg+1)*segk) only and writes its keys from its own first slot
+// of the row and its count to counts[(bh*nc + jr)*nseg + seg].  One pass when
+// segments are multiples of the group span (each starts a group).
 // Two passes when one group spans the row (segments then do not start
 // groups): the maxima pass (mode kPassMax) stores each (row, segment)'s
 // exact running maximum at the segment's end, carry[(bh*nc + jr)*nseg + seg],
