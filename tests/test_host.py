@@ -66,3 +66,16 @@ def test_workload_table_matches_plan():
     assert WORKLOADS["C"].S == 131072 and WORKLOADS["C"].keep == 0.05
     assert WORKLOADS["D"].S == 21 * 1560 and not WORKLOADS["D"].causal
     assert WORKLOADS["E"].S == 33 * 3600 + 256
+
+
+def test_bench_refuses_more_than_one_gpu():
+    # bench.py measures one GPU: asked for more it exits with status 2 and says
+    # so, before touching a device (runs on the CPU-only host too).
+    import os
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([sys.executable, os.path.join(root, "bench.py"), "--gpus", "2"],
+                       capture_output=True, text=True, timeout=300, cwd=root)
+    assert r.returncode == 2
+    assert "measures one GPU" in r.stderr and r.stdout == ""
