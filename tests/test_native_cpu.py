@@ -374,3 +374,23 @@ def test_m0_is_only_set_by_the_lds_copies(src, tmp_path):
                 outside.append(line.strip())
     assert sets > 0
     assert outside == []
+
+
+def _stats_seg(L, **over):
+    args = dict(dtype=nat.VA_BF16, q=256, sqb=0, sqh=0, sqs=128, k=256, skb=0, skh=0, sks=128,
+                B=1, Hq=4, Hk=2, Sq=1024, Sk=1024, D=128, qps=64, causal=1, wo_init=1, J0=0,
+                nc=16, dense_stride=0, segk=256, counts=256, indices=256, scale=0.088,
+                stats=256, stream=None)
+    args.update(over)
+    return L.va_sparse_row_stats_segments(*args.values())
+
+
+def test_sparse_row_stats_segments_argument_errors_before_launch(L):
+    assert _stats_seg(L, stats=None) == nat.VA_ERR_ARG
+    assert _stats_seg(L, counts=None) == nat.VA_ERR_ARG
+    assert _stats_seg(L, segk=100) == nat.VA_ERR_ARG                 # not a multiple of 64
+    assert _stats_seg(L, segk=0) == nat.VA_ERR_ARG
+    assert _stats_seg(L, Sk=8192, Sq=8192, nc=128, segk=64) == nat.VA_ERR_ARG  # 128 segments
+    # segmented lists run on the MFMA kernel only: not fp32, not D = 96
+    assert _stats_seg(L, dtype=nat.VA_F32) == nat.VA_ERR_UNSUPPORTED
+    assert _stats_seg(L, D=96, sqs=96, sks=96) == nat.VA_ERR_UNSUPPORTED
